@@ -1,0 +1,306 @@
+/*
+ * lsamp.h — C ABI of the MI355X (gfx950) logits-to-token stage.
+ *
+ * One call turns a batch of [rows, vocab] logits that already sit in HBM into
+ * one token id per row: penalties, grammar bitmask, temperature,
+ * top-k / top-p / min-p and the draw run as hand-written HIP kernels that read
+ * every logit once.  The ABI replaces the MLX graph that the reference builds
+ * for this stage:
+ *
+ *   - mlx-lm order (single stream):  PenaltyProcessor.process
+ *       (Libraries/MLXLMCommon/Evaluate.swift:687-693) followed by
+ *       ArgMaxSampler / TopPSampler / CategoricalSampler .sample
+ *       (Evaluate.swift:394-396, 432-491, 506-510);
+ *   - CBv2 order (batched):  LogitsPipelineV2.process
+ *       (Libraries/MLXLMCommon/ContinuousBatchingV2/LogitsPipelineV2.swift:292-352,
+ *       applyTopKTopPMinP :421-453) followed by SamplerV2.sample
+ *       (ContinuousBatchingV2/SamplerV2.swift:85-107);
+ *   - the grammar mask apply of xgrammar's ApplyTokenBitmaskInplaceCPU
+ *       (Libraries/MLXCXGrammar/xgrammar/cpp/grammar_matcher.cc:89-235) and of
+ *       GuidedGenerationLoop.bitmaskToMLXArray
+ *       (Libraries/MLXGuidedGeneration/GuidedGenerationLoop.swift:595-610);
+ *   - MTP verification: CBv2DefaultSampler.verifyWindow
+ *       (ContinuousBatchingV2/DefaultSamplerV2.swift:382-503) and textbook
+ *       speculative sampling (accept min(1, p_t/p_d), residual max(0, p_t-p_d)).
+ *
+ * Conventions follow the reference's own C ABI (Libraries/MLXCXGrammar/include/
+ * xgrammar_c.h:28-69): opaque handles, caller-owned buffers, int32 status
+ * codes (0 = OK, negative = error) and a thread-local last-error string.
+ * Every pointer in an args struct is a DEVICE pointer unless stated
+ * otherwise; the call enqueues work on `stream` (a hipStream_t, NULL = the
+ * default stream) and never synchronizes or allocates.
+ *
+ * Draw rule.  The reference draws with MLX's Gumbel / exponential race
+ * (Evaluate.swift:456,508; SamplerV2.swift:101-106), which consumes V random
+ * numbers per row.  This library draws by inverse CDF from ONE uniform per row,
+ * in token-id order, with integer (fixed-point) weights so that the CPU
+ * restatement reproduces the chosen token bit for bit:
+ *     d_i = fl(fl(y_i - y_max) * scale)   (scale = 1 in CBv2, fl(1/T) in mlx-lm)
+ *     w_i = (uint64) (dexp(d_i) * 2^40)   for kept tokens, 0 otherwise
+ *     W = sum w_i;  U = (uint32)(u * 2^32);  target = (U * W) >> 32
+ *     token = smallest id i with  w_0 + ... + w_i > target.
+ * dexp is a fixed fp32 Cody-Waite + Taylor-7 exponential evaluated with fma,
+ * identical on host and device.
+ */
+#ifndef LSAMP_H
+#define LSAMP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LSAMP_ABI_VERSION 1
+
+/* ---- status codes (xgrammar_c.h:55-61 style) ---------------------------- */
+typedef int32_t lsamp_status;
+#define LSAMP_OK 0
+#define LSAMP_ERR_INVALID_ARGUMENT (-1) /* null pointer, bad enum, bad size   */
+#define LSAMP_ERR_SHAPE (-2)            /* rows/vocab/strides out of range     */
+#define LSAMP_ERR_DTYPE (-3)            /* unsupported logits dtype            */
+#define LSAMP_ERR_CAPACITY (-4)         /* larger than the context was made for */
+#define LSAMP_ERR_DEVICE (-5)           /* a HIP runtime call failed           */
+
+/* ---- enums ---------------------------------------------------------------- */
+typedef enum lsamp_dtype {
+  LSAMP_DTYPE_F32 = 0,
+  LSAMP_DTYPE_BF16 = 1,
+  LSAMP_DTYPE_F16 = 2
+} lsamp_dtype;
+
+/* Which of the reference's two pipelines a call reproduces. */
+typedef enum lsamp_semantics {
+  /* Evaluate.swift:328-746: penalties in the logits dtype, filters top-p ->
+   * min-p -> top-k on un-tempered log-probs, draw from logprobs * (1/T). */
+  LSAMP_SEM_MLXLM = 0,
+  /* LogitsPipelineV2.swift:292-453: fp32 cast, bias, repetition,
+   * frequency/presence, x / T, grammar mask, one joint top-k/top-p/min-p. */
+  LSAMP_SEM_CBV2 = 1
+} lsamp_semantics;
+
+/* Per-row sampler after parameter resolution. */
+typedef enum lsamp_kind {
+  LSAMP_KIND_ARGMAX = 0,      /* ArgMaxSampler; CBv2 greedy row (T < 1e-5)  */
+  LSAMP_KIND_FILTERED = 1,    /* TopPSampler; CBv2 sampled row              */
+  LSAMP_KIND_CATEGORICAL = 2  /* CategoricalSampler (mlx-lm, no filters)    */
+} lsamp_kind;
+
+/* Bitmask words past `mask_bits`:
+ * KEEP   = ApplyTokenBitmaskInplaceCPU leaves ids >= vocab_size untouched
+ *          (grammar_matcher.cc:108-121);
+ * FORBID = bitmaskToMLXArray sets ids >= maskBitCount to -inf
+ *          (GuidedGenerationLoop.swift:600-601). */
+typedef enum lsamp_mask_tail {
+  LSAMP_MASK_TAIL_KEEP = 0,
+  LSAMP_MASK_TAIL_FORBID = 1
+} lsamp_mask_tail;
+
+/* Penalty entry flags. */
+#define LSAMP_PEN_REPETITION 1u /* token is in the repetition window        */
+#define LSAMP_PEN_PRESENCE 2u   /* mlx-lm only: token is in the presence window */
+
+/* Row flags written to `row_flags`. */
+#define LSAMP_ROW_NONFINITE 1u /* a raw logit is NaN or +-inf (CBv2NonFiniteLogits.swift:30-34) */
+#define LSAMP_ROW_EMPTY 2u     /* no token survived masking; token = -1       */
+#define LSAMP_ROW_OVERFLOW 4u  /* the cut bucket held more candidates than the
+                                  context's candidate capacity; token = -1   */
+
+/* ---- per-row inputs ------------------------------------------------------- */
+
+/* Resolved sampling parameters of one row (32 bytes).  Build them with
+ * lsamp_resolve_generate_parameters (mlx-lm) or lsamp_resolve_cbv2_params
+ * (CBv2); both reproduce the reference's own resolution rules. */
+typedef struct lsamp_row_params {
+  int32_t kind;             /* lsamp_kind                                        */
+  float temperature;        /* > 0 for FILTERED / CATEGORICAL rows               */
+  int32_t top_k;            /* <= 0 or >= vocab: off                             */
+  float top_p;              /* >= 1: off; CBv2 keeps the top token at 0          */
+  float min_p;              /* <= 0: off                                         */
+  float repetition_penalty; /* applied to entries flagged REPETITION; 1 = off   */
+  float presence_penalty;   /* 0 = off                                           */
+  float frequency_penalty;  /* 0 = off                                           */
+} lsamp_row_params;
+
+/* One sparse penalty / bias entry (16 bytes).  A row's entries are the
+ * distinct token ids of its history (CSR rows `row_ptr[r] .. row_ptr[r+1]`);
+ * a token id appears at most once per row and lies in [0, vocab).  This
+ * replaces the dense [B, vocab] float32 count tensors that the reference keeps
+ * (LogitsPipelineV2.swift:127-129) and the per-step scatter-add histogram of
+ * FrequencyPenaltyContext (Evaluate.swift:649-658). */
+typedef struct lsamp_penalty_entry {
+  int32_t token;  /* vocabulary id                                            */
+  int32_t count;  /* CBv2: occurrences in the output tokens (frequency and
+                     presence, LogitsPipelineV2.swift:327-330); mlx-lm:
+                     occurrences in the frequency window                      */
+  uint32_t flags; /* LSAMP_PEN_*                                              */
+  float bias;     /* CBv2 additive logit bias (LogitsPipelineV2.swift:317-319)  */
+} lsamp_penalty_entry;
+
+/* Optional per-row statistics (parity / logprobs / MTP).  48 bytes. */
+typedef struct lsamp_row_stats {
+  float max_value;       /* y_max: largest filter-space logit                    */
+  float log_normalizer;  /* log sum exp(y - y_max) over unmasked tokens          */
+  int32_t kept;          /* number of tokens that survive the filters            */
+  int32_t token;         /* the drawn token (same as tokens[r])                  */
+  uint64_t kept_weight;  /* W = sum of fixed-point weights of kept tokens        */
+  uint64_t probe_weight; /* w of probe_tokens[r] (0 if not kept / no probe)      */
+  float cut_value;       /* smallest kept filter-space logit                     */
+  float kept_mass;       /* sum exp(y - y_max) over kept tokens                  */
+  float kept_entropy;    /* Shannon entropy (nats) of the kept, renormalized row */
+  float probe_prob;      /* kept_weight-normalized probability of the probe      */
+} lsamp_row_stats;
+
+/* ---- the sampling step ---------------------------------------------------- */
+typedef struct lsamp_sample_args {
+  int32_t semantics;  /* lsamp_semantics                                        */
+  int32_t rows;       /* B                                                      */
+  int32_t vocab;      /* V (logit dimension)                                    */
+  int32_t dtype;      /* lsamp_dtype of `logits`                                */
+  int64_t row_stride; /* elements between consecutive rows (>= vocab)           */
+  const void* logits; /* [rows, row_stride]                                     */
+  const lsamp_row_params* params; /* [rows]                                     */
+
+  const int32_t* penalty_row_ptr;             /* [rows + 1] or NULL              */
+  const lsamp_penalty_entry* penalty_entries; /* [penalty_row_ptr[rows]]         */
+
+  const uint32_t* bitmask; /* [rows, mask_words] packed LSB-first, or NULL      */
+  int32_t mask_words;      /* words per row (>= ceil(mask_bits / 32))           */
+  int32_t mask_bits;       /* valid bits per row (tokenizer vocab size)         */
+  int32_t mask_tail;       /* lsamp_mask_tail                                   */
+
+  const float* uniforms;       /* [rows] in [0, 1), or NULL to use philox_keys */
+  const uint64_t* philox_keys; /* [rows] Philox4x32-10 keys (lsamp_rng_key)     */
+
+  const int32_t* probe_tokens; /* [rows] or NULL: report their kept weight      */
+
+  int32_t* tokens;        /* [rows] out                                         */
+  uint32_t* row_flags;    /* [rows] out or NULL                                 */
+  float* processed;       /* [rows, vocab] out or NULL: filter-space logits
+                             after penalties, temperature (CBv2) and mask,
+                             before top-k/top-p/min-p (parity mode)            */
+  uint8_t* keep;          /* [rows, vocab] out or NULL: 1 where the token
+                             survives the filters (parity mode)               */
+  lsamp_row_stats* stats; /* [rows] out or NULL                                 */
+} lsamp_sample_args;
+
+/* ---- MTP verification ----------------------------------------------------- */
+typedef enum lsamp_verify_mode {
+  /* Textbook speculative sampling (Leviathan et al. 2023; Chen et al. 2023):
+   * accept draft j iff u[j] < min(1, p_t(x_j) / p_d(x_j)); on the first
+   * rejection draw from normalize(max(0, p_t - p_d)) with u[W-1]; if every
+   * draft is accepted draw the bonus token from the last target position.  */
+  LSAMP_VERIFY_RESIDUAL = 0,
+  /* Reference exact mode (DefaultSamplerV2.swift:378-380): the target token at
+   * every position is drawn with u[j]; accept iff it equals the draft.      */
+  LSAMP_VERIFY_EXACT = 1,
+  /* Reference typical mode (DefaultSamplerV2.swift:485-502): same draws;
+   * accept iff p_t(draft) > min(1, delta * exp(-H)); greedy rows exact.      */
+  LSAMP_VERIFY_TYPICAL = 2
+} lsamp_verify_mode;
+
+typedef struct lsamp_verify_args {
+  int32_t mode;      /* lsamp_verify_mode                                      */
+  int32_t sequences; /* S                                                      */
+  int32_t window;    /* W = drafts + 1                                         */
+  int32_t vocab;     /* V                                                      */
+  int32_t dtype;     /* lsamp_dtype of both logit tensors                      */
+  const void* target_logits;  /* [S, W, V] contiguous                          */
+  const void* draft_logits;   /* [S, W-1, V] contiguous (RESIDUAL mode only)   */
+  const int32_t* draft_tokens;/* [S, W-1]                                      */
+  const lsamp_row_params* params; /* [S] CBv2-resolved, one per sequence       */
+  const float* uniforms;      /* [S, W]                                        */
+  float typical_delta;        /* TYPICAL mode, > 0                             */
+  int32_t* accepted;          /* [S] out: number of accepted drafts            */
+  int32_t* tokens;            /* [S, W] out: RESIDUAL mode emits accepted drafts
+                                 then the correction / bonus token, -1 after;
+                                 EXACT / TYPICAL write the target draw at every
+                                 position                                      */
+  uint8_t* accept_mask;       /* [S, W-1] out or NULL: per-position decision   */
+} lsamp_verify_args;
+
+/* ---- context ------------------------------------------------------------- */
+typedef struct lsamp_context lsamp_context;
+
+/* Allocates the device workspace for up to `max_rows` rows of up to
+ * `max_vocab` logits on `device` (and for MTP verification of up to
+ * max_rows target+draft rows).  The step functions allocate nothing. */
+lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_vocab,
+                                  lsamp_context** out);
+void lsamp_context_destroy(lsamp_context* ctx);
+
+/* Enqueue one sampling step on `stream`. */
+lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* args, void* stream);
+
+/* Enqueue one MTP verification on `stream`. */
+lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* args, void* stream);
+
+/* ---- host-side parameter resolution (no device work) ---------------------- */
+
+/* GenerateParameters subset that drives the mlx-lm sampler/processor factory
+ * (Evaluate.swift:127-289; defaults T=0.6, top-p 1, top-k 0, min-p 0,
+ * context sizes 20).  `has_*` = 0 reproduces a nil optional. */
+typedef struct lsamp_generate_parameters {
+  float temperature;
+  float top_p;
+  int32_t top_k;
+  float min_p;
+  int32_t has_repetition_penalty;
+  float repetition_penalty;
+  int32_t repetition_context_size;
+  int32_t has_presence_penalty;
+  float presence_penalty;
+  int32_t presence_context_size;
+  int32_t has_frequency_penalty;
+  float frequency_penalty;
+  int32_t frequency_context_size;
+} lsamp_generate_parameters;
+
+/* GenerateParameters.sampler() / .processor() (Evaluate.swift:328-387).
+ * Writes the resolved row, and in `*contexts` a bit set of the penalty
+ * contexts the reference would build (1 repetition, 2 presence, 4 frequency;
+ * 0 = processor() returns nil). */
+lsamp_status lsamp_resolve_generate_parameters(const lsamp_generate_parameters* gp,
+                                               lsamp_row_params* out, int32_t* contexts);
+
+/* CBv2SamplingParams subset (CBv2Contracts.swift:37-75; defaults T=1,
+ * repetition window 64). */
+typedef struct lsamp_cbv2_params {
+  float temperature;
+  float top_p;
+  int32_t top_k;
+  float min_p;
+  float repetition_penalty;
+  int32_t repetition_context_size;
+  float frequency_penalty;
+  float presence_penalty;
+} lsamp_cbv2_params;
+
+/* LogitsPipelineV2.setRows resolution (LogitsPipelineV2.swift:188-227):
+ * greedy iff T < 1e-5; top-k off unless 0 < k < vocab; top-p off (2.0) unless
+ * 0 < p < 1, p <= 0 keeps the top token; min-p clamped to 1; repetition only
+ * when p != 1 and the window is positive. */
+lsamp_status lsamp_resolve_cbv2_params(const lsamp_cbv2_params* sp, int32_t vocab,
+                                       lsamp_row_params* out);
+
+/* SamplerV2.mix (SamplerV2.swift:183-191): SplitMix64 of (seed, id, step). */
+uint64_t lsamp_rng_key(uint64_t seed, uint64_t request_id, uint64_t step);
+
+/* The uniform the kernels draw for `key` when `uniforms` is NULL:
+ * Philox4x32-10 (Salmon et al., SC'11) of counter {purpose, 0, 0, 0} and key
+ * {lo32(key), hi32(key)}; u = (x0 >> 8) * 2^-24.  purpose 0 = token draw. */
+float lsamp_rng_uniform(uint64_t key, uint32_t purpose);
+
+/* ---- diagnostics ----------------------------------------------------------- */
+const char* lsamp_last_error(void);
+const char* lsamp_version(void);
+/* sizeof of an ABI struct by name ("lsamp_row_params", ...), -1 if unknown;
+ * lets bindings in other languages verify their layouts. */
+int64_t lsamp_abi_sizeof(const char* type_name);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LSAMP_H */

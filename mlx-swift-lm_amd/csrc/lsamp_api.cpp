@@ -1,0 +1,378 @@
+// lsamp_api.cpp — the C ABI of include/lsamp.h: context (device workspace),
+// argument validation, launch planning, host-side parameter resolution.
+//
+// Conventions follow Libraries/MLXCXGrammar/include/xgrammar_c.h:28-69:
+// int32 status codes and a thread-local last-error message; a failed call
+// leaves every output untouched.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "lsamp_internal.h"
+
+using namespace lsamp;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+lsamp_status fail(lsamp_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+lsamp_status ok() {
+  g_last_error.clear();
+  return LSAMP_OK;
+}
+
+// Restores the caller's current device on scope exit.
+struct DeviceGuard {
+  int prev = -1;
+  bool changed = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
+      changed = hipSetDevice(dev) == hipSuccess;
+    }
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+constexpr int32_t kMaxVocab = kMaxSlices * kMaxSliceLen;  // 524288
+
+}  // namespace
+
+struct lsamp_context {
+  int32_t device;
+  int32_t cus;
+  Workspace ws;
+  void* block;  // single device allocation backing the workspace
+  size_t bytes;
+};
+
+namespace {
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Number of slices per row: enough work-groups to cover every CU twice,
+// slices of whole 1024-token chunks, at most kMaxSliceLen tokens each.
+void plan_slices(int32_t rows, int32_t vocab, int32_t cus, int32_t* slices, int32_t* slice_len,
+                 int32_t* nchunks) {
+  const int32_t nch = (vocab + kChunk - 1) / kChunk;
+  const int32_t g_min = (vocab + kMaxSliceLen - 1) / kMaxSliceLen;
+  int32_t target = 2 * (cus > 0 ? cus : 256);
+  int32_t g = (target + rows - 1) / rows;
+  if (g < g_min) g = g_min;
+  if (g > kMaxSlices) g = kMaxSlices;
+  if (g > nch) g = nch;
+  if (g < 1) g = 1;
+  const int32_t cps = (nch + g - 1) / g;
+  *slice_len = cps * kChunk;
+  *slices = (nch + cps - 1) / cps;
+  *nchunks = nch;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* lsamp_last_error(void) { return g_last_error.c_str(); }
+
+const char* lsamp_version(void) { return "lsamp 0.1.0 (gfx950, abi 1)"; }
+
+int64_t lsamp_abi_sizeof(const char* name) {
+  if (!name) return -1;
+  if (!strcmp(name, "lsamp_row_params")) return (int64_t)sizeof(lsamp_row_params);
+  if (!strcmp(name, "lsamp_penalty_entry")) return (int64_t)sizeof(lsamp_penalty_entry);
+  if (!strcmp(name, "lsamp_row_stats")) return (int64_t)sizeof(lsamp_row_stats);
+  if (!strcmp(name, "lsamp_sample_args")) return (int64_t)sizeof(lsamp_sample_args);
+  if (!strcmp(name, "lsamp_verify_args")) return (int64_t)sizeof(lsamp_verify_args);
+  if (!strcmp(name, "lsamp_generate_parameters")) return (int64_t)sizeof(lsamp_generate_parameters);
+  if (!strcmp(name, "lsamp_cbv2_params")) return (int64_t)sizeof(lsamp_cbv2_params);
+  return -1;
+}
+
+lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_vocab,
+                                  lsamp_context** out) {
+  if (!out) return fail(LSAMP_ERR_INVALID_ARGUMENT, "out is NULL");
+  *out = nullptr;
+  if (max_rows <= 0 || max_rows > (1 << 20))
+    return fail(LSAMP_ERR_SHAPE, "max_rows %d out of range [1, 1048576]", max_rows);
+  if (max_vocab <= 0 || max_vocab > kMaxVocab)
+    return fail(LSAMP_ERR_SHAPE, "max_vocab %d out of range [1, %d]", max_vocab, kMaxVocab);
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+    return fail(LSAMP_ERR_DEVICE, "device %d not available (%d devices)", device, ndev);
+  DeviceGuard guard(device);
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+    return fail(LSAMP_ERR_DEVICE, "hipGetDeviceProperties failed");
+
+  const size_t R = (size_t)max_rows;
+  const size_t chunks = (size_t)((max_vocab + kChunk - 1) / kChunk);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = align_up(off + bytes, 256);
+    return o;
+  };
+  const size_t o_sum = take(R * kMaxSlices * sizeof(SliceSummary));
+  const size_t o_rows = take(R * sizeof(RowInfo));
+  const size_t o_chunk = take(R * chunks * sizeof(uint64_t));
+  const size_t o_cand = take(R * kCandCap * sizeof(Candidate));
+  const size_t o_part = take(R * kMaxSlices * sizeof(SelectPartial));
+  const size_t o_cc = take(R * sizeof(uint32_t));
+  const size_t o_as = take(R * sizeof(uint32_t));
+  const size_t o_asel = take(R * sizeof(uint32_t));
+  const size_t o_vstats = take(R * sizeof(lsamp_row_stats));
+  const size_t o_vtok = take(R * sizeof(int32_t));
+  const size_t o_vfl = take(R * sizeof(uint32_t));
+  const size_t o_vprobe = take(R * sizeof(int32_t));
+  const size_t o_vu = take(R * sizeof(float));
+  const size_t o_vparams = take(R * sizeof(lsamp_row_params));
+  const size_t o_vres = take(R * chunks * sizeof(uint64_t));
+  const size_t o_ares = take(R * sizeof(uint32_t));
+  const size_t total = off;
+
+  void* block = nullptr;
+  if (hipMalloc(&block, total) != hipSuccess)
+    return fail(LSAMP_ERR_DEVICE, "hipMalloc(%zu) failed", total);
+  // Arrival counters and candidate counts must start at zero; the kernels
+  // return them to zero at the end of every step.
+  if (hipMemset(block, 0, total) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    (void)hipFree(block);
+    return fail(LSAMP_ERR_DEVICE, "hipMemset of the workspace failed");
+  }
+  lsamp_context* ctx = new lsamp_context();
+  ctx->device = device;
+  ctx->cus = prop.multiProcessorCount;
+  ctx->block = block;
+  ctx->bytes = total;
+  char* b = reinterpret_cast<char*>(block);
+  Workspace& ws = ctx->ws;
+  ws.max_rows = max_rows;
+  ws.max_vocab = max_vocab;
+  ws.max_chunks = (int32_t)chunks;
+  ws.summaries = reinterpret_cast<SliceSummary*>(b + o_sum);
+  ws.rows = reinterpret_cast<RowInfo*>(b + o_rows);
+  ws.chunk_w = reinterpret_cast<uint64_t*>(b + o_chunk);
+  ws.cands = reinterpret_cast<Candidate*>(b + o_cand);
+  ws.partials = reinterpret_cast<SelectPartial*>(b + o_part);
+  ws.cand_count = reinterpret_cast<uint32_t*>(b + o_cc);
+  ws.arrive_stats = reinterpret_cast<uint32_t*>(b + o_as);
+  ws.arrive_select = reinterpret_cast<uint32_t*>(b + o_asel);
+  ws.vstats = reinterpret_cast<lsamp_row_stats*>(b + o_vstats);
+  ws.vtokens = reinterpret_cast<int32_t*>(b + o_vtok);
+  ws.vflags = reinterpret_cast<uint32_t*>(b + o_vfl);
+  ws.vprobe = reinterpret_cast<int32_t*>(b + o_vprobe);
+  ws.vuniform = reinterpret_cast<float*>(b + o_vu);
+  ws.vparams = reinterpret_cast<lsamp_row_params*>(b + o_vparams);
+  ws.vres_chunk = reinterpret_cast<uint64_t*>(b + o_vres);
+  ws.arrive_resid = reinterpret_cast<uint32_t*>(b + o_ares);
+  *out = ctx;
+  return ok();
+}
+
+void lsamp_context_destroy(lsamp_context* ctx) {
+  if (!ctx) return;
+  {
+    DeviceGuard guard(ctx->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(ctx->block);
+  }
+  delete ctx;
+}
+
+lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* stream) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->semantics != LSAMP_SEM_MLXLM && a->semantics != LSAMP_SEM_CBV2)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown semantics %d", a->semantics);
+  if (a->dtype != LSAMP_DTYPE_F32 && a->dtype != LSAMP_DTYPE_BF16 && a->dtype != LSAMP_DTYPE_F16)
+    return fail(LSAMP_ERR_DTYPE, "unsupported dtype %d", a->dtype);
+  if (a->rows <= 0 || a->rows > ctx->ws.max_rows)
+    return fail(a->rows <= 0 ? LSAMP_ERR_SHAPE : LSAMP_ERR_CAPACITY,
+                "rows %d outside [1, %d]", a->rows, ctx->ws.max_rows);
+  if (a->vocab <= 0 || a->vocab > ctx->ws.max_vocab)
+    return fail(a->vocab <= 0 ? LSAMP_ERR_SHAPE : LSAMP_ERR_CAPACITY,
+                "vocab %d outside [1, %d]", a->vocab, ctx->ws.max_vocab);
+  if (a->row_stride < a->vocab)
+    return fail(LSAMP_ERR_SHAPE, "row_stride %lld < vocab %d", (long long)a->row_stride, a->vocab);
+  if (!a->logits || !a->params || !a->tokens)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "logits, params and tokens are required");
+  if (!a->uniforms && !a->philox_keys)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "either uniforms or philox_keys is required");
+  if ((a->penalty_row_ptr == nullptr) != (a->penalty_entries == nullptr))
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "penalty_row_ptr and penalty_entries go together");
+  if (a->bitmask) {
+    if (a->mask_words <= 0 || a->mask_bits < 0)
+      return fail(LSAMP_ERR_SHAPE, "mask_words %d / mask_bits %d invalid", a->mask_words,
+                  a->mask_bits);
+    // xgrammar: vocab_size <= bitmask words * 32 (grammar_matcher.cc:219-222)
+    if ((int64_t)a->mask_bits > (int64_t)a->mask_words * 32)
+      return fail(LSAMP_ERR_SHAPE, "mask_bits %d exceed %d words", a->mask_bits, a->mask_words);
+    if (a->mask_tail != LSAMP_MASK_TAIL_KEEP && a->mask_tail != LSAMP_MASK_TAIL_FORBID)
+      return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown mask_tail %d", a->mask_tail);
+  }
+  SamplePlan P{};
+  P.semantics = a->semantics;
+  P.rows = a->rows;
+  P.vocab = a->vocab;
+  P.dtype = a->dtype;
+  P.row_stride = a->row_stride;
+  plan_slices(a->rows, a->vocab, ctx->cus, &P.slices, &P.slice_len, &P.nchunks);
+  const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
+  P.aligned = aligned16(a->logits) && ((size_t)a->row_stride * es) % 16 == 0;
+  P.logits = a->logits;
+  P.logits2 = a->logits;
+  P.rows_split = a->rows;
+  P.params = a->params;
+  P.row_ptr = a->penalty_row_ptr;
+  P.entries = a->penalty_entries;
+  P.bitmask = a->bitmask;
+  P.mask_words = a->mask_words;
+  P.mask_bits = a->mask_bits;
+  P.mask_tail = a->mask_tail;
+  P.uniforms = a->uniforms;
+  P.philox_keys = a->philox_keys;
+  P.probe_tokens = a->probe_tokens;
+  P.tokens = a->tokens;
+  P.row_flags = a->row_flags;
+  P.processed = a->processed;
+  P.keep = a->keep;
+  P.stats = a->stats;
+  DeviceGuard guard(ctx->device);
+  const int err = launch_sample(ctx->ws, P, stream);
+  if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
+                            hipGetErrorString((hipError_t)err));
+  return ok();
+}
+
+// ---------------------------------------------------------------- resolution
+
+lsamp_status lsamp_resolve_generate_parameters(const lsamp_generate_parameters* gp,
+                                               lsamp_row_params* out, int32_t* contexts) {
+  if (!gp || !out) return fail(LSAMP_ERR_INVALID_ARGUMENT, "NULL argument");
+  lsamp_row_params r{};
+  // GenerateParameters.sampler() (Evaluate.swift:328-341)
+  const bool uses_top_p = gp->top_p > 0.0f && gp->top_p < 1.0f;
+  const bool uses_top_k = gp->top_k > 0;
+  const bool uses_min_p = gp->min_p > 0.0f;
+  if (gp->temperature == 0.0f) {
+    r.kind = LSAMP_KIND_ARGMAX;
+  } else if (uses_top_p || uses_top_k || uses_min_p) {
+    r.kind = LSAMP_KIND_FILTERED;
+  } else {
+    r.kind = LSAMP_KIND_CATEGORICAL;
+  }
+  r.temperature = gp->temperature;
+  // TopPSampler.init keeps each filter only when enabled (Evaluate.swift:420-427)
+  r.top_p = uses_top_p ? gp->top_p : 1.0f;
+  r.top_k = uses_top_k ? gp->top_k : 0;
+  r.min_p = uses_min_p ? gp->min_p : 0.0f;
+  // GenerateParameters.processor() (Evaluate.swift:343-387)
+  int32_t ctxs = 0;
+  r.repetition_penalty = 1.0f;
+  if (gp->has_repetition_penalty && gp->repetition_penalty != 0.0f &&
+      gp->repetition_penalty != 1.0f && gp->repetition_context_size > 0) {
+    r.repetition_penalty = gp->repetition_penalty;
+    ctxs |= 1;
+  }
+  r.presence_penalty = 0.0f;
+  if (gp->has_presence_penalty && gp->presence_penalty != 0.0f && gp->presence_context_size > 0) {
+    r.presence_penalty = gp->presence_penalty;
+    ctxs |= 2;
+  }
+  r.frequency_penalty = 0.0f;
+  if (gp->has_frequency_penalty && gp->frequency_penalty != 0.0f &&
+      gp->frequency_context_size > 0) {
+    r.frequency_penalty = gp->frequency_penalty;
+    ctxs |= 4;
+  }
+  *out = r;
+  if (contexts) *contexts = ctxs;
+  return ok();
+}
+
+lsamp_status lsamp_resolve_cbv2_params(const lsamp_cbv2_params* sp, int32_t vocab,
+                                       lsamp_row_params* out) {
+  if (!sp || !out) return fail(LSAMP_ERR_INVALID_ARGUMENT, "NULL argument");
+  if (vocab <= 0) return fail(LSAMP_ERR_SHAPE, "vocab %d must be positive", vocab);
+  lsamp_row_params r{};
+  // LogitsPipelineV2.setRows (LogitsPipelineV2.swift:188-227)
+  const bool greedy = sp->temperature < 1e-5f;  // greedyEpsilon (:79)
+  r.kind = greedy ? LSAMP_KIND_ARGMAX : LSAMP_KIND_FILTERED;
+  r.temperature = greedy ? 1.0f : sp->temperature;
+  r.top_k = 0;
+  r.top_p = 2.0f;
+  r.min_p = 0.0f;
+  if (!greedy) {
+    if (sp->top_k > 0 && sp->top_k < vocab) r.top_k = sp->top_k;
+    if (sp->top_p > 0.0f && sp->top_p < 1.0f)
+      r.top_p = sp->top_p;
+    else if (sp->top_p <= 0.0f)
+      r.top_p = 0.0f;  // top_p == 0 keeps only the most probable token (:204-207)
+    if (sp->min_p > 0.0f) r.min_p = sp->min_p < 1.0f ? sp->min_p : 1.0f;
+  }
+  const bool windowed = sp->repetition_penalty != 1.0f && sp->repetition_context_size > 0;
+  r.repetition_penalty = windowed ? sp->repetition_penalty : 1.0f;
+  if (sp->frequency_penalty != 0.0f || sp->presence_penalty != 0.0f) {
+    r.frequency_penalty = sp->frequency_penalty;
+    r.presence_penalty = sp->presence_penalty;
+  }
+  *out = r;
+  return ok();
+}
+
+// SamplerV2.mix (SamplerV2.swift:183-191).
+static uint64_t splitmix64(uint64_t v) {
+  uint64_t z = v + 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+uint64_t lsamp_rng_key(uint64_t seed, uint64_t request_id, uint64_t step) {
+  return splitmix64(splitmix64(splitmix64(seed) ^ request_id) ^ step);
+}
+
+float lsamp_rng_uniform(uint64_t key, uint32_t purpose) {
+  uint32_t c0 = purpose, c1 = 0, c2 = 0, c3 = 0;
+  uint32_t k0 = (uint32_t)key, k1 = (uint32_t)(key >> 32);
+  for (int round = 0; round < 10; ++round) {
+    if (round > 0) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
+    c1 = (uint32_t)p1;
+    c3 = (uint32_t)p0;
+    c0 = n0;
+    c2 = n2;
+  }
+  return (float)(c0 >> 8) * 5.9604644775390625e-08f;
+}
+
+lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* stream) {
+  (void)stream;
+  if (!ctx || !a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "NULL argument");
+  return fail(LSAMP_ERR_INVALID_ARGUMENT, "lsamp_verify: not available in this build");
+}
+
+}  // extern "C"

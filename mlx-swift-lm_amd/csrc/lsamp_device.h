@@ -1,0 +1,316 @@
+// lsamp_device.h — device helpers shared by the kernels: dtype decoding,
+// the deterministic exponential and fixed-point draw weights, Philox, and
+// block-level reductions / scans for 512-thread work-groups.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "lsamp_internal.h"
+
+namespace lsamp {
+namespace dev {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kPosInf = __builtin_huge_valf();
+
+// ---------------------------------------------------------------- dtypes
+template <int DT>
+struct Vec {
+  static constexpr int N = DT == LSAMP_DTYPE_F32 ? 4 : 8;  // elements per 16 bytes
+  static constexpr int ESIZE = DT == LSAMP_DTYPE_F32 ? 4 : 2;
+  static constexpr uint32_t NEG_INF_BITS =
+      DT == LSAMP_DTYPE_F32 ? 0xff800000u : (DT == LSAMP_DTYPE_BF16 ? 0xff80u : 0xfc00u);
+};
+
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+}
+
+// Element k of a 16-byte vector.
+template <int DT>
+__device__ __forceinline__ float vec_elem(const uint4& r, int k) {
+  if constexpr (DT == LSAMP_DTYPE_F32) {
+    const uint32_t v = k == 0 ? r.x : (k == 1 ? r.y : (k == 2 ? r.z : r.w));
+    return __uint_as_float(v);
+  } else {
+    const int q = k >> 1;
+    const uint32_t word = q == 0 ? r.x : (q == 1 ? r.y : (q == 2 ? r.z : r.w));
+    if constexpr (DT == LSAMP_DTYPE_BF16) {
+      return (k & 1) ? __uint_as_float(word & 0xffff0000u) : __uint_as_float(word << 16);
+    } else {
+      return half_bits_to_f32((k & 1) ? (word >> 16) : (word & 0xffffu));
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float load_scalar(const void* row, int64_t i) {
+  if constexpr (DT == LSAMP_DTYPE_F32) {
+    return reinterpret_cast<const float*>(row)[i];
+  } else if constexpr (DT == LSAMP_DTYPE_BF16) {
+    return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(row)[i] << 16);
+  } else {
+    return half_bits_to_f32(reinterpret_cast<const uint16_t*>(row)[i]);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t load_raw_bits(const void* row, int64_t i) {
+  if constexpr (DT == LSAMP_DTYPE_F32)
+    return reinterpret_cast<const uint32_t*>(row)[i];
+  else
+    return reinterpret_cast<const uint16_t*>(row)[i];
+}
+
+// Load the 16-byte vector starting at token i0; lanes past `end` (or the whole
+// vector when the row is not 16-byte aligned) are read one element at a time
+// and out-of-range lanes are filled with -inf bits.
+template <int DT>
+__device__ __forceinline__ uint4 load_vec(const void* row, int64_t i0, int64_t end, bool aligned) {
+  constexpr int N = Vec<DT>::N;
+  if (aligned && i0 + N <= end) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(row) +
+                                           i0 * Vec<DT>::ESIZE);
+  }
+  uint32_t b[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+    b[k] = (i0 + k < end) ? load_raw_bits<DT>(row, i0 + k) : Vec<DT>::NEG_INF_BITS;
+  uint4 r;
+  if constexpr (DT == LSAMP_DTYPE_F32) {
+    r.x = b[0];
+    r.y = b[1];
+    r.z = b[2];
+    r.w = b[3];
+  } else {
+    r.x = b[0] | (b[1] << 16);
+    r.y = b[2] | (b[3] << 16);
+    r.z = b[4] | (b[5] << 16);
+    r.w = b[6] | (b[7] << 16);
+  }
+  return r;
+}
+
+// Value an MLX array of `dt` holds after an op computed in float (RNE).
+__device__ __forceinline__ float round_bf16(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b & 0x7fffffffu) > 0x7f800000u) return __uint_as_float(((b >> 16) | 0x40u) << 16);
+  const uint32_t bias = 0x7fffu + ((b >> 16) & 1u);
+  return __uint_as_float(((b + bias) >> 16) << 16);
+}
+__device__ __forceinline__ float round_dtype(float v, int dt) {
+  if (dt == LSAMP_DTYPE_BF16) return round_bf16(v);
+  if (dt == LSAMP_DTYPE_F16) return (float)(_Float16)v;
+  return v;
+}
+
+// ------------------------------------------------------ deterministic math
+// e^d for d <= 0 with a fixed sequence of IEEE fp32 operations: Cody & Waite
+// (1980) range reduction with a two-part ln 2, Taylor polynomial of e^r to
+// degree 7 in Horner form with fma, exact scaling by 2^n.  The host restates
+// the same steps; results agree bit for bit.
+__device__ __forceinline__ float dexp(float d) {
+  if (!(d > -80.0f)) return 0.0f;
+  if (d > 0.0f) d = 0.0f;
+  const float n = __builtin_rintf(d * 1.44269504088896341f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, d);
+  r = __builtin_fmaf(-n, 1.428606765330187e-06f, r);
+  float p = 1.984126984e-04f;
+  p = __builtin_fmaf(p, r, 1.388888889e-03f);
+  p = __builtin_fmaf(p, r, 8.333333333e-03f);
+  p = __builtin_fmaf(p, r, 4.166666667e-02f);
+  p = __builtin_fmaf(p, r, 1.666666667e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  const int ni = (int)n;
+  return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+}
+
+// Fixed-point draw weight 2^40 * dexp(fl(fl(y - y_max) * scale)).
+__device__ __forceinline__ uint64_t weight(float y, float y_max, float scale) {
+  if (!(y > kNegInf)) return 0ull;
+  float d;
+  if (y == y_max) {
+    d = 0.0f;
+  } else {
+    const float diff = y - y_max;
+    d = diff * scale;
+  }
+  const float e = dexp(d);
+  return (uint64_t)(e * kWeightScale);
+}
+
+// The exponent argument used by `weight` (for entropy accumulation).
+__device__ __forceinline__ float weight_arg(float y, float y_max, float scale) {
+  if (y == y_max) return 0.0f;
+  const float diff = y - y_max;
+  return diff * scale;
+}
+
+__device__ __forceinline__ uint32_t uniform_u32(float u) {
+  if (!(u > 0.0f)) return 0u;
+  if (u >= 1.0f) return 0xffffffffu;
+  return (uint32_t)(u * 4294967296.0f);
+}
+
+__device__ __forceinline__ uint64_t scaled_target(uint32_t U, uint64_t W) {
+  const uint64_t hi = W >> 32, lo = W & 0xffffffffull;
+  return (uint64_t)U * hi + (((uint64_t)U * lo) >> 32);
+}
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11).
+__device__ __forceinline__ uint32_t philox_x0(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                              uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int round = 0; round < 10; ++round) {
+    if (round > 0) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+    const uint32_t n0 = hi1 ^ c1 ^ k0;
+    const uint32_t n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+  }
+  return c0;
+}
+
+__device__ __forceinline__ float philox_uniform(uint64_t key, uint32_t purpose) {
+  const uint32_t x0 = philox_x0(purpose, 0u, 0u, 0u, (uint32_t)key, (uint32_t)(key >> 32));
+  return (float)(x0 >> 8) * 5.9604644775390625e-08f;
+}
+
+// Order-preserving key of a float (ascending).
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(b);
+}
+
+// Histogram bin of a transformed logit: floor(x * c32) with c32 = 32 / T,
+// clamped so the integer conversion is defined for any finite x.
+__device__ __forceinline__ float bin_pos(float x, float c32) {
+  const float s = x * c32;
+  return __builtin_fminf(__builtin_fmaxf(s, -1.0e9f), 1.0e9f);
+}
+__device__ __forceinline__ int bin_of(float x, float c32) {
+  return (int)__builtin_floorf(bin_pos(x, c32));
+}
+
+// ------------------------------------------------------------ block ops
+// All helpers assume blockDim.x == kThreads and are called by every thread.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    T o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_min(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    T o = __shfl_xor(v, off, 64);
+    v = o < v ? o : v;
+  }
+  return v;
+}
+
+// scratch: at least kWaves elements of T.
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* scratch) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  T r = scratch[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) r += scratch[i];
+  __syncthreads();
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ T block_max(T v, T* scratch) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  T r = scratch[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) r = scratch[i] > r ? scratch[i] : r;
+  __syncthreads();
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ T block_min(T v, T* scratch) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_min(v);
+  __syncthreads();
+  if (lane == 0) scratch[w] = v;
+  __syncthreads();
+  T r = scratch[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) r = scratch[i] < r ? scratch[i] : r;
+  __syncthreads();
+  return r;
+}
+
+// Inclusive scan within a wave.
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    T o = __shfl_up(v, off, 64);
+    if (lane >= off) v += o;
+  }
+  return v;
+}
+
+// Exclusive block scan in thread order; returns the exclusive prefix and
+// writes the block total.  scratch: at least kWaves elements of T.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T* scratch, T* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const T incl = wave_incl_scan(v);
+  __syncthreads();
+  if (lane == 63) scratch[w] = incl;
+  __syncthreads();
+  T off = T(0), tot = T(0);
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) {
+    if (i < w) off += scratch[i];
+    tot += scratch[i];
+  }
+  __syncthreads();
+  *total = tot;
+  return off + incl - v;
+}
+
+// Device-coherent load of data another work-group published before its
+// release fence (bypasses non-coherent caches).
+template <typename T>
+__device__ __forceinline__ T ld_coherent(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace dev
+}  // namespace lsamp

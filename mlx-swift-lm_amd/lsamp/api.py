@@ -1,0 +1,213 @@
+"""torch-facing wrapper of the C ABI (include/lsamp.h).
+
+Device memory and streams come from torch; every computation runs in the HIP
+kernels of liblsamp.so.  Nothing here falls back to a CPU path: a missing
+library raises _ffi.LibraryMissing.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Iterable, Optional, Sequence
+
+import numpy as np
+import torch
+
+from . import _ffi
+
+PENALTY_DTYPE = np.dtype([("token", "<i4"), ("count", "<i4"), ("flags", "<u4"), ("bias", "<f4")])
+PARAMS_DTYPE = np.dtype([
+    ("kind", "<i4"), ("temperature", "<f4"), ("top_k", "<i4"), ("top_p", "<f4"),
+    ("min_p", "<f4"), ("repetition_penalty", "<f4"), ("presence_penalty", "<f4"),
+    ("frequency_penalty", "<f4")])
+STATS_DTYPE = np.dtype([
+    ("max_value", "<f4"), ("log_normalizer", "<f4"), ("kept", "<i4"), ("token", "<i4"),
+    ("kept_weight", "<u8"), ("probe_weight", "<u8"), ("cut_value", "<f4"),
+    ("kept_mass", "<f4"), ("kept_entropy", "<f4"), ("probe_prob", "<f4")])
+
+TORCH_DTYPE = {_ffi.DTYPE_F32: torch.float32, _ffi.DTYPE_BF16: torch.bfloat16,
+               _ffi.DTYPE_F16: torch.float16}
+LSAMP_DTYPE = {v: k for k, v in TORCH_DTYPE.items()}
+
+
+def params_array(rows: Iterable) -> np.ndarray:
+    """Per-row parameters (dicts, RowParams or a structured array) -> numpy
+    structured array in the lsamp_row_params layout."""
+    if isinstance(rows, np.ndarray) and rows.dtype == PARAMS_DTYPE:
+        return rows
+    rows = list(rows)
+    out = np.zeros(len(rows), PARAMS_DTYPE)
+    for i, p in enumerate(rows):
+        if isinstance(p, _ffi.RowParams):
+            p = {f: getattr(p, f) for f, _ in _ffi.RowParams._fields_}
+        for k, v in p.items():
+            out[i][k] = v
+    return out
+
+
+def to_device_bytes(arr: np.ndarray, device) -> torch.Tensor:
+    """Host numpy array -> device uint8 tensor holding the same bytes."""
+    a = np.ascontiguousarray(arr)
+    t = torch.from_numpy(a.view(np.uint8).reshape(-1).copy())
+    return t.to(device)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def current_stream_handle(device=None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class Context:
+    """Owns the device workspace (lsamp_context) for up to `max_rows` rows of
+    up to `max_vocab` logits on `device`."""
+
+    def __init__(self, device: int = 0, max_rows: int = 512, max_vocab: int = 262144):
+        self.lib = _ffi.load_library()
+        h = ctypes.c_void_p()
+        _ffi.check(self.lib.lsamp_context_create(device, max_rows, max_vocab, ctypes.byref(h)),
+                   "lsamp_context_create")
+        self.handle = h
+        self.device = device
+        self.max_rows = max_rows
+        self.max_vocab = max_vocab
+
+    def close(self):
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.lib.lsamp_context_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ----------------------------------------------------------------- sample
+    def prepare_sample(self, logits: torch.Tensor, params, *, semantics: int, vocab: Optional[int] = None,
+                       row_ptr=None, entries=None, bitmask=None, mask_bits: Optional[int] = None,
+                       mask_tail: int = _ffi.MASK_TAIL_KEEP, uniforms=None, philox_keys=None,
+                       probe_tokens=None, want_processed: bool = False, want_keep: bool = False,
+                       want_stats: bool = False) -> "PreparedSample":
+        return PreparedSample(self, logits, params, semantics=semantics, vocab=vocab,
+                              row_ptr=row_ptr, entries=entries, bitmask=bitmask,
+                              mask_bits=mask_bits, mask_tail=mask_tail, uniforms=uniforms,
+                              philox_keys=philox_keys, probe_tokens=probe_tokens,
+                              want_processed=want_processed, want_keep=want_keep,
+                              want_stats=want_stats)
+
+    def sample(self, logits: torch.Tensor, params, **kw) -> dict:
+        prep = self.prepare_sample(logits, params, **kw)
+        prep.launch()
+        return prep.outputs()
+
+
+class PreparedSample:
+    """A fully bound lsamp_sample call: every input and output buffer is a
+    device tensor kept alive by this object, so `launch()` is one C call (and
+    can be captured in a HIP graph)."""
+
+    def __init__(self, ctx: Context, logits: torch.Tensor, params, *, semantics, vocab, row_ptr,
+                 entries, bitmask, mask_bits, mask_tail, uniforms, philox_keys, probe_tokens,
+                 want_processed, want_keep, want_stats):
+        dev = logits.device
+        if logits.dim() != 2:
+            raise ValueError("logits must be [rows, row_stride]")
+        if logits.stride(1) != 1:
+            raise ValueError("logits rows must be contiguous")
+        rows = logits.shape[0]
+        V = int(vocab) if vocab is not None else logits.shape[1]
+        self.ctx = ctx
+        self.keep_alive = [logits]
+        if isinstance(params, torch.Tensor):
+            self.params = params
+        else:
+            self.params = to_device_bytes(params_array(params), dev)
+        self.keep_alive.append(self.params)
+        a = _ffi.SampleArgs()
+        a.semantics = semantics
+        a.rows = rows
+        a.vocab = V
+        a.dtype = LSAMP_DTYPE[logits.dtype]
+        # a size-1 row axis may carry any stride (numpy [None, :] gives 0)
+        a.row_stride = logits.stride(0) if rows > 1 else logits.shape[1]
+        a.logits = logits.data_ptr()
+        a.params = self.params.data_ptr()
+
+        def dev_tensor(x, np_dtype, torch_dtype):
+            if x is None:
+                return None
+            if isinstance(x, torch.Tensor):
+                return x.to(dev)
+            return torch.from_numpy(np.ascontiguousarray(x, np_dtype)).to(dev)
+
+        if row_ptr is not None:
+            rp = dev_tensor(row_ptr, np.int32, torch.int32)
+            if isinstance(entries, torch.Tensor):
+                en = entries.to(dev)
+            else:
+                e = np.ascontiguousarray(entries, PENALTY_DTYPE)
+                if len(e) == 0:
+                    e = np.zeros(1, PENALTY_DTYPE)
+                en = to_device_bytes(e, dev)
+            self.keep_alive += [rp, en]
+            a.penalty_row_ptr = rp.data_ptr()
+            a.penalty_entries = en.data_ptr()
+        if bitmask is not None:
+            bm = dev_tensor(bitmask, np.uint32, torch.int32)
+            if bm.dtype != torch.int32:
+                bm = bm.view(torch.int32) if bm.element_size() == 4 else bm.to(torch.int32)
+            self.keep_alive.append(bm)
+            a.bitmask = bm.data_ptr()
+            a.mask_words = bm.shape[-1]
+            a.mask_bits = int(mask_bits) if mask_bits is not None else a.mask_words * 32
+            a.mask_tail = mask_tail
+        if uniforms is not None:
+            u = dev_tensor(uniforms, np.float32, torch.float32)
+            self.keep_alive.append(u)
+            a.uniforms = u.data_ptr()
+        if philox_keys is not None:
+            k = dev_tensor(np.asarray(philox_keys, np.uint64).view(np.int64), np.int64, torch.int64)
+            self.keep_alive.append(k)
+            a.philox_keys = k.data_ptr()
+        if probe_tokens is not None:
+            pt = dev_tensor(probe_tokens, np.int32, torch.int32)
+            self.keep_alive.append(pt)
+            a.probe_tokens = pt.data_ptr()
+        self.tokens = torch.empty(rows, dtype=torch.int32, device=dev)
+        self.row_flags = torch.empty(rows, dtype=torch.int32, device=dev)
+        a.tokens = self.tokens.data_ptr()
+        a.row_flags = self.row_flags.data_ptr()
+        self.processed = torch.empty((rows, V), dtype=torch.float32, device=dev) if want_processed else None
+        self.keep = torch.empty((rows, V), dtype=torch.uint8, device=dev) if want_keep else None
+        self.stats = (torch.empty(rows * STATS_DTYPE.itemsize, dtype=torch.uint8, device=dev)
+                      if want_stats else None)
+        a.processed = _ptr(self.processed)
+        a.keep = _ptr(self.keep)
+        a.stats = _ptr(self.stats)
+        self.args = a
+        self._byref = ctypes.byref(a)
+
+    def launch(self, stream: Optional[int] = None) -> None:
+        s = stream if stream is not None else current_stream_handle(self.tokens.device)
+        st = self.ctx.lib.lsamp_sample(self.ctx.handle, self._byref, ctypes.c_void_p(s))
+        if st != 0:
+            raise _ffi.LsampError(st, "lsamp_sample")
+
+    def outputs(self) -> dict:
+        out = {"tokens": self.tokens, "row_flags": self.row_flags}
+        if self.processed is not None:
+            out["processed"] = self.processed
+        if self.keep is not None:
+            out["keep"] = self.keep
+        if self.stats is not None:
+            out["stats"] = self.stats
+        return out
+
+    def stats_numpy(self) -> np.ndarray:
+        return self.stats.cpu().numpy().view(STATS_DTYPE)
+
+
+def stats_to_numpy(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(STATS_DTYPE)

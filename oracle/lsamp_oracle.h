@@ -1,0 +1,97 @@
+/*
+ * lsamp_oracle.h — CPU restatement of the reference's logits-to-token stage.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or the timed CPU baseline), never as the thing measured or shipped.  The
+ * product path (liblsamp.so) does not link it.
+ *
+ * It follows the reference op sequence literally: full per-row sorts for
+ * top-p / top-k / min-p, dense per-row penalty tensors, one materialized
+ * intermediate per stage.  Each function names the reference lines it restates.
+ * Host pointers throughout.
+ */
+#ifndef LSAMP_ORACLE_H
+#define LSAMP_ORACLE_H
+
+#include <stdint.h>
+
+#include "../include/lsamp.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct lso_sample_args {
+  int32_t semantics;
+  int32_t rows;
+  int32_t vocab;
+  int32_t dtype;
+  int64_t row_stride;
+  const void* logits;
+  const lsamp_row_params* params;
+  const int32_t* penalty_row_ptr;
+  const lsamp_penalty_entry* penalty_entries;
+  const uint32_t* bitmask;
+  int32_t mask_words;
+  int32_t mask_bits;
+  int32_t mask_tail;
+  const float* uniforms;       /* or NULL -> lso_rng_uniform(philox_keys[r], 0) */
+  const uint64_t* philox_keys;
+  const int32_t* probe_tokens; /* or NULL */
+  int32_t threads;             /* worker threads over rows (<= 1: serial) */
+  /* outputs (NULL = not wanted) */
+  int32_t* tokens;       /* [rows] */
+  uint32_t* row_flags;   /* [rows] */
+  float* processed;      /* [rows, vocab] filter-space logits before the filters */
+  uint8_t* keep;         /* [rows, vocab] 1 = token survives the filters */
+  float* top_p_margin;   /* [rows, vocab] signed distance of the top-p test */
+  float* min_p_margin;   /* [rows, vocab] signed distance of the min-p test */
+  double* top_p_margin_exact; /* [rows, vocab] the top-p distance in exact
+                                 (double) arithmetic from the same logits */
+  lsamp_row_stats* stats;/* [rows] */
+} lso_sample_args;
+
+/* Full sampling step (both semantics).  Returns 0 or a negative status. */
+int32_t lso_sample(const lso_sample_args* a);
+
+typedef struct lso_verify_args {
+  int32_t mode;
+  int32_t sequences;
+  int32_t window;
+  int32_t vocab;
+  int32_t dtype;
+  const void* target_logits;
+  const void* draft_logits;
+  const int32_t* draft_tokens;
+  const lsamp_row_params* params;
+  const float* uniforms;
+  float typical_delta;
+  int32_t threads;
+  int32_t* accepted;
+  int32_t* tokens;
+  uint8_t* accept_mask;
+  double* typical_margin; /* [S, W-1] or NULL: p(draft) - floor (TYPICAL) */
+} lso_verify_args;
+
+/* MTP verification (RESIDUAL / EXACT / TYPICAL).  Returns 0 or < 0. */
+int32_t lso_verify(const lso_verify_args* a);
+
+/* Building blocks exposed for known-answer tests. */
+float lso_dexp(float d);
+uint64_t lso_weight(float y, float y_max, float scale);
+int32_t lso_draw(int32_t n, const float* y, const uint8_t* keep, float scale, float u,
+                 uint64_t* total_out);
+void lso_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+uint64_t lso_rng_key(uint64_t seed, uint64_t id, uint64_t step);
+float lso_rng_uniform(uint64_t key, uint32_t purpose);
+float lso_bf16_to_f32(uint16_t h);
+uint16_t lso_f32_to_bf16(float f);
+float lso_f16_to_f32(uint16_t h);
+uint16_t lso_f32_to_f16(float f);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

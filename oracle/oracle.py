@@ -1,0 +1,257 @@
+"""ctypes front end of the oracle (liblsamp_oracle.so).
+
+TEST INFRASTRUCTURE ONLY.  Imported by tests/, by __graft_entry__.smoke() as
+the checker and by bench.py's cpu_baseline leg; never by the product path.
+All arrays are host numpy arrays.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+from ctypes import POINTER, Structure, c_double, c_float, c_int32, c_int64, c_uint8, c_uint32, c_uint64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REPO = os.path.dirname(HERE)
+sys.path.insert(0, os.path.join(REPO, "mlx-swift-lm_amd"))
+
+from lsamp import _ffi  # noqa: E402  (struct layouts shared with the ABI)
+
+LIB_PATH = os.path.join(HERE, "liblsamp_oracle.so")
+
+
+class LsoSampleArgs(Structure):
+    _fields_ = [
+        ("semantics", c_int32), ("rows", c_int32), ("vocab", c_int32), ("dtype", c_int32),
+        ("row_stride", c_int64), ("logits", c_void_p), ("params", c_void_p),
+        ("penalty_row_ptr", c_void_p), ("penalty_entries", c_void_p),
+        ("bitmask", c_void_p), ("mask_words", c_int32), ("mask_bits", c_int32),
+        ("mask_tail", c_int32), ("uniforms", c_void_p), ("philox_keys", c_void_p),
+        ("probe_tokens", c_void_p), ("threads", c_int32),
+        ("tokens", c_void_p), ("row_flags", c_void_p), ("processed", c_void_p),
+        ("keep", c_void_p), ("top_p_margin", c_void_p), ("min_p_margin", c_void_p),
+        ("top_p_margin_exact", c_void_p), ("stats", c_void_p),
+    ]
+
+
+class LsoVerifyArgs(Structure):
+    _fields_ = [
+        ("mode", c_int32), ("sequences", c_int32), ("window", c_int32), ("vocab", c_int32),
+        ("dtype", c_int32), ("target_logits", c_void_p), ("draft_logits", c_void_p),
+        ("draft_tokens", c_void_p), ("params", c_void_p), ("uniforms", c_void_p),
+        ("typical_delta", c_float), ("threads", c_int32), ("accepted", c_void_p),
+        ("tokens", c_void_p), ("accept_mask", c_void_p), ("typical_margin", c_void_p),
+    ]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        L.lso_sample.argtypes = [POINTER(LsoSampleArgs)]
+        L.lso_sample.restype = c_int32
+        L.lso_verify.argtypes = [POINTER(LsoVerifyArgs)]
+        L.lso_verify.restype = c_int32
+        L.lso_dexp.argtypes = [c_float]
+        L.lso_dexp.restype = c_float
+        L.lso_weight.argtypes = [c_float, c_float, c_float]
+        L.lso_weight.restype = c_uint64
+        L.lso_draw.argtypes = [c_int32, c_void_p, c_void_p, c_float, c_float, POINTER(c_uint64)]
+        L.lso_draw.restype = c_int32
+        L.lso_philox4x32_10.argtypes = [c_void_p, c_void_p, c_void_p]
+        L.lso_philox4x32_10.restype = None
+        L.lso_rng_key.argtypes = [c_uint64, c_uint64, c_uint64]
+        L.lso_rng_key.restype = c_uint64
+        L.lso_rng_uniform.argtypes = [c_uint64, c_uint32]
+        L.lso_rng_uniform.restype = c_float
+        L.lso_f32_to_bf16.argtypes = [c_float]
+        L.lso_f32_to_bf16.restype = ctypes.c_uint16
+        L.lso_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.lso_bf16_to_f32.restype = c_float
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(c_void_p).value
+
+
+def params_array(rows):
+    """List of dicts / RowParams -> contiguous RowParams array."""
+    arr = (_ffi.RowParams * len(rows))()
+    for i, p in enumerate(rows):
+        if isinstance(p, _ffi.RowParams):
+            arr[i] = p
+        else:
+            for k, v in p.items():
+                setattr(arr[i], k, v)
+    return arr
+
+
+PARAMS_DTYPE = np.dtype([
+    ("kind", "<i4"), ("temperature", "<f4"), ("top_k", "<i4"), ("top_p", "<f4"),
+    ("min_p", "<f4"), ("repetition_penalty", "<f4"), ("presence_penalty", "<f4"),
+    ("frequency_penalty", "<f4")])
+
+
+def _params_buffer(params):
+    """Per-row params (structured array, RowParams array, or list of dicts /
+    RowParams) -> contiguous numpy bytes in the lsamp_row_params layout."""
+    if isinstance(params, np.ndarray):
+        return np.ascontiguousarray(params)
+    if isinstance(params, ctypes.Array):
+        return np.frombuffer(bytes(params), dtype=PARAMS_DTYPE).copy()
+    arr = params_array(params)
+    return np.frombuffer(bytes(arr), dtype=PARAMS_DTYPE).copy()
+
+
+def entries_array(entries):
+    """Structured numpy array of PenaltyEntry (token, count, flags, bias)."""
+    dt = np.dtype([("token", "<i4"), ("count", "<i4"), ("flags", "<u4"), ("bias", "<f4")])
+    out = np.zeros(len(entries), dtype=dt)
+    for i, e in enumerate(entries):
+        out[i] = e
+    return out
+
+
+PENALTY_DTYPE = np.dtype([("token", "<i4"), ("count", "<i4"), ("flags", "<u4"), ("bias", "<f4")])
+STATS_DTYPE = np.dtype([
+    ("max_value", "<f4"), ("log_normalizer", "<f4"), ("kept", "<i4"), ("token", "<i4"),
+    ("kept_weight", "<u8"), ("probe_weight", "<u8"), ("cut_value", "<f4"),
+    ("kept_mass", "<f4"), ("kept_entropy", "<f4"), ("probe_prob", "<f4")])
+
+
+def sample(*, semantics, logits, dtype, params, row_ptr=None, entries=None, bitmask=None,
+           mask_bits=0, mask_tail=0, uniforms=None, philox_keys=None, probe_tokens=None,
+           threads=1, want_processed=False, want_keep=False, want_margins=False,
+           want_stats=False, vocab=None, row_stride=None):
+    """Run the oracle.  `logits` is a 2-D numpy array: float32, or uint16 bit
+    patterns for bf16 / f16 (dtype says which)."""
+    logits = np.ascontiguousarray(logits)
+    rows = logits.shape[0]
+    V = vocab if vocab is not None else logits.shape[1]
+    stride = row_stride if row_stride is not None else logits.shape[1]
+    params_keep = _params_buffer(params)
+    out = {"tokens": np.zeros(rows, np.int32), "row_flags": np.zeros(rows, np.uint32)}
+    if want_processed:
+        out["processed"] = np.zeros((rows, V), np.float32)
+    if want_keep:
+        out["keep"] = np.zeros((rows, V), np.uint8)
+    if want_margins:
+        out["top_p_margin"] = np.zeros((rows, V), np.float32)
+        out["min_p_margin"] = np.zeros((rows, V), np.float32)
+        out["top_p_margin_exact"] = np.zeros((rows, V), np.float64)
+    if want_stats:
+        out["stats"] = np.zeros(rows, STATS_DTYPE)
+    a = LsoSampleArgs()
+    a.semantics = semantics
+    a.rows = rows
+    a.vocab = V
+    a.dtype = dtype
+    a.row_stride = stride
+    a.logits = _ptr(logits)
+    a.params = params_keep.ctypes.data_as(c_void_p).value
+    if row_ptr is not None:
+        row_ptr = np.ascontiguousarray(row_ptr, np.int32)
+        entries = np.ascontiguousarray(entries, PENALTY_DTYPE)
+        a.penalty_row_ptr = _ptr(row_ptr)
+        a.penalty_entries = _ptr(entries) if len(entries) else _ptr(np.zeros(1, PENALTY_DTYPE))
+    if bitmask is not None:
+        bitmask = np.ascontiguousarray(bitmask, np.uint32)
+        a.bitmask = _ptr(bitmask)
+        a.mask_words = bitmask.shape[1]
+        a.mask_bits = mask_bits
+        a.mask_tail = mask_tail
+    if uniforms is not None:
+        uniforms = np.ascontiguousarray(uniforms, np.float32)
+        a.uniforms = _ptr(uniforms)
+    if philox_keys is not None:
+        philox_keys = np.ascontiguousarray(philox_keys, np.uint64)
+        a.philox_keys = _ptr(philox_keys)
+    if probe_tokens is not None:
+        probe_tokens = np.ascontiguousarray(probe_tokens, np.int32)
+        a.probe_tokens = _ptr(probe_tokens)
+    a.threads = threads
+    for k in ("tokens", "row_flags", "processed", "keep", "top_p_margin", "min_p_margin",
+              "top_p_margin_exact", "stats"):
+        if k in out:
+            setattr(a, k, _ptr(out[k]))
+    st = lib().lso_sample(ctypes.byref(a))
+    if st != 0:
+        raise RuntimeError(f"lso_sample failed: {st}")
+    return out
+
+
+def verify(*, mode, target, draft, draft_tokens, dtype, params, uniforms, typical_delta=0.0,
+           threads=1):
+    """target [S, W, V], draft [S, W-1, V] (or None), draft_tokens [S, W-1]."""
+    target = np.ascontiguousarray(target)
+    S, W, V = target.shape
+    if draft is not None:
+        draft = np.ascontiguousarray(draft)
+    draft_tokens = np.ascontiguousarray(draft_tokens, np.int32)
+    uniforms = np.ascontiguousarray(uniforms, np.float32)
+    params_keep = _params_buffer(params)
+    out = {"accepted": np.zeros(S, np.int32), "tokens": np.zeros((S, W), np.int32),
+           "accept_mask": np.zeros((S, W - 1), np.uint8),
+           "typical_margin": np.zeros((S, W - 1), np.float64)}
+    a = LsoVerifyArgs()
+    a.mode = mode
+    a.sequences = S
+    a.window = W
+    a.vocab = V
+    a.dtype = dtype
+    a.target_logits = _ptr(target)
+    a.draft_logits = _ptr(draft)
+    a.draft_tokens = _ptr(draft_tokens)
+    a.params = params_keep.ctypes.data_as(c_void_p).value
+    a.uniforms = _ptr(uniforms)
+    a.typical_delta = typical_delta
+    a.threads = threads
+    a.accepted = _ptr(out["accepted"])
+    a.tokens = _ptr(out["tokens"])
+    a.accept_mask = _ptr(out["accept_mask"])
+    a.typical_margin = _ptr(out["typical_margin"])
+    st = lib().lso_verify(ctypes.byref(a))
+    if st != 0:
+        raise RuntimeError(f"lso_verify failed: {st}")
+    return out
+
+
+def dexp(d):
+    return lib().lso_dexp(float(d))
+
+
+def weight(y, y_max, scale=1.0):
+    return lib().lso_weight(float(y), float(y_max), float(scale))
+
+
+def draw(y, keep, scale, u):
+    y = np.ascontiguousarray(y, np.float32)
+    keep = np.ascontiguousarray(keep, np.uint8)
+    tot = c_uint64(0)
+    t = lib().lso_draw(len(y), _ptr(y), _ptr(keep), float(scale), float(u), ctypes.byref(tot))
+    return t, tot.value
+
+
+def philox(ctr, key):
+    c = np.ascontiguousarray(ctr, np.uint32)
+    k = np.ascontiguousarray(key, np.uint32)
+    o = np.zeros(4, np.uint32)
+    lib().lso_philox4x32_10(_ptr(c), _ptr(k), _ptr(o))
+    return o
+
+
+def rng_key(seed, rid, step):
+    return lib().lso_rng_key(seed, rid, step)
+
+
+def rng_uniform(key, purpose=0):
+    return lib().lso_rng_uniform(key, purpose)
