@@ -1,0 +1,199 @@
+#!/usr/bin/env python3
+"""Benchmark of the logits-to-token stage on one MI355X.
+
+Headline workload (the metric's configuration): one CBv2 decode sampling step
+over B=64 rows of V=151,936 bf16 logits (N(0,3^2) plus a per-row Zipf(1.1)
+log-prior), 2048-token Zipf output histories feeding presence 0.5 and
+frequency 0.3 penalties, T=0.8, top-k 50, top-p 0.95, min-p 0.05, one uniform
+per row.  A "step" is one lsamp_sample call over that batch.
+
+* value: steps/s of whole steps replayed from a HIP graph.  The graph holds
+  `--copies` steps over distinct copies of the input (16 x 19.4 MB, more than
+  the 256 MB Infinity Cache holds), so each step reads its logits from HBM.
+* kernel times: an eager pass with the library's per-kernel timing hook (HIP
+  events on the launch stream, queue kept full by a leading GPU sleep).
+* roofline: algorithmic bytes of one step / average duration of the stats
+  kernel (the one pass that reads the logits from HBM), against 8 TB/s.
+* cpu_baseline: the oracle (the reference op sequence restated in C: full
+  sorts, dense penalty tensors) timed on the host's cores on whole steps.
+
+Usage: python bench.py [--gpus 1] [--steps 1600] [--warmup 160]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "mlx-swift-lm_amd"))
+
+METRIC = "sampling steps/s + µs/step at B=64 V=151,936; achieved HBM GB/s vs 8 TB/s"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1600)
+    ap.add_argument("--warmup", type=int, default=160)
+    ap.add_argument("--copies", type=int, default=16)
+    ap.add_argument("--kernel-steps", type=int, default=512)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic", default=os.path.join(REPO, "profiles", "traffic_c2.json"),
+                    help="measured HBM traffic per launch (rocprofv3 --pmc summary)")
+    return ap.parse_args()
+
+
+def cpu_baseline(cfg, seconds):
+    """Time whole oracle steps on the host's cores (bounded sample)."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    threads = min(16, os.cpu_count() or 1)
+    kw = dict(semantics=cfg["semantics"], logits=cfg["logits"], dtype=cfg["dtype"],
+              params=cfg["params"], row_ptr=cfg["row_ptr"], entries=cfg["entries"],
+              uniforms=cfg["uniforms"])
+    O.sample(threads=threads, **kw)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.sample(threads=threads, **kw)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 3:
+            break
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": n / el, "unit": "steps/s", "cores": threads, "kind": "port",
+            "sample": f"{n} whole steps of the same workload ({cfg['rows']} rows) in {el:.1f} s, "
+                      f"rows over {threads} threads; host {model}; ms/step {1e3 * el / n:.2f}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py runs on one GPU only: the sampling stage is row-parallel and needs no "
+              "collective; multi-GPU runs are not part of this build.", file=sys.stderr)
+        return 2
+    import numpy as np
+    import torch
+
+    from lsamp import _ffi, workloads as W
+    from lsamp.api import Context
+
+    cfg = W.config2()
+    B, V, R = cfg["rows"], cfg["vocab"], args.copies
+    steps = max(R, (args.steps + R - 1) // R * R)
+    warm = max(R, (args.warmup + R - 1) // R * R)
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(7)
+    base = torch.from_numpy(cfg["logits"].view(np.int16)).view(torch.bfloat16)
+    # R copies in HBM: copy 0 is the workload itself, the others perturb
+    # one random token per row so no two copies share cache lines' contents
+    copies = torch.empty((R, B, V), dtype=torch.bfloat16, device=dev)
+    for i in range(R):
+        copies[i].copy_(base)
+        if i:
+            idx = torch.from_numpy(rng.integers(0, V, B)).to(dev)
+            copies[i, torch.arange(B, device=dev), idx] = 0.0
+    uniforms = torch.from_numpy(rng.random((R, B), dtype=np.float32)).to(dev)
+    uniforms[0] = torch.from_numpy(cfg["uniforms"]).to(dev)
+    ctx = Context(0, max_rows=B, max_vocab=V)
+    preps = [ctx.prepare_sample(copies[i], cfg["params"], semantics=cfg["semantics"],
+                                row_ptr=cfg["row_ptr"], entries=cfg["entries"],
+                                uniforms=uniforms[i]) for i in range(R)]
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for p in preps:
+            p.launch()
+    torch.cuda.synchronize()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for p in preps:
+            p.launch()
+    torch.cuda.synchronize()
+
+    # warm-up, then exactly `steps` steps
+    for _ in range(warm // R):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps // R):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall_s = t1 - t0
+    ev_ms = e0.elapsed_time(e1)
+    us_step = 1e6 * wall_s / steps
+
+    # per-kernel durations: eager launches with the timing hook, queue kept full
+    kn = min(args.kernel_steps, 4096)
+    ctx.set_timing(True)
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(50_000_000)
+        for i in range(kn):
+            preps[i % R].launch()
+    torch.cuda.synchronize()
+    k1_ms, k2_ms, n_timed = ctx.read_timing()
+    ctx.set_timing(False)
+    k1_us = 1e3 * k1_ms / n_timed
+    k2_us = 1e3 * k2_ms / n_timed
+
+    # correctness guard for the copy that is the workload itself
+    tok0 = preps[0].tokens.cpu().numpy()
+
+    alg_bytes = W.algorithmic_bytes(cfg)
+    achieved = alg_bytes / (k1_us * 1e-6) / 1e9
+    traffic = None
+    if args.traffic and os.path.exists(args.traffic):
+        with open(args.traffic) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    out = {
+        "metric": METRIC,
+        "value": steps / wall_s,
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm,
+        "ms_per_step": 1e3 * wall_s / steps,
+        "us_per_step": us_step,
+        "us_per_step_events": 1e3 * ev_ms / steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"], "rows": B, "vocab": V, "logits_dtype": "bf16",
+                   "semantics": "CBv2", "input_copies": R, "graph_steps_per_replay": R},
+        "kernel_us": {"k_stats": k1_us, "k_select": k2_us, "timed_calls": n_timed},
+        "step_effective_GBps": alg_bytes / (us_step * 1e-6) / 1e9,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "algorithmic_bytes": alg_bytes, "kernel": "k_stats"},
+        "tokens_copy0_head": tok0[:4].tolist(),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    ctx.close()
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

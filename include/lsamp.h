@@ -233,6 +233,17 @@ void lsamp_context_destroy(lsamp_context* ctx);
 /* Enqueue one sampling step on `stream`. */
 lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* args, void* stream);
 
+/* Per-kernel timing hook, off by default (the role CBv2StepProfiler plays for
+ * the reference, StepProfilerV2.swift:15-60).  While enabled, each
+ * lsamp_sample call that is not under graph capture records three HIP events
+ * on its stream: before the stats kernel, between the two kernels, after the
+ * select kernel (up to 4096 calls).  lsamp_context_read_timing waits for them,
+ * returns the summed milliseconds per kernel and the number of timed calls,
+ * and starts a new window. */
+lsamp_status lsamp_context_set_timing(lsamp_context* ctx, int32_t enable);
+lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, double* select_ms,
+                                       int64_t* calls);
+
 /* Enqueue one MTP verification on `stream`. */
 lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* args, void* stream);
 

@@ -59,6 +59,11 @@ struct lsamp_context {
   Workspace ws;
   void* block;  // single device allocation backing the workspace
   size_t bytes;
+  // timing hook
+  static constexpr int kTimedCalls = 4096;
+  bool timing = false;
+  int timed = 0;
+  hipEvent_t* events = nullptr;  // [kTimedCalls * 3]
 };
 
 namespace {
@@ -192,8 +197,53 @@ void lsamp_context_destroy(lsamp_context* ctx) {
     DeviceGuard guard(ctx->device);
     (void)hipDeviceSynchronize();
     (void)hipFree(ctx->block);
+    if (ctx->events) {
+      for (int i = 0; i < lsamp_context::kTimedCalls * 3; ++i) (void)hipEventDestroy(ctx->events[i]);
+      delete[] ctx->events;
+    }
   }
   delete ctx;
+}
+
+lsamp_status lsamp_context_set_timing(lsamp_context* ctx, int32_t enable) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  DeviceGuard guard(ctx->device);
+  if (enable && !ctx->events) {
+    ctx->events = new hipEvent_t[lsamp_context::kTimedCalls * 3];
+    for (int i = 0; i < lsamp_context::kTimedCalls * 3; ++i) {
+      if (hipEventCreate(&ctx->events[i]) != hipSuccess) {
+        for (int j = 0; j < i; ++j) (void)hipEventDestroy(ctx->events[j]);
+        delete[] ctx->events;
+        ctx->events = nullptr;
+        return fail(LSAMP_ERR_DEVICE, "hipEventCreate failed");
+      }
+    }
+  }
+  ctx->timing = enable != 0;
+  ctx->timed = 0;
+  return ok();
+}
+
+lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, double* select_ms,
+                                       int64_t* calls) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  DeviceGuard guard(ctx->device);
+  double a = 0.0, b = 0.0;
+  for (int i = 0; i < ctx->timed; ++i) {
+    hipEvent_t* e = ctx->events + 3 * i;
+    if (hipEventSynchronize(e[2]) != hipSuccess) return fail(LSAMP_ERR_DEVICE, "hipEventSynchronize failed");
+    float t01 = 0.0f, t12 = 0.0f;
+    if (hipEventElapsedTime(&t01, e[0], e[1]) != hipSuccess ||
+        hipEventElapsedTime(&t12, e[1], e[2]) != hipSuccess)
+      return fail(LSAMP_ERR_DEVICE, "hipEventElapsedTime failed");
+    a += t01;
+    b += t12;
+  }
+  if (stats_ms) *stats_ms = a;
+  if (select_ms) *select_ms = b;
+  if (calls) *calls = ctx->timed;
+  ctx->timed = 0;
+  return ok();
 }
 
 lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* stream) {
@@ -255,7 +305,16 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
   P.keep = a->keep;
   P.stats = a->stats;
   DeviceGuard guard(ctx->device);
-  const int err = launch_sample(ctx->ws, P, stream);
+  void* const* ev = nullptr;
+  if (ctx->timing && ctx->timed < lsamp_context::kTimedCalls) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &cs) == hipSuccess &&
+        cs == hipStreamCaptureStatusNone) {
+      ev = reinterpret_cast<void* const*>(ctx->events + 3 * ctx->timed);
+      ++ctx->timed;
+    }
+  }
+  const int err = launch_sample(ctx->ws, P, stream, ev);
   if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                             hipGetErrorString((hipError_t)err));
   return ok();

@@ -305,11 +305,44 @@ __device__ __forceinline__ T block_excl_scan(T v, T* scratch, T* total) {
   return off + incl - v;
 }
 
-// Device-coherent load of data another work-group published before its
-// release fence (bypasses non-coherent caches).
+// Cross-work-group hand-off without fences.  An agent-scope fence on CDNA
+// lowers to a walk of the whole L2 (write-back on release, invalidate on
+// acquire), which serializes per XCD when hundreds of work-groups issue it.
+// Instead, data another work-group will read is written with agent-scope
+// relaxed atomic stores (write-through to the device coherence point), each
+// wave waits for its stores to complete before the work-group barrier, the
+// arrival counter is a returning agent-scope atomic, and the last arriver
+// reads with agent-scope relaxed atomic loads (served from the coherence
+// point, never from a stale L2 line).
 template <typename T>
 __device__ __forceinline__ T ld_coherent(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void st_coherent(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent_f32(float* p, float v) {
+  st_coherent(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+__device__ __forceinline__ void st_coherent_f64(double* p, double v) {
+  st_coherent(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v));
+}
+// Wait until every memory operation this wave issued has completed.
+__device__ __forceinline__ void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Arrival on a per-row counter; true in every thread of the last arriver.
+// `flag` is an LDS int.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, int* flag) {
+  drain_memory();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = prev == expected - 1u;
+  }
+  __syncthreads();
+  return *flag != 0;
 }
 
 }  // namespace dev

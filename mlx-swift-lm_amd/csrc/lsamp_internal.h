@@ -139,7 +139,9 @@ struct SamplePlan {
 };
 
 // Kernel launchers (lsamp_kernels.hip).  Return a hipError_t as int.
-int launch_sample(const Workspace& ws, const SamplePlan& plan, void* stream);
+// `events` (3 hipEvent_t or NULL) are recorded before, between and after the
+// two kernels.
+int launch_sample(const Workspace& ws, const SamplePlan& plan, void* stream, void* const* events);
 int launch_verify_residual(const Workspace& ws, const lsamp_verify_args& va, int32_t slices,
                            int32_t slice_len, int32_t nchunks, int32_t aligned, void* stream);
 int launch_verify_gather(const Workspace& ws, const lsamp_verify_args& va, int32_t nchunks,

@@ -385,22 +385,14 @@ __global__ __launch_bounds__(kThreads) void k_stats(Workspace ws, SamplePlan P) 
   __syncthreads();
   SliceSummary* S = ws.summaries + ((size_t)row * kMaxSlices + slice);
   if (tid == 0) {
-    S->x_max = xmax;
-    S->top_bin = top;
-    S->flags = sflags;
-    S->n_finite = nfin;
+    st_coherent_f32(&S->x_max, xmax);
+    st_coherent(&S->top_bin, top);
+    st_coherent(&S->flags, sflags);
+    st_coherent(&S->n_finite, nfin);
   }
   if (want_hist)
-    for (int i = tid; i < kHist; i += kThreads) S->hist[i] = s_hist[i];
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(&ws.arrive_stats[row], 1u);
-    s_last = prev == (uint32_t)(P.slices - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+    for (int i = tid; i < kHist; i += kThreads) st_coherent(&S->hist[i], s_hist[i]);
+  if (!arrive_last(&ws.arrive_stats[row], (uint32_t)P.slices, &s_last)) return;
 
   // 7. last arriver: merge the row
   const int G = P.slices;
@@ -662,11 +654,15 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
 #pragma unroll
         for (int q = 0; q < N; ++q) {
           cy[q] = 0.0f;
-          if (kout && ((valid & ~pen) >> q & 1u)) kout[i0 + q] = 0;
-          if ((ex >> q) & 1u) continue;
+          // keep bytes of candidates are written by the finalize alone (one
+          // writer per byte: plain stores from different XCDs have no order)
+          if ((ex >> q) & 1u) {
+            if (kout && ((valid & ~pen) >> q & 1u)) kout[i0 + q] = 0;
+            continue;
+          }
           const float x = vec_elem<DT>(raw, q);
           const int cls = classify(info, c, x);
-          if (kout && cls == kKept) kout[i0 + q] = 1;
+          if (kout && cls != kCand) kout[i0 + q] = cls == kKept ? 1 : 0;
           if (cls == kKept) {
             const float y = to_filter(c, x);
             const uint64_t w = weight(y, y_max, c.scale);
@@ -713,7 +709,7 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
       const float x = L.a.ex[j2];
       const int cls = classify(info, c, x);
       const int32_t t = L.a.etok[j2];
-      if (P.keep) P.keep[(size_t)row * (size_t)V + t] = cls == kKept ? 1 : 0;
+      if (P.keep && cls != kCand) P.keep[(size_t)row * (size_t)V + t] = cls == kKept ? 1 : 0;
       if (cls == kKept) {
         const float y = to_filter(c, x);
         const uint64_t w = weight(y, y_max, c.scale);
@@ -739,33 +735,30 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
   const int64_t chunk0 = base / kChunk;
   const int nch = (int)((end - base + kChunk - 1) / kChunk);
   uint64_t* rowchunks = ws.chunk_w + (size_t)row * (size_t)ws.max_chunks;
-  for (int i = tid; i < nch; i += kThreads) rowchunks[chunk0 + i] = L.a.chunk[i];
+  for (int i = tid; i < nch; i += kThreads) st_coherent(&rowchunks[chunk0 + i], L.a.chunk[i]);
   const int ncand = s_ncand;
-  if (tid == 0) s_misc[0] = ncand > 0 ? (int)atomicAdd(&ws.cand_count[row], (uint32_t)ncand) : 0;
+  if (tid == 0)
+    s_misc[0] = ncand > 0 ? (int)__hip_atomic_fetch_add(&ws.cand_count[row], (uint32_t)ncand,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : 0;
   __syncthreads();
   const int gbase = s_misc[0];
   const int ncopy = ncand < kWgCandCap ? ncand : kWgCandCap;
   Candidate* rc = ws.cands + (size_t)row * kCandCap;
   for (int i = tid; i < ncopy; i += kThreads)
-    if (gbase + i < kCandCap) rc[gbase + i] = L.a.wcand[i];
+    if (gbase + i < kCandCap) {
+      st_coherent_f32(&rc[gbase + i].y, L.a.wcand[i].y);
+      st_coherent(&rc[gbase + i].id, L.a.wcand[i].id);
+    }
   if (tid == 0) {
-    SelectPartial sp;
-    sp.ent = ent;
-    sp.min_kept = min_kept;
-    sp.n_kept = n_kept;
-    sp.n_cand = ncand;
-    sp.pad = ent_overflow ? 1 : 0;
-    ws.partials[(size_t)row * kMaxSlices + slice] = sp;
+    SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + slice;
+    st_coherent_f64(&sp->ent, ent);
+    st_coherent_f32(&sp->min_kept, min_kept);
+    st_coherent(&sp->n_kept, n_kept);
+    st_coherent(&sp->n_cand, ncand);
+    st_coherent(&sp->pad, ent_overflow ? 1 : 0);
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(&ws.arrive_select[row], 1u);
-    s_last = prev == (uint32_t)(P.slices - 1);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+  if (!arrive_last(&ws.arrive_select[row], (uint32_t)P.slices, &s_last)) return;
 
   // ------------------------------------------------------------ finalize
   const int G = P.slices;
@@ -939,7 +932,12 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
       rc[kexcl].y = y;
       rc[kexcl].id = id;
       ++kexcl;
-      if (P.keep) P.keep[(size_t)row * (size_t)V + id] = 1;
+    }
+    if (P.keep) {
+      for (int r = tid; r < nc; r += kThreads) {
+        const int32_t id = (int32_t)(0xffffffffu - (uint32_t)(L.b.keys[r] & 0xffffffffull));
+        P.keep[(size_t)row * (size_t)V + id] = L.b.keep[r];
+      }
     }
   }
 
@@ -1089,24 +1087,32 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
 
 }  // namespace
 
-int launch_sample(const Workspace& ws, const SamplePlan& P, void* stream) {
+int launch_sample(const Workspace& ws, const SamplePlan& P, void* stream, void* const* events) {
   const dim3 grid((unsigned)P.slices, (unsigned)P.rows);
   const dim3 block(kThreads);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  auto mark = [&](int i) {
+    if (events) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), st);
+  };
+  mark(0);
   switch (P.dtype) {
     case LSAMP_DTYPE_F32:
       hipLaunchKernelGGL(k_stats<LSAMP_DTYPE_F32>, grid, block, 0, st, ws, P);
+      mark(1);
       hipLaunchKernelGGL(k_select<LSAMP_DTYPE_F32>, grid, block, 0, st, ws, P);
       break;
     case LSAMP_DTYPE_BF16:
       hipLaunchKernelGGL(k_stats<LSAMP_DTYPE_BF16>, grid, block, 0, st, ws, P);
+      mark(1);
       hipLaunchKernelGGL(k_select<LSAMP_DTYPE_BF16>, grid, block, 0, st, ws, P);
       break;
     default:
       hipLaunchKernelGGL(k_stats<LSAMP_DTYPE_F16>, grid, block, 0, st, ws, P);
+      mark(1);
       hipLaunchKernelGGL(k_select<LSAMP_DTYPE_F16>, grid, block, 0, st, ws, P);
       break;
   }
+  mark(2);
   return (int)hipGetLastError();
 }
 

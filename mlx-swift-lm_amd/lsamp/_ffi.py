@@ -173,6 +173,11 @@ def load_library(path: str | None = None):
     lib.lsamp_context_destroy.restype = None
     lib.lsamp_sample.argtypes = [c_void_p, POINTER(SampleArgs), c_void_p]
     lib.lsamp_sample.restype = c_int32
+    lib.lsamp_context_set_timing.argtypes = [c_void_p, c_int32]
+    lib.lsamp_context_set_timing.restype = c_int32
+    lib.lsamp_context_read_timing.argtypes = [c_void_p, POINTER(c_double), POINTER(c_double),
+                                              POINTER(c_int64)]
+    lib.lsamp_context_read_timing.restype = c_int32
     lib.lsamp_verify.argtypes = [c_void_p, POINTER(VerifyArgs), c_void_p]
     lib.lsamp_verify.restype = c_int32
     lib.lsamp_resolve_generate_parameters.argtypes = [

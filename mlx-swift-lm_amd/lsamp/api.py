@@ -84,6 +84,18 @@ class Context:
         except Exception:
             pass
 
+    # ----------------------------------------------------------------- timing
+    def set_timing(self, enable: bool) -> None:
+        _ffi.check(self.lib.lsamp_context_set_timing(self.handle, 1 if enable else 0),
+                   "lsamp_context_set_timing")
+
+    def read_timing(self):
+        """(stats kernel ms, select kernel ms, timed calls) since the last read."""
+        a, b, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
+        _ffi.check(self.lib.lsamp_context_read_timing(self.handle, ctypes.byref(a), ctypes.byref(b),
+                                                      ctypes.byref(n)), "lsamp_context_read_timing")
+        return a.value, b.value, n.value
+
     # ----------------------------------------------------------------- sample
     def prepare_sample(self, logits: torch.Tensor, params, *, semantics: int, vocab: Optional[int] = None,
                        row_ptr=None, entries=None, bitmask=None, mask_bits: Optional[int] = None,
