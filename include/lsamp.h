@@ -244,6 +244,23 @@ lsamp_status lsamp_context_set_timing(lsamp_context* ctx, int32_t enable);
 lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, double* select_ms,
                                        int64_t* calls);
 
+/* Kernel arrangement.  AUTO (default) runs one kernel whose grid fits on the
+ * device at once (the slices of a row hand their results to each other while
+ * the logits stay in registers); SPLIT runs two kernels with no co-residency
+ * requirement (the second re-reads each slice from L2).  Both give identical
+ * results. */
+#define LSAMP_MODE_AUTO 0
+#define LSAMP_MODE_FUSED 1
+#define LSAMP_MODE_SPLIT 2
+lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode);
+
+/* Sticky device-side status bits raised since the last read (waits for the
+ * device); clears them.  LSAMP_STATUS_SPIN_TIMEOUT: a fused step could not
+ * gather all slices of a row (another workload held the CUs); that step's
+ * outputs are unreliable. */
+#define LSAMP_STATUS_SPIN_TIMEOUT 1u
+lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
+
 /* Enqueue one MTP verification on `stream`. */
 lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* args, void* stream);
 

@@ -49,13 +49,13 @@ struct DeviceGuard {
   }
 };
 
-constexpr int32_t kMaxVocab = kMaxSlices * kMaxSliceLen;  // 524288
-
 }  // namespace
 
 struct lsamp_context {
   int32_t device;
   int32_t cus;
+  int32_t mode = LSAMP_MODE_AUTO;
+  int32_t blocks_per_cu[3] = {0, 0, 0};  // fused-kernel occupancy per dtype
   Workspace ws;
   void* block;  // single device allocation backing the workspace
   size_t bytes;
@@ -70,13 +70,13 @@ namespace {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Number of slices per row: enough work-groups to cover every CU twice,
-// slices of whole 1024-token chunks, at most kMaxSliceLen tokens each.
-void plan_slices(int32_t rows, int32_t vocab, int32_t cus, int32_t* slices, int32_t* slice_len,
+// Number of slices per row: about one work-group per resident slot of the
+// device, slices of whole 1024-token chunks, at most kMaxSliceLen tokens each.
+void plan_slices(int32_t rows, int32_t vocab, int32_t slots, int32_t* slices, int32_t* slice_len,
                  int32_t* nchunks) {
   const int32_t nch = (vocab + kChunk - 1) / kChunk;
   const int32_t g_min = (vocab + kMaxSliceLen - 1) / kMaxSliceLen;
-  int32_t target = 2 * (cus > 0 ? cus : 256);
+  int32_t target = slots > 0 ? slots : 256;
   int32_t g = (target + rows - 1) / rows;
   if (g < g_min) g = g_min;
   if (g > kMaxSlices) g = kMaxSlices;
@@ -138,7 +138,9 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   const size_t o_rows = take(R * sizeof(RowInfo));
   const size_t o_chunk = take(R * chunks * sizeof(uint64_t));
   const size_t o_cand = take(R * kCandCap * sizeof(Candidate));
+  const size_t o_klist = take(R * kMaxSlices * kKeptCap * sizeof(KeptItem));
   const size_t o_part = take(R * kMaxSlices * sizeof(SelectPartial));
+  const size_t o_status = take(sizeof(uint32_t));
   const size_t o_cc = take(R * sizeof(uint32_t));
   const size_t o_as = take(R * sizeof(uint32_t));
   const size_t o_asel = take(R * sizeof(uint32_t));
@@ -164,6 +166,7 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   lsamp_context* ctx = new lsamp_context();
   ctx->device = device;
   ctx->cus = prop.multiProcessorCount;
+  for (int dt = 0; dt < 3; ++dt) ctx->blocks_per_cu[dt] = fused_blocks_per_cu(dt);
   ctx->block = block;
   ctx->bytes = total;
   char* b = reinterpret_cast<char*>(block);
@@ -175,6 +178,8 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   ws.rows = reinterpret_cast<RowInfo*>(b + o_rows);
   ws.chunk_w = reinterpret_cast<uint64_t*>(b + o_chunk);
   ws.cands = reinterpret_cast<Candidate*>(b + o_cand);
+  ws.klist = reinterpret_cast<KeptItem*>(b + o_klist);
+  ws.status = reinterpret_cast<uint32_t*>(b + o_status);
   ws.partials = reinterpret_cast<SelectPartial*>(b + o_part);
   ws.cand_count = reinterpret_cast<uint32_t*>(b + o_cc);
   ws.arrive_stats = reinterpret_cast<uint32_t*>(b + o_as);
@@ -203,6 +208,26 @@ void lsamp_context_destroy(lsamp_context* ctx) {
     }
   }
   delete ctx;
+}
+
+lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (mode != LSAMP_MODE_AUTO && mode != LSAMP_MODE_FUSED && mode != LSAMP_MODE_SPLIT)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown mode %d", mode);
+  ctx->mode = mode;
+  return ok();
+}
+
+lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits) {
+  if (!ctx || !bits) return fail(LSAMP_ERR_INVALID_ARGUMENT, "NULL argument");
+  DeviceGuard guard(ctx->device);
+  uint32_t v = 0, zero = 0;
+  if (hipDeviceSynchronize() != hipSuccess ||
+      hipMemcpy(&v, ctx->ws.status, sizeof v, hipMemcpyDeviceToHost) != hipSuccess ||
+      hipMemcpy(ctx->ws.status, &zero, sizeof zero, hipMemcpyHostToDevice) != hipSuccess)
+    return fail(LSAMP_ERR_DEVICE, "reading the device status failed");
+  *bits = v;
+  return ok();
 }
 
 lsamp_status lsamp_context_set_timing(lsamp_context* ctx, int32_t enable) {
@@ -283,7 +308,11 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
   P.vocab = a->vocab;
   P.dtype = a->dtype;
   P.row_stride = a->row_stride;
-  plan_slices(a->rows, a->vocab, ctx->cus, &P.slices, &P.slice_len, &P.nchunks);
+  const int32_t bpc = ctx->blocks_per_cu[a->dtype];
+  const int32_t slots = ctx->cus * (bpc > 0 ? bpc : 1);
+  plan_slices(a->rows, a->vocab, slots, &P.slices, &P.slice_len, &P.nchunks);
+  P.fused = ctx->mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;
+  P.rows_per_round = P.fused ? slots / P.slices : a->rows;
   const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
   P.aligned = aligned16(a->logits) && ((size_t)a->row_stride * es) % 16 == 0;
   P.logits = a->logits;

@@ -43,6 +43,28 @@ __device__ __forceinline__ float vec_elem(const uint4& r, int k) {
   }
 }
 
+// Replace the elements of a 16-byte vector whose bit is set in `excl` by -inf
+// (branch-free: one mask per 32-bit word).
+template <int DT>
+__device__ __forceinline__ void exclude_elems(uint4& r, uint32_t excl) {
+  uint32_t* w = reinterpret_cast<uint32_t*>(&r);
+  if constexpr (DT == LSAMP_DTYPE_F32) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t m = 0u - ((excl >> k) & 1u);
+      w[k] = (w[k] & ~m) | (Vec<DT>::NEG_INF_BITS & m);
+    }
+  } else {
+    constexpr uint32_t pair = Vec<DT>::NEG_INF_BITS * 0x10001u;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t m = ((0u - ((excl >> (2 * k)) & 1u)) & 0xffffu) |
+                         ((0u - ((excl >> (2 * k + 1)) & 1u)) & 0xffff0000u);
+      w[k] = (w[k] & ~m) | (pair & m);
+    }
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ float load_scalar(const void* row, int64_t i) {
   if constexpr (DT == LSAMP_DTYPE_F32) {

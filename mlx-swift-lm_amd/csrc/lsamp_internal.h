@@ -8,26 +8,33 @@
 
 namespace lsamp {
 
-// Work-group shape.  One work-group owns one slice of one row.
-constexpr int kThreads = 512;            // 8 wave64s
+// Work-group shape: one 512-thread work-group (8 wave64s, up to 256 VGPRs per
+// lane) owns one slice of one row and holds the slice's logits in registers,
+// 80 per thread at most (10 bf16 or 20 fp32 16-byte vectors).
+constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kElemsPerThread = 64;      // register budget per thread (logits)
-constexpr int kMaxSliceLen = kThreads * kElemsPerThread;  // 32768 tokens
-constexpr int kChunk = 1024;             // draw granularity (tokens)
-constexpr int kMaxSlices = 16;           // slices per row
+constexpr int kElemsPerThread = 80;
+constexpr int kMaxSliceLen = kThreads * kElemsPerThread;  // 40960 tokens
+constexpr int kChunk = 1024;                              // draw granularity (tokens)
+constexpr int kMaxSlices = 12;                            // slices per row
+constexpr int kMaxVocab = kMaxSlices * kMaxSliceLen;      // 491520
+constexpr int kMaxRowChunks = kMaxVocab / kChunk;         // 480 <= one per thread
+constexpr int kSliceChunks = kMaxSliceLen / kChunk;       // 40
 // Histogram: bins of 1/32 nat of the filter-space logit, kBins of them below
 // the slice's top bin (a 32-nat window), plus one tail bin for the rest.
-constexpr int kBinScale = 32;
 constexpr int kBins = 1024;
-constexpr int kTail = kBins;             // index of the tail bin
+constexpr int kTail = kBins;
 constexpr int kHist = kBins + 1;
-// Packed histogram word: count in bits 46..63, fixed-point mass in 0..45.
+// Packed histogram word of a slice: count in bits 46..63, fixed-point mass in
+// 0..45 (mass = sum exp(q - bin edge) * 2^30 < 2^46 for <= 40960 tokens).
 constexpr int kCountShift = 46;
 constexpr uint64_t kMassMask = (1ull << kCountShift) - 1;
-constexpr int kMassFracBits = 30;        // mass = sum(exp(q - edge)) * 2^30
+constexpr int kMassFracBits = 30;
 // Candidates (tokens in the cut bin) per row, and per work-group in LDS.
 constexpr int kCandCap = 4096;
 constexpr int kWgCandCap = 2048;
+// Kept tokens listed per slice (fast draw path); beyond this the draw scans.
+constexpr int kKeptCap = 256;
 // Penalty entries handled per slice (LDS).
 constexpr int kSliceEntryCap = 2048;
 // Fixed-point draw weights: 2^40 * dexp(d).
@@ -42,40 +49,44 @@ constexpr int32_t kModeNormal = 0;
 constexpr int32_t kModeEmpty = 1;   // every logit masked / NaN
 constexpr int32_t kModePosInf = 2;  // +inf logits present: keep exactly those
 
-// Per-slice summary written by the stats kernel.
-struct SliceSummary {
-  float x_max;         // largest finite transformed logit (pre-temperature)
-  int32_t top_bin;     // bin of x_max
-  uint32_t flags;      // LSAMP_ROW_NONFINITE | kSliceOverflow | kSlicePosInf
-  int32_t n_finite;    // tokens with a finite transformed logit
-  uint64_t hist[kHist];
-};
+// Slice flags.
 constexpr uint32_t kSlicePosInf = 0x100u;
 constexpr uint32_t kSliceEntryOverflow = 0x200u;
 
-// Per-row decision written by the last stats work-group of the row.
+// Per-slice summary written by the stats phase.
+struct SliceSummary {
+  float x_max;       // largest finite transformed logit (pre-temperature)
+  int32_t top_bin;   // bin of x_max
+  uint32_t flags;    // LSAMP_ROW_NONFINITE | kSlice*
+  int32_t n_finite;  // tokens with a finite transformed logit
+  uint64_t hist[kHist];
+};
+
+// Per-row decision of the stats merge.
 struct RowInfo {
-  float x_max;       // row max (pre-temperature space)
-  float q_top;       // s_max / 32: fast filter-space max used by the masses
-  int32_t top_bin;   // absolute bin of x_max
-  int32_t cut;       // kCut* or bin index relative to top_bin
-  int32_t mode;      // kMode*
-  uint32_t flags;    // LSAMP_ROW_* accumulated so far
+  float x_max;          // row max (pre-temperature space)
+  float q_top;          // fast filter-space max that the masses are relative to
+  int32_t top_bin;      // absolute bin of x_max
+  int32_t cut;          // kCut* or bin index relative to top_bin
+  int32_t mode;         // kMode*
+  uint32_t flags;       // LSAMP_ROW_* accumulated so far
   int32_t count_above;  // tokens in bins above the cut
   int32_t n_finite;
   double mass_above;    // sum exp(q - q_top) of bins above the cut
   double z;             // sum exp(q - q_top) over every finite token
-  double p_limit;       // top_p * z (top-p comparison bound), < 0 if off
-  float t_min_p;        // min-p threshold in filter space (-inf if off)
+  double p_limit;       // top-p comparison bound (top_p * z), < 0 if off
   int32_t kept_cands;   // select finalize: kept candidates, listed first in cands[row]
+  int32_t pad;
 };
 
-// Per-slice partial results of the select kernel.
+// Per-slice partial results of the select phase.
 struct SelectPartial {
-  double ent;       // sum over kept tokens of e * d (entropy numerator)
-  float min_kept;   // smallest kept filter-space logit
+  double ent;        // sum over kept tokens of e * d (entropy numerator)
+  float min_kept;    // smallest kept filter-space logit
   int32_t n_kept;
-  int32_t n_cand;   // candidates this slice produced (for overflow)
+  int32_t n_cand;    // candidates this slice produced
+  int32_t n_list;    // kept tokens listed (> kKeptCap: list incomplete)
+  int32_t overflow;  // entry-table overflow in this slice
   int32_t pad;
 };
 
@@ -84,28 +95,42 @@ struct Candidate {
   int32_t id;  // token id
 };
 
+struct KeptItem {
+  uint64_t w;  // fixed-point draw weight
+  int32_t id;
+  int32_t pad;
+};
+
+static_assert(kMaxRowChunks <= kThreads, "the draw keeps one chunk per thread");
+static_assert(kBins == 2 * kThreads, "the merge keeps two bins per thread");
+
 struct Workspace {
   int32_t max_rows;
   int32_t max_vocab;
   int32_t max_chunks;
-  SliceSummary* summaries;   // [max_rows][kMaxSlices]
-  RowInfo* rows;             // [max_rows]
-  uint64_t* chunk_w;         // [max_rows][max_chunks]
-  Candidate* cands;          // [max_rows][kCandCap]
-  SelectPartial* partials;   // [max_rows][kMaxSlices]
-  uint32_t* cand_count;      // [max_rows]
-  uint32_t* arrive_stats;    // [max_rows]
-  uint32_t* arrive_select;   // [max_rows]
+  SliceSummary* summaries;  // [max_rows][kMaxSlices]
+  RowInfo* rows;            // [max_rows]
+  uint64_t* chunk_w;        // [max_rows][max_chunks]
+  Candidate* cands;         // [max_rows][kCandCap]
+  KeptItem* klist;          // [max_rows][kMaxSlices][kKeptCap]
+  SelectPartial* partials;  // [max_rows][kMaxSlices]
+  uint32_t* cand_count;     // [max_rows]
+  uint32_t* arrive_stats;   // [max_rows]
+  uint32_t* arrive_select;  // [max_rows]
+  uint32_t* status;         // [1] sticky error bits (kStatus*)
   // MTP verification scratch
-  lsamp_row_stats* vstats;   // [max_rows]
-  int32_t* vtokens;          // [max_rows]
-  uint32_t* vflags;          // [max_rows]
-  int32_t* vprobe;           // [max_rows]
-  float* vuniform;           // [max_rows]
-  lsamp_row_params* vparams; // [max_rows]
-  uint64_t* vres_chunk;      // [max_rows][max_chunks] residual chunk sums
-  uint32_t* arrive_resid;    // [max_rows]
+  lsamp_row_stats* vstats;    // [max_rows]
+  int32_t* vtokens;           // [max_rows]
+  uint32_t* vflags;           // [max_rows]
+  int32_t* vprobe;            // [max_rows]
+  float* vuniform;            // [max_rows]
+  lsamp_row_params* vparams;  // [max_rows]
+  uint64_t* vres_chunk;       // [max_rows][max_chunks] residual chunk sums
+  uint32_t* arrive_resid;     // [max_rows]
 };
+
+// Sticky device status bits.
+constexpr uint32_t kStatusSpinTimeout = 1u;  // a fused-kernel barrier wait timed out
 
 // Launch description resolved on the host.
 struct SamplePlan {
@@ -114,12 +139,14 @@ struct SamplePlan {
   int32_t vocab;
   int32_t dtype;
   int64_t row_stride;
-  int32_t slices;        // G
-  int32_t slice_len;     // tokens per slice (multiple of kChunk)
+  int32_t slices;          // G
+  int32_t slice_len;       // tokens per slice (multiple of kChunk)
   int32_t nchunks;
-  int32_t aligned;       // 16-byte vector loads allowed
+  int32_t aligned;         // 16-byte vector loads allowed
+  int32_t fused;           // one co-resident kernel (1) or two kernels (0)
+  int32_t rows_per_round;  // fused: rows processed per round of the grid
   const void* logits;
-  const void* logits2;   // rows >= rows_split read logits2 (MTP draft rows)
+  const void* logits2;     // rows >= rows_split read logits2 (MTP draft rows)
   int32_t rows_split;
   const lsamp_row_params* params;
   const int32_t* row_ptr;
@@ -139,12 +166,10 @@ struct SamplePlan {
 };
 
 // Kernel launchers (lsamp_kernels.hip).  Return a hipError_t as int.
-// `events` (3 hipEvent_t or NULL) are recorded before, between and after the
-// two kernels.
+// `events` (3 hipEvent_t or NULL) bracket the step: before, between the two
+// kernels (split mode; same as before in fused mode), after.
 int launch_sample(const Workspace& ws, const SamplePlan& plan, void* stream, void* const* events);
-int launch_verify_residual(const Workspace& ws, const lsamp_verify_args& va, int32_t slices,
-                           int32_t slice_len, int32_t nchunks, int32_t aligned, void* stream);
-int launch_verify_gather(const Workspace& ws, const lsamp_verify_args& va, int32_t nchunks,
-                         void* stream);
+// Work-groups of the fused kernel that fit on one CU (occupancy query).
+int fused_blocks_per_cu(int dtype);
 
 }  // namespace lsamp

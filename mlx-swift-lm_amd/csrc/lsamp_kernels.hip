@@ -1,26 +1,29 @@
 // lsamp_kernels.hip — gfx950 kernels of the logits-to-token stage.
 //
-// One sampling step is two launches over a (slices, rows) grid of 512-thread
-// work-groups; each work-group owns one slice (<= 32768 tokens) of one row.
+// A sampling step runs over tasks (row, slice): one 512-thread work-group
+// owns one slice (<= 40960 tokens) of one row and keeps the slice's logits in
+// registers from the moment they arrive from HBM until the token is drawn.
 //
-//  k_stats   reads its slice of logits once from HBM (16-byte vector loads),
-//            applies the grammar mask and the sparse penalties exactly as the
-//            reference orders them, and builds a histogram of the filter-space
-//            logit in 1/32-nat bins (count + fixed-point mass, one packed
-//            64-bit LDS atomic per token).  The last work-group of the row to
-//            finish merges the slices' histograms and locates the bin that
-//            holds the top-k / top-p / min-p cut.
-//  k_select  re-reads its slice (L2-resident: same XCD as k_stats), keeps the
-//            tokens above the cut bin (fixed-point draw weight per 1024-token
-//            chunk) and lists the tokens inside it.  The last work-group of
-//            the row sorts those candidates, applies the exact keep rule of
-//            the row's semantics, and draws the token by inverse CDF in
-//            token-id order: chunk prefix sums, then one 1024-token scan.
+//  stats phase   16-byte vector loads of the slice, the grammar mask and the
+//                sparse penalties applied exactly as the reference orders
+//                them, then a histogram of the filter-space logit in 1/32-nat
+//                bins (count + fixed-point mass, one packed 64-bit LDS atomic
+//                per token).  The last work-group of the row merges the
+//                slices' histograms and locates the bin holding the
+//                top-k / top-p / min-p cut.
+//  select phase  every work-group keeps the tokens above the cut bin (fixed-
+//                point draw weight per 1024-token chunk, and a short list of
+//                them) and lists the tokens inside it.  The last work-group of
+//                the row sorts those candidates, applies the exact keep rule of
+//                the row's semantics and draws the token by inverse CDF in
+//                token-id order.
 //
-// Neither kernel waits on another work-group: cross-work-group results are
-// published before an atomic arrival counter and only the last arriver reads
-// them, so no launch shape can deadlock.  MFMA is not used: the stage is a
-// bandwidth- and reduction-bound pass, not a contraction.
+// Fused mode runs both phases in one kernel whose grid fits on the device at
+// once: the slices of a row wait for the merge on a bounded spin (a wait that
+// runs out sets a status bit and the work-group carries on, so the grid always
+// drains).  Split mode runs the phases as two kernels, the second re-reading
+// its slice from L2; it needs no co-residency.  Neither mode uses MFMA: the
+// stage is a bandwidth- and reduction-bound pass, not a contraction.
 #include <hip/hip_runtime.h>
 
 #include "lsamp_device.h"
@@ -32,9 +35,11 @@ namespace {
 using namespace dev;
 
 constexpr int kSliceWords = kMaxSliceLen / 32;       // penalty bitmap words
-constexpr int kSliceChunks = kMaxSliceLen / kChunk;  // chunks per slice
-constexpr int kMaxRowChunks = kMaxSlices * kSliceChunks;
 constexpr int kFinalPerThread = kCandCap / kThreads;  // sorted candidates per thread
+constexpr uint32_t kReady = 1u << 16;                 // merge-done bias on arrive_stats
+constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
+
+enum TaskMode { kFused = 0, kStatsOnly = 1, kSelectOnly = 2 };
 
 // ------------------------------------------------------------ row context
 struct RowCtx {
@@ -108,30 +113,26 @@ __device__ __forceinline__ float patch_value(const RowCtx& c, const lsamp_row_pa
   return x;
 }
 
-// Allowed bits (1 = allowed) of the N tokens starting at i0.
+// Allowed bits (1 = allowed) of the N tokens starting at i0, N <= 32 and i0 a
+// multiple of N with N a power of two, so the N bits lie in one mask word.
+// Tokens at or past mask_bits, or in words past mask_words, follow `tail`.
 __device__ __forceinline__ uint32_t mask_allow_bits(const uint32_t* mrow, int32_t mask_words,
-                                                    int32_t mask_bits, int32_t tail, int64_t i0,
+                                                    int32_t mask_bits, int32_t tail, int32_t i0,
                                                     int N) {
   const uint32_t full = (N == 32) ? 0xffffffffu : ((1u << N) - 1u);
   if (!mrow) return full;
-  if (i0 + N <= mask_bits && (i0 >> 5) < mask_words) {
-    return (mrow[i0 >> 5] >> (uint32_t)(i0 & 31)) & full;
-  }
-  uint32_t bits = 0;
-  for (int q = 0; q < N; ++q) {
-    const int64_t i = i0 + q;
-    uint32_t a;
-    if (i >= mask_bits || (i >> 5) >= mask_words)
-      a = tail == LSAMP_MASK_TAIL_KEEP ? 1u : 0u;
-    else
-      a = (mrow[i >> 5] >> (uint32_t)(i & 31)) & 1u;
-    bits |= a << q;
-  }
-  return bits;
+  const int32_t wi = i0 >> 5;
+  const bool word_in = wi < mask_words;
+  const uint32_t word = word_in ? mrow[wi] : 0u;
+  int32_t nin = word_in ? mask_bits - i0 : 0;  // leading positions the mask covers
+  nin = nin < 0 ? 0 : (nin > N ? N : nin);
+  const uint32_t in_mask = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
+  const uint32_t bits = (word >> (uint32_t)(i0 & 31)) & in_mask;
+  return (bits | (tail == LSAMP_MASK_TAIL_KEEP ? (full & ~in_mask) : 0u)) & full;
 }
 
 __device__ __forceinline__ bool mask_allows(const uint32_t* mrow, int32_t mask_words,
-                                            int32_t mask_bits, int32_t tail, int64_t i) {
+                                            int32_t mask_bits, int32_t tail, int32_t i) {
   return mask_allow_bits(mrow, mask_words, mask_bits, tail, i, 1) != 0u;
 }
 
@@ -147,6 +148,26 @@ __device__ __forceinline__ float load_logit(int dt, const char* rowp, int64_t i)
   if (dt == LSAMP_DTYPE_F32) return load_scalar<LSAMP_DTYPE_F32>(rowp, i);
   if (dt == LSAMP_DTYPE_BF16) return load_scalar<LSAMP_DTYPE_BF16>(rowp, i);
   return load_scalar<LSAMP_DTYPE_F16>(rowp, i);
+}
+
+// The thread index through an empty asm statement: index arithmetic derived
+// from it cannot be merged with that of another phase, so per-element
+// conditions (lane masks) are recomputed where used instead of being kept
+// live across the phase boundary.
+__device__ __forceinline__ int32_t fresh_tid() {
+  int32_t t = (int32_t)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// Makes the register copy of the logits opaque: values derived from it
+// (converted floats, comparisons) are recomputed after this point rather than
+// kept live.  Used only where the registers have already been consumed.
+template <int NV>
+__device__ __forceinline__ void opaque_regs(uint4 (&raw)[NV]) {
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+    asm volatile("" : "+v"(raw[k].x), "+v"(raw[k].y), "+v"(raw[k].z), "+v"(raw[k].w));
 }
 
 // Token classes relative to the row's cut.
@@ -213,207 +234,121 @@ __device__ __forceinline__ int build_slice_entries(const SamplePlan& P, const Ro
   return n;
 }
 
-// ================================================================ k_stats
+// ----------------------------------------------------------------- LDS
+struct MergeLds {
+  uint64_t mass[kBins];  // row-aligned fixed-point mass per bin
+  uint32_t cnt[kBins];
+};
+struct SelectLds {
+  Candidate cand[kWgCandCap];
+  KeptItem klist[kKeptCap];
+  uint64_t chunk[kSliceChunks];
+};
+struct FinalLds {
+  uint64_t keys[kCandCap];
+  uint8_t keep[kCandCap];
+  uint64_t rowchunk[kMaxRowChunks];
+  uint64_t dw[kChunk];
+  int32_t did[kChunk];
+  float cx[kChunk];
+  uint8_t cent[kChunk];
+  uint8_t cflag[kChunk];
+};
+union PhaseLds {
+  uint64_t hist[kHist];
+  MergeLds m;
+  SelectLds s;
+  FinalLds f;
+};
+struct TaskLds {
+  PhaseLds u;
+  uint32_t pen[kSliceWords];
+  int32_t etok[kSliceEntryCap];
+  float ex[kSliceEntryCap];
+  RowInfo info;
+  SelectPartial part[kMaxSlices];
+  float hx[kMaxSlices];
+  int32_t htop[kMaxSlices];
+  uint32_t hfl[kMaxSlices];
+  int32_t hn[kMaxSlices];
+  float redf[kWaves];
+  int32_t redi[kWaves];
+  double redd[kWaves];
+  uint64_t redu[kWaves];
+  uint64_t misc64[4];
+  int32_t misc[8];
+  int32_t ecount;
+  int32_t ncand;
+  int32_t nlist;
+  int32_t nitems;
+  int32_t last;
+  uint32_t flags;
+};
+
+// Wave-aggregated append to an LDS list: returns this lane's slot or -1.
+__device__ __forceinline__ int wave_append(bool pred, int32_t* counter) {
+  const uint64_t m = __ballot(pred);
+  if (m == 0ull) return -1;
+  const int lane = threadIdx.x & 63;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  int b = 0;
+  if (lane == leader) b = atomicAdd(counter, (int)__popcll(m));
+  b = __shfl(b, leader, 64);
+  return pred ? b + (int)__popcll(m & ((1ull << lane) - 1ull)) : -1;
+}
+
+__device__ __forceinline__ int32_t key_id(uint64_t key) {
+  return (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+}
+__device__ __forceinline__ float key_y(uint64_t key) { return key_to_float((uint32_t)(key >> 32)); }
+
+// Transformed value of one token read on its own (chunk scan, probe).
 template <int DT>
-__global__ __launch_bounds__(kThreads) void k_stats(Workspace ws, SamplePlan P) {
-  constexpr int N = Vec<DT>::N;
-  constexpr int NV = kElemsPerThread / N;
-  constexpr uint32_t FULL = (1u << N) - 1u;
+__device__ __forceinline__ float token_value(const SamplePlan& P, const RowCtx& c, const lsamp_row_params& prm,
+                             int row, const char* rowp, const uint32_t* mrow, int64_t i,
+                             const float* patched, const uint8_t* has_patch) {
+  float x;
+  if (has_patch && has_patch[0]) {
+    x = patched[0];
+  } else {
+    x = load_scalar<DT>(rowp, i);
+    if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, i)) x = kNegInf;
+  }
+  if (x != x) x = kNegInf;
+  return x;
+}
 
-  __shared__ uint64_t s_hist[kHist];
-  __shared__ uint32_t s_pen[kSliceWords];
-  __shared__ int32_t s_etok[kSliceEntryCap];
-  __shared__ float s_ex[kSliceEntryCap];
-  __shared__ int32_t s_ecount;
-  __shared__ float s_redf[kWaves];
-  __shared__ int32_t s_redi[kWaves];
-  __shared__ double s_redd[kWaves];
-  __shared__ uint32_t s_flags;
-  __shared__ int32_t s_last;
-  // merge-phase scratch
-  __shared__ float s_hx[kMaxSlices];
-  __shared__ int32_t s_htop[kMaxSlices];
-  __shared__ uint32_t s_hfl[kMaxSlices];
-  __shared__ int32_t s_hn[kMaxSlices];
-  __shared__ int32_t s_cutinfo_cnt;
-  __shared__ double s_cutinfo_mass;
-
+// ============================================================ merge (stats)
+// Last stats work-group of a row: merges the G slice histograms (integer
+// sums on the absolute bin grid) and locates the cut bin.  Result in L.info.
+__device__ __forceinline__ void merge_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
+                          const lsamp_row_params& prm, TaskLds& L) {
   const int tid = threadIdx.x;
-  const int slice = blockIdx.x;
-  const int row = blockIdx.y;
-  const lsamp_row_params prm = P.params[row];
-  const RowCtx c = make_ctx(P.semantics, prm);
-  const int64_t V = P.vocab;
-  const int64_t base = (int64_t)slice * P.slice_len;
-  const int64_t end = (base + P.slice_len < V) ? base + P.slice_len : V;
-  const char* rowp = row_base(P, row);
-  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
-  const bool aligned = P.aligned != 0;
-
-  // 1. issue the slice's loads (held in registers through both sweeps)
-  uint4 raw[NV];
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int64_t i0 = base + (int64_t)(tid + k * kThreads) * N;
-    if (i0 < end) raw[k] = load_vec<DT>(rowp, i0, end, aligned);
-  }
-
-  // 2. penalties of the slice
-  for (int i = tid; i < kHist; i += kThreads) s_hist[i] = 0ull;
-  if (tid == 0) s_flags = 0u;
-  SliceEntries se{s_pen, s_etok, s_ex, &s_ecount};
-  bool ent_overflow = false;
-  const int n_ent = build_slice_entries<DT>(P, c, prm, row, rowp, base, end, se, &ent_overflow);
-
-  // 3. sweep 1: exclusions, non-finite flag, max
-  uint32_t excl[NV];
-  uint32_t fl = 0u;
-  float xmax = kNegInf;
-  int32_t nfin = 0;
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int64_t i0 = base + (int64_t)(tid + k * kThreads) * N;
-    if (i0 >= end) {
-      excl[k] = FULL;
-      continue;
-    }
-    const int64_t nvalid = end - i0 < N ? end - i0 : N;
-    const uint32_t valid = nvalid >= N ? FULL : ((1u << nvalid) - 1u);
-    const uint32_t allow = mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N);
-    const int32_t li0 = (int32_t)(i0 - base);
-    const uint32_t pen = (s_pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
-    excl[k] = (~allow | pen | ~valid) & FULL;
-#pragma unroll
-    for (int q = 0; q < N; ++q) {
-      const float x = vec_elem<DT>(raw[k], q);
-      if (((valid >> q) & 1u) && !__builtin_isfinite(x)) fl |= LSAMP_ROW_NONFINITE;
-      if ((excl[k] >> q) & 1u) continue;
-      if (!(x > kNegInf)) continue;
-      if (x == kPosInf) {
-        fl |= kSlicePosInf;
-        continue;
-      }
-      xmax = __builtin_fmaxf(xmax, x);
-      ++nfin;
-    }
-  }
-  for (int j = tid; j < n_ent; j += kThreads) {
-    const float x = s_ex[j];
-    if (!(x > kNegInf)) continue;
-    if (x == kPosInf) {
-      fl |= kSlicePosInf;
-      continue;
-    }
-    xmax = __builtin_fmaxf(xmax, x);
-    ++nfin;
-  }
-  if (fl) atomicOr(&s_flags, fl);
-  xmax = block_max(xmax, s_redf);
-  nfin = block_sum(nfin, s_redi);
-  const uint32_t sflags = s_flags | (ent_overflow ? kSliceEntryOverflow : 0u);
-  const int32_t top = nfin > 0 ? bin_of(xmax, c.c32) : 0;
-
-  // 4. sweep 2: histogram (count, mass relative to the bin's lower edge)
-  const bool want_hist = nfin > 0 && c.kind != LSAMP_KIND_ARGMAX;
-  if (want_hist) {
-    const float L = 1.4426950408889634f / 32.0f;
-    const float tail_edge = (float)(top - kBins + 1);
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      if (excl[k] == FULL) continue;
-#pragma unroll
-      for (int q = 0; q < N; ++q) {
-        if ((excl[k] >> q) & 1u) continue;
-        const float x = vec_elem<DT>(raw[k], q);
-        if (!(x > kNegInf) || x == kPosInf) continue;
-        const float s = bin_pos(x, c.c32);
-        const float fb = __builtin_floorf(s);
-        const int j = top - (int)fb;
-        float e;
-        int idx;
-        if (j < kBins) {
-          e = __builtin_amdgcn_exp2f((s - fb) * L + 30.0f);
-          idx = j;
-        } else {
-          e = __builtin_amdgcn_exp2f((s - tail_edge) * L + 30.0f);
-          idx = kTail;
-        }
-        atomicAdd(reinterpret_cast<unsigned long long*>(&s_hist[idx]),
-                  (unsigned long long)((1ull << kCountShift) | (uint64_t)(uint32_t)e));
-      }
-    }
-    for (int j2 = tid; j2 < n_ent; j2 += kThreads) {
-      const float x = s_ex[j2];
-      if (!(x > kNegInf) || x == kPosInf) continue;
-      const float s = bin_pos(x, c.c32);
-      const float fb = __builtin_floorf(s);
-      const int j = top - (int)fb;
-      float e;
-      int idx;
-      if (j < kBins) {
-        e = __builtin_amdgcn_exp2f((s - fb) * L + 30.0f);
-        idx = j;
-      } else {
-        e = __builtin_amdgcn_exp2f((s - tail_edge) * L + 30.0f);
-        idx = kTail;
-      }
-      atomicAdd(reinterpret_cast<unsigned long long*>(&s_hist[idx]),
-                (unsigned long long)((1ull << kCountShift) | (uint64_t)(uint32_t)e));
-    }
-  }
-
-  // 5. parity output: filter-space logits before the filters
-  if (P.processed) {
-    float* out = P.processed + (size_t)row * (size_t)V;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int64_t i0 = base + (int64_t)(tid + k * kThreads) * N;
-      if (i0 >= end) continue;
-      const int32_t li0 = (int32_t)(i0 - base);
-      const uint32_t pen = (s_pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
-#pragma unroll
-      for (int q = 0; q < N; ++q) {
-        if (i0 + q >= end || ((pen >> q) & 1u)) continue;
-        const float x = vec_elem<DT>(raw[k], q);
-        out[i0 + q] = ((excl[k] >> q) & 1u) || (x != x) ? kNegInf : to_filter(c, x);
-      }
-    }
-    for (int j = tid; j < n_ent; j += kThreads) out[s_etok[j]] = to_filter(c, s_ex[j]);
-  }
-
-  // 6. publish the slice summary
-  __syncthreads();
-  SliceSummary* S = ws.summaries + ((size_t)row * kMaxSlices + slice);
-  if (tid == 0) {
-    st_coherent_f32(&S->x_max, xmax);
-    st_coherent(&S->top_bin, top);
-    st_coherent(&S->flags, sflags);
-    st_coherent(&S->n_finite, nfin);
-  }
-  if (want_hist)
-    for (int i = tid; i < kHist; i += kThreads) st_coherent(&S->hist[i], s_hist[i]);
-  if (!arrive_last(&ws.arrive_stats[row], (uint32_t)P.slices, &s_last)) return;
-
-  // 7. last arriver: merge the row
   const int G = P.slices;
+  const int64_t V = P.vocab;
+  const SliceSummary* summ = ws.summaries + (size_t)row * kMaxSlices;
   if (tid < G) {
-    const SliceSummary* Ss = ws.summaries + ((size_t)row * kMaxSlices + tid);
-    s_hx[tid] = ld_coherent(&Ss->x_max);
-    s_htop[tid] = ld_coherent(&Ss->top_bin);
-    s_hfl[tid] = ld_coherent(&Ss->flags);
-    s_hn[tid] = ld_coherent(&Ss->n_finite);
+    L.hx[tid] = ld_coherent(&summ[tid].x_max);
+    L.htop[tid] = ld_coherent(&summ[tid].top_bin);
+    L.hfl[tid] = ld_coherent(&summ[tid].flags);
+    L.hn[tid] = ld_coherent(&summ[tid].n_finite);
   }
+  const uint64_t wtail = tid < G ? ld_coherent(&summ[tid].hist[kTail]) : 0ull;
+  L.u.m.mass[2 * tid] = 0ull;
+  L.u.m.mass[2 * tid + 1] = 0ull;
+  L.u.m.cnt[2 * tid] = 0u;
+  L.u.m.cnt[2 * tid + 1] = 0u;
   __syncthreads();
   float row_max = kNegInf;
   int32_t row_top = 0, n_total = 0;
   uint32_t rflags = 0u;
   bool first = true;
   for (int s = 0; s < G; ++s) {
-    rflags |= s_hfl[s];
-    n_total += s_hn[s];
-    if (s_hn[s] > 0) {
-      if (first || s_hx[s] > row_max) row_max = s_hx[s];
-      if (first || s_htop[s] > row_top) row_top = s_htop[s];
+    rflags |= L.hfl[s];
+    n_total += L.hn[s];
+    if (L.hn[s] > 0) {
+      if (first || L.hx[s] > row_max) row_max = L.hx[s];
+      if (first || L.htop[s] > row_top) row_top = L.htop[s];
       first = false;
     }
   }
@@ -429,8 +364,8 @@ __global__ __launch_bounds__(kThreads) void k_stats(Workspace ws, SamplePlan P) 
   info.mass_above = 0.0;
   info.z = 0.0;
   info.p_limit = -1.0;
-  info.t_min_p = kNegInf;
   info.kept_cands = 0;
+  info.pad = 0;
   const float s_top = bin_pos(row_max, c.c32);
   info.q_top = s_top * (1.0f / 32.0f);
 
@@ -438,78 +373,81 @@ __global__ __launch_bounds__(kThreads) void k_stats(Workspace ws, SamplePlan P) 
     info.cut = 0;
     info.count_above = 0;
   } else if (info.mode == kModeNormal) {
-    // per-bin counts and masses of the row (thread t owns bins 2t, 2t+1)
-    int32_t cnt[2] = {0, 0};
-    double mass[2] = {0.0, 0.0};
+    const double inv_frac = 1.0 / (double)(1ull << kMassFracBits);
     int32_t tcnt = 0;
     double tmass = 0.0;
-    const double inv_frac = 1.0 / (double)(1ull << kMassFracBits);
-    for (int s = 0; s < G; ++s) {
-      if (s_hn[s] <= 0) continue;
-      const int shift = row_top - s_htop[s];
-      const uint64_t* h = ws.summaries[(size_t)row * kMaxSlices + s].hist;
-      for (int u = 0; u < 2; ++u) {
-        const int i = 2 * tid + u;  // slice-local bin
-        const uint64_t w = ld_coherent(&h[i]);
-        if (w == 0ull) continue;
-        const int32_t wc = (int32_t)(w >> kCountShift);
-        const double wm = (double)(w & kMassMask) * inv_frac;
-        const int b = s_htop[s] - i;  // absolute bin
-        const double f = exp(((double)b - (double)s_top) / 32.0);
-        const int j = i + shift;
-        if (j >= kBins) {
-          tcnt += wc;
-          tmass += wm * f;
-        }
-      }
-      if (tid == s) {
-        const uint64_t w = ld_coherent(&h[kTail]);
-        if (w) {
-          tcnt += (int32_t)(w >> kCountShift);
-          const double edge = (double)(s_htop[s] - kBins + 1);
-          tmass += (double)(w & kMassMask) * inv_frac * exp((edge - (double)s_top) / 32.0);
+    // slice-local bin i of slice s is row bin i + (row_top - top_s); the
+    // slices are read four at a time (eight independent loads per thread)
+    for (int s0 = 0; s0 < G; s0 += 4) {
+      uint64_t w[4][2];
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          w[d][u] = (s0 + d < G && L.hn[s0 + d] > 0) ? ld_coherent(&summ[s0 + d].hist[2 * tid + u])
+                                                     : 0ull;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (w[d][u] == 0ull) continue;
+          const int s = s0 + d;
+          const int i = 2 * tid + u;
+          const int j = i + (row_top - L.htop[s]);
+          const uint32_t wc = (uint32_t)(w[d][u] >> kCountShift);
+          const uint64_t wm = w[d][u] & kMassMask;
+          if (j < kBins) {
+            atomicAdd(&L.u.m.cnt[j], wc);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.m.mass[j]), (unsigned long long)wm);
+          } else {
+            const int b = L.htop[s] - i;  // absolute bin
+            tcnt += (int32_t)wc;
+            tmass += (double)wm * inv_frac * exp(((double)b - (double)s_top) / 32.0);
+          }
         }
       }
     }
-    // gather-by-owner: each row bin j collects its slices directly
+    if (tid < G && L.hn[tid] > 0 && wtail) {
+      const double edge = (double)(L.htop[tid] - kBins + 1);
+      tcnt += (int32_t)(wtail >> kCountShift);
+      tmass += (double)(wtail & kMassMask) * inv_frac * exp((edge - (double)s_top) / 32.0);
+    }
+    __syncthreads();
+    int32_t cnt[2];
+    double mass[2];
+#pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int j = 2 * tid + u;
-      for (int s = 0; s < G; ++s) {
-        if (s_hn[s] <= 0) continue;
-        const int i = j - (row_top - s_htop[s]);
-        if (i < 0 || i >= kBins) continue;
-        const uint64_t w = ld_coherent(&ws.summaries[(size_t)row * kMaxSlices + s].hist[i]);
-        if (w == 0ull) continue;
-        cnt[u] += (int32_t)(w >> kCountShift);
-        mass[u] += (double)(w & kMassMask) * inv_frac;
-      }
-      mass[u] *= exp(((double)(row_top - j) - (double)s_top) / 32.0);
+      cnt[u] = (int32_t)L.u.m.cnt[j];
+      mass[u] = cnt[u] ? (double)L.u.m.mass[j] * inv_frac *
+                             exp(((double)(row_top - j) - (double)s_top) / 32.0)
+                       : 0.0;
     }
-    tcnt = block_sum(tcnt, s_redi);
-    tmass = block_sum(tmass, s_redd);
+    tcnt = block_sum(tcnt, L.redi);
+    tmass = block_sum(tmass, L.redd);
     int32_t tot_cnt = 0;
     double tot_mass = 0.0;
-    const int32_t excl_cnt = block_excl_scan(cnt[0] + cnt[1], s_redi, &tot_cnt);
-    const double excl_mass = block_excl_scan(mass[0] + mass[1], s_redd, &tot_mass);
+    const int32_t excl_cnt = block_excl_scan(cnt[0] + cnt[1], L.redi, &tot_cnt);
+    const double excl_mass = block_excl_scan(mass[0] + mass[1], L.redd, &tot_mass);
     const double z = tot_mass + tmass;
     info.z = z;
 
     const int32_t k_lim = (prm.top_k > 0 && (int64_t)prm.top_k < V) ? prm.top_k : 0;
     bool p_on;
     double P_lim;
-    bool strict;  // CBv2: exclusive mass <= P keeps; mlx-lm: ascending cum > 1-P keeps
+    bool strict;  // CBv2 keeps exclusive mass <= P; mlx-lm keeps mass-before < P
     if (P.semantics == LSAMP_SEM_CBV2) {
       p_on = prm.top_p < 1.0f;
       P_lim = (double)(prm.top_p > 0.0f ? prm.top_p : 0.0f) * z;
       strict = false;
     } else {
-      p_on = c.kind == LSAMP_KIND_FILTERED && prm.top_p > 0.0f && prm.top_p < 1.0f;
+      p_on = prm.top_p > 0.0f && prm.top_p < 1.0f;
       P_lim = (double)prm.top_p * z;
       strict = true;
     }
-    if (c.kind == LSAMP_KIND_CATEGORICAL) p_on = false;
+    if (c.kind != LSAMP_KIND_FILTERED) p_on = false;
     const bool k_on = c.kind == LSAMP_KIND_FILTERED && k_lim > 0;
-    float mp = prm.min_p > 1.0f ? 1.0f : prm.min_p;
+    const float mp = prm.min_p > 1.0f ? 1.0f : prm.min_p;
     const bool m_on = c.kind == LSAMP_KIND_FILTERED && mp > 0.0f;
     int32_t j_t = kBins + 1;
     if (m_on) {
@@ -517,35 +455,34 @@ __global__ __launch_bounds__(kThreads) void k_stats(Workspace ws, SamplePlan P) 
       j_t = row_top - (int32_t)__builtin_floorf(__builtin_fmaxf(st, -1.0e9f));
       if (j_t < 0) j_t = 0;
       if (j_t > kBins) j_t = kBins;
-      info.t_min_p = __builtin_logf(mp);
     }
     info.p_limit = p_on ? P_lim : -1.0;
-
     int my_cut = 0x7fffffff;
     int32_t C = excl_cnt;
     double M = excl_mass;
+#pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int j = 2 * tid + u;
       if (cnt[u] > 0 || (m_on && j == j_t)) {
         const bool tk = k_on && C + cnt[u] >= k_lim;
-        const bool tp = p_on && cnt[u] > 0 && (strict ? (M + mass[u] >= P_lim) : (M + mass[u] > P_lim));
+        const bool tp = p_on && cnt[u] > 0 &&
+                        (strict ? (M + mass[u] >= P_lim) : (M + mass[u] > P_lim));
         const bool tm = m_on && j >= j_t;
         if ((tk || tp || tm) && j < my_cut) my_cut = j;
       }
       C += cnt[u];
       M += mass[u];
     }
-    const int cut = block_min(my_cut, s_redi);
+    const int cut = block_min(my_cut, L.redi);
     if (cut != 0x7fffffff) {
-      // owner thread publishes the prefix at the cut
       if (cut / 2 == tid) {
-        s_cutinfo_cnt = excl_cnt + ((cut & 1) ? cnt[0] : 0);
-        s_cutinfo_mass = excl_mass + ((cut & 1) ? mass[0] : 0.0);
+        L.misc[0] = excl_cnt + ((cut & 1) ? cnt[0] : 0);
+        L.misc64[0] = __builtin_bit_cast(uint64_t, excl_mass + ((cut & 1) ? mass[0] : 0.0));
       }
       __syncthreads();
       info.cut = cut;
-      info.count_above = s_cutinfo_cnt;
-      info.mass_above = s_cutinfo_mass;
+      info.count_above = L.misc[0];
+      info.mass_above = __builtin_bit_cast(double, L.misc64[0]);
     } else {
       const bool tk = k_on && tot_cnt + tcnt >= k_lim;
       const bool tp = p_on && tcnt > 0 && (strict ? (z >= P_lim) : (z > P_lim));
@@ -561,238 +498,114 @@ __global__ __launch_bounds__(kThreads) void k_stats(Workspace ws, SamplePlan P) 
       }
     }
   }
-  if (tid == 0) {
-    ws.rows[row] = info;
-    ws.arrive_stats[row] = 0u;
-  }
+  __syncthreads();
+  if (tid == 0) L.info = info;
+  __syncthreads();
 }
 
-// =============================================================== k_select
-struct SelectShared {
-  // bulk phase
-  uint32_t pen[kSliceWords];
-  int32_t etok[kSliceEntryCap];
-  float ex[kSliceEntryCap];
-  Candidate wcand[kWgCandCap];
-  uint64_t chunk[kSliceChunks];
-};
-struct FinalShared {
-  uint64_t keys[kCandCap];
-  uint8_t keep[kCandCap];
-  uint64_t rowchunk[kMaxRowChunks];
-  float cx[kChunk];
-  uint8_t cent[kChunk];
-  uint8_t cflag[kChunk];
-};
-union SelectLds {
-  SelectShared a;
-  FinalShared b;
-};
+__device__ __forceinline__ void publish_rowinfo(RowInfo* dst, const RowInfo& v) {
+  st_coherent_f32(&dst->x_max, v.x_max);
+  st_coherent_f32(&dst->q_top, v.q_top);
+  st_coherent(&dst->top_bin, v.top_bin);
+  st_coherent(&dst->cut, v.cut);
+  st_coherent(&dst->mode, v.mode);
+  st_coherent(&dst->flags, v.flags);
+  st_coherent(&dst->count_above, v.count_above);
+  st_coherent(&dst->n_finite, v.n_finite);
+  st_coherent_f64(&dst->mass_above, v.mass_above);
+  st_coherent_f64(&dst->z, v.z);
+  st_coherent_f64(&dst->p_limit, v.p_limit);
+  st_coherent(&dst->kept_cands, v.kept_cands);
+}
 
+__device__ __forceinline__ RowInfo read_rowinfo(const RowInfo* src) {
+  RowInfo v;
+  v.x_max = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&src->x_max)));
+  v.q_top = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&src->q_top)));
+  v.top_bin = ld_coherent(&src->top_bin);
+  v.cut = ld_coherent(&src->cut);
+  v.mode = ld_coherent(&src->mode);
+  v.flags = ld_coherent(&src->flags);
+  v.count_above = ld_coherent(&src->count_above);
+  v.n_finite = ld_coherent(&src->n_finite);
+  v.mass_above = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&src->mass_above)));
+  v.z = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&src->z)));
+  v.p_limit = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&src->p_limit)));
+  v.kept_cands = ld_coherent(&src->kept_cands);
+  v.pad = 0;
+  return v;
+}
+
+// ========================================================= finalize (select)
+// Last select work-group of a row: exact cut among the candidates, kept
+// weights per chunk, and the inverse-CDF draw.
 template <int DT>
-__global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P) {
-  constexpr int N = Vec<DT>::N;
-  constexpr int NV = kElemsPerThread / N;
-  constexpr uint32_t FULL = (1u << N) - 1u;
-
-  __shared__ SelectLds L;
-  __shared__ int32_t s_ecount;
-  __shared__ int32_t s_ncand;
-  __shared__ float s_redf[kWaves];
-  __shared__ int32_t s_redi[kWaves];
-  __shared__ double s_redd[kWaves];
-  __shared__ uint64_t s_redu[kWaves];
-  __shared__ int32_t s_last;
-  __shared__ int32_t s_misc[4];
-  __shared__ uint64_t s_misc64[2];
-
+__device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
+                             const lsamp_row_params& prm, const RowInfo& info, TaskLds& L,
+                             const char* rowp, const uint32_t* mrow, bool fused) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int slice = blockIdx.x;
-  const int row = blockIdx.y;
-  const lsamp_row_params prm = P.params[row];
-  const RowCtx c = make_ctx(P.semantics, prm);
-  const RowInfo info = ws.rows[row];
+  const int G = P.slices;
   const int64_t V = P.vocab;
-  const int64_t base = (int64_t)slice * P.slice_len;
-  const int64_t end = (base + P.slice_len < V) ? base + P.slice_len : V;
-  const char* rowp = row_base(P, row);
-  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
-  const bool aligned = P.aligned != 0;
+  const int nch_row = P.nchunks;
   const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
   const bool active = info.mode != kModeEmpty;
-
-  for (int i = tid; i < kSliceChunks; i += kThreads) L.a.chunk[i] = 0ull;
-  if (tid == 0) s_ncand = 0;
-  SliceEntries se{L.a.pen, L.a.etok, L.a.ex, &s_ecount};
-  bool ent_overflow = false;
-  const int n_ent = build_slice_entries<DT>(P, c, prm, row, rowp, base, end, se, &ent_overflow);
-
-  double ent = 0.0;
-  float min_kept = kPosInf;
-  int32_t n_kept = 0;
-  if (!active && P.keep) {
-    for (int64_t i = base + tid; i < end; i += kThreads) P.keep[(size_t)row * (size_t)V + i] = 0;
-  }
-  if (active) {
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int64_t i0 = base + (int64_t)(tid + k * kThreads) * N;
-      const bool in = i0 < end;
-      uint64_t part = 0ull;
-      uint32_t cand_bits = 0u;
-      float cy[N];
-      if (in) {
-        const uint4 raw = load_vec<DT>(rowp, i0, end, aligned);
-        const int64_t nvalid = end - i0 < N ? end - i0 : N;
-        const uint32_t valid = nvalid >= N ? FULL : ((1u << nvalid) - 1u);
-        const uint32_t allow = mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N);
-        const int32_t li0 = (int32_t)(i0 - base);
-        const uint32_t pen = (L.a.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
-        const uint32_t ex = (~allow | pen | ~valid) & FULL;
-        uint8_t* kout = P.keep ? P.keep + (size_t)row * (size_t)V : nullptr;
-#pragma unroll
-        for (int q = 0; q < N; ++q) {
-          cy[q] = 0.0f;
-          // keep bytes of candidates are written by the finalize alone (one
-          // writer per byte: plain stores from different XCDs have no order)
-          if ((ex >> q) & 1u) {
-            if (kout && ((valid & ~pen) >> q & 1u)) kout[i0 + q] = 0;
-            continue;
-          }
-          const float x = vec_elem<DT>(raw, q);
-          const int cls = classify(info, c, x);
-          if (kout && cls != kCand) kout[i0 + q] = cls == kKept ? 1 : 0;
-          if (cls == kKept) {
-            const float y = to_filter(c, x);
-            const uint64_t w = weight(y, y_max, c.scale);
-            part += w;
-            ent += (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
-            min_kept = __builtin_fminf(min_kept, y);
-            ++n_kept;
-          } else if (cls == kCand) {
-            cy[q] = to_filter(c, x);
-            cand_bits |= 1u << q;
-          }
-        }
-      }
-      // chunk sums: a wave's vectors lie in one chunk
-      const uint64_t any = __ballot(part != 0ull);
-      if (any) {
-        const uint64_t sum = wave_sum(part);
-        if (lane == 0) {
-          const int64_t wi0 = (int64_t)((tid & ~63) + k * kThreads) * N;  // slice-local
-          atomicAdd(reinterpret_cast<unsigned long long*>(&L.a.chunk[wi0 / kChunk]),
-                    (unsigned long long)sum);
-        }
-      }
-      // candidates: wave-aggregated append per element position
-#pragma unroll
-      for (int q = 0; q < N; ++q) {
-        const bool is_c = (cand_bits >> q) & 1u;
-        const uint64_t m = __ballot(is_c);
-        if (m == 0ull) continue;
-        int basei = 0;
-        if (lane == __ffsll((unsigned long long)m) - 1)
-          basei = atomicAdd(&s_ncand, (int)__popcll(m));
-        basei = __shfl(basei, __ffsll((unsigned long long)m) - 1, 64);
-        if (is_c) {
-          const int off = basei + (int)__popcll(m & ((1ull << lane) - 1ull));
-          if (off < kWgCandCap) {
-            L.a.wcand[off].y = cy[q];
-            L.a.wcand[off].id = (int32_t)(i0 + q);
-          }
-        }
-      }
-    }
-    for (int j2 = tid; j2 < n_ent; j2 += kThreads) {
-      const float x = L.a.ex[j2];
-      const int cls = classify(info, c, x);
-      const int32_t t = L.a.etok[j2];
-      if (P.keep && cls != kCand) P.keep[(size_t)row * (size_t)V + t] = cls == kKept ? 1 : 0;
-      if (cls == kKept) {
-        const float y = to_filter(c, x);
-        const uint64_t w = weight(y, y_max, c.scale);
-        atomicAdd(reinterpret_cast<unsigned long long*>(&L.a.chunk[(t - base) / kChunk]),
-                  (unsigned long long)w);
-        ent += (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
-        min_kept = __builtin_fminf(min_kept, y);
-        ++n_kept;
-      } else if (cls == kCand) {
-        const int off = atomicAdd(&s_ncand, 1);
-        if (off < kWgCandCap) {
-          L.a.wcand[off].y = to_filter(c, x);
-          L.a.wcand[off].id = t;
-        }
-      }
-    }
-  }
-  ent = block_sum(ent, s_redd);
-  min_kept = block_min(min_kept, s_redf);
-  n_kept = block_sum(n_kept, s_redi);
-
-  // publish chunk sums, candidates, partials
-  const int64_t chunk0 = base / kChunk;
-  const int nch = (int)((end - base + kChunk - 1) / kChunk);
   uint64_t* rowchunks = ws.chunk_w + (size_t)row * (size_t)ws.max_chunks;
-  for (int i = tid; i < nch; i += kThreads) st_coherent(&rowchunks[chunk0 + i], L.a.chunk[i]);
-  const int ncand = s_ncand;
-  if (tid == 0)
-    s_misc[0] = ncand > 0 ? (int)__hip_atomic_fetch_add(&ws.cand_count[row], (uint32_t)ncand,
-                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                          : 0;
-  __syncthreads();
-  const int gbase = s_misc[0];
-  const int ncopy = ncand < kWgCandCap ? ncand : kWgCandCap;
   Candidate* rc = ws.cands + (size_t)row * kCandCap;
-  for (int i = tid; i < ncopy; i += kThreads)
-    if (gbase + i < kCandCap) {
-      st_coherent_f32(&rc[gbase + i].y, L.a.wcand[i].y);
-      st_coherent(&rc[gbase + i].id, L.a.wcand[i].id);
-    }
-  if (tid == 0) {
-    SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + slice;
-    st_coherent_f64(&sp->ent, ent);
-    st_coherent_f32(&sp->min_kept, min_kept);
-    st_coherent(&sp->n_kept, n_kept);
-    st_coherent(&sp->n_cand, ncand);
-    st_coherent(&sp->pad, ent_overflow ? 1 : 0);
-  }
-  if (!arrive_last(&ws.arrive_select[row], (uint32_t)P.slices, &s_last)) return;
+  FinalLds& F = L.u.f;
 
-  // ------------------------------------------------------------ finalize
-  const int G = P.slices;
+  // ---- every independent load first
+  if (tid < G) {
+    const SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + tid;
+    SelectPartial v;
+    v.ent = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&sp->ent)));
+    v.min_kept = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&sp->min_kept)));
+    v.n_kept = ld_coherent(&sp->n_kept);
+    v.n_cand = ld_coherent(&sp->n_cand);
+    v.n_list = ld_coherent(&sp->n_list);
+    v.overflow = ld_coherent(&sp->overflow);
+    v.pad = 0;
+    L.part[tid] = v;
+  }
+  F.rowchunk[tid] = tid < nch_row ? ld_coherent(&rowchunks[tid]) : 0ull;
+  if (tid == 0) {
+    L.misc[0] = (int32_t)ld_coherent(&ws.cand_count[row]);
+    float u = 0.0f;
+    if (P.uniforms)
+      u = P.uniforms[row];
+    else if (P.philox_keys)
+      u = philox_uniform(P.philox_keys[row], 0u);
+    L.misc64[1] = (uint64_t)__float_as_uint(u);
+    L.misc[1] = P.probe_tokens ? P.probe_tokens[row] : -1;
+  }
+  __syncthreads();
   double ent_all = 0.0;
   float min_all = kPosInf;
   int32_t kept_all = 0;
   bool overflow = (info.flags & LSAMP_ROW_OVERFLOW) != 0;
   for (int s = 0; s < G; ++s) {
-    const SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + s;
-    const double pe = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&sp->ent)));
-    ent_all += pe;
-    min_all = __builtin_fminf(min_all, ld_coherent(&sp->min_kept));
-    kept_all += ld_coherent(&sp->n_kept);
-    if (ld_coherent(&sp->n_cand) > kWgCandCap || ld_coherent(&sp->pad)) overflow = true;
+    ent_all += L.part[s].ent;
+    min_all = __builtin_fminf(min_all, L.part[s].min_kept);
+    kept_all += L.part[s].n_kept;
+    if (L.part[s].n_cand > kWgCandCap || L.part[s].overflow) overflow = true;
   }
-  const uint32_t total_cand = ld_coherent(&ws.cand_count[row]);
-  if (total_cand > (uint32_t)kCandCap) overflow = true;
-  const int nc = overflow ? 0 : (int)total_cand;
-  const int nch_row = P.nchunks;
+  const int total_cand = L.misc[0];
+  if (total_cand > kCandCap) overflow = true;
+  const float u_draw = __uint_as_float((uint32_t)L.misc64[1]);
+  const int32_t probe = L.misc[1];
+  const int nc = (overflow || !active) ? 0 : total_cand;
 
-  // sort candidates: value descending, id ascending
+  // ---- sort candidates: value descending, id ascending (-0 == +0)
   int n2 = 1;
   while (n2 < nc) n2 <<= 1;
   for (int i = tid; i < n2; i += kThreads) {
     uint64_t key = 0ull;
     if (i < nc) {
-      const float y =
-          __builtin_bit_cast(float, ld_coherent(reinterpret_cast<const uint32_t*>(&rc[i].y)));
+      const float y = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[i].y)));
       const int32_t id = ld_coherent(&rc[i].id);
-      // -0 and +0 are equal values: both order as +0, ties then go by id
       key = ((uint64_t)ordered_key(y == 0.0f ? 0.0f : y) << 32) |
             (uint64_t)(0xffffffffu - (uint32_t)id);
     }
-    L.b.keys[i] = key;
+    F.keys[i] = key;
   }
   __syncthreads();
   for (int kk = 2; kk <= n2; kk <<= 1) {
@@ -800,11 +613,11 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
       for (int i = tid; i < n2; i += kThreads) {
         const int ixj = i ^ jj;
         if (ixj > i) {
-          const uint64_t a = L.b.keys[i], b = L.b.keys[ixj];
+          const uint64_t a = F.keys[i], b = F.keys[ixj];
           const bool desc = (i & kk) == 0;
           if (desc ? (a < b) : (a > b)) {
-            L.b.keys[i] = b;
-            L.b.keys[ixj] = a;
+            F.keys[i] = b;
+            F.keys[ixj] = a;
           }
         }
       }
@@ -812,7 +625,7 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
     }
   }
 
-  // keep rule over the sorted candidates (thread t owns a contiguous run)
+  // ---- keep rule over the sorted candidates (thread t owns a contiguous run)
   const int per = (n2 + kThreads - 1) / kThreads;  // <= kFinalPerThread
   const int r0 = tid * per;
   const double P_lim = info.p_limit;
@@ -824,27 +637,27 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
   const bool m_on = c.kind == LSAMP_KIND_FILTERED && mp > 0.0f;
   const float ln_mp = m_on ? __builtin_logf(mp) : 0.0f;
   const bool mlx = P.semantics == LSAMP_SEM_MLXLM;
+  // the per-thread arrays are indexed by unrolled constants only (registers)
   double e_loc[kFinalPerThread];
   double e_sum = 0.0;
-  for (int u = 0; u < per; ++u) {
+#pragma unroll
+  for (int u = 0; u < kFinalPerThread; ++u) {
     const int r = r0 + u;
     double e = 0.0;
-    if (r < nc) {
-      const float y = key_to_float((uint32_t)(L.b.keys[r] >> 32));
-      e = (double)__builtin_expf(y - info.q_top);
-    }
+    if (u < per && r < nc) e = (double)__builtin_expf(key_y(F.keys[r]) - info.q_top);
     e_loc[u] = e;
     e_sum += e;
   }
   double e_tot = 0.0;
-  double e_excl = block_excl_scan(e_sum, s_redd, &e_tot);
+  double e_excl = block_excl_scan(e_sum, L.redd, &e_tot);
   int32_t surv_loc = 0;
   uint8_t surv[kFinalPerThread];
-  for (int u = 0; u < per; ++u) {
+#pragma unroll
+  for (int u = 0; u < kFinalPerThread; ++u) {
     const int r = r0 + u;
     surv[u] = 0;
-    if (r >= nc) continue;
-    const uint32_t kr = (uint32_t)(L.b.keys[r] >> 32);
+    if (u >= per || r >= nc) continue;
+    const uint32_t kr = (uint32_t)(F.keys[r] >> 32);
     const float y = key_to_float(kr);
     bool keep_p = true, keep_m = true;
     if (mlx) {
@@ -852,14 +665,14 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
       int lo = 0, hi = r;
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if ((uint32_t)(L.b.keys[mid] >> 32) == kr) hi = mid; else lo = mid + 1;
+        if ((uint32_t)(F.keys[mid] >> 32) == kr) hi = mid; else lo = mid + 1;
       }
       const int g0 = lo;
       lo = r;
       hi = nc - 1;
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if ((uint32_t)(L.b.keys[mid] >> 32) == kr) lo = mid; else hi = mid - 1;
+        if ((uint32_t)(F.keys[mid] >> 32) == kr) lo = mid; else hi = mid - 1;
       }
       const int g1 = lo + 1;
       // mass ranked strictly before r when equal values put higher ids first
@@ -880,195 +693,229 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
     e_excl += e_loc[u];
   }
   int32_t surv_tot = 0;
-  int32_t surv_excl = block_excl_scan(surv_loc, s_redi, &surv_tot);
+  int32_t surv_excl = block_excl_scan(surv_loc, L.redi, &surv_tot);
   int32_t kc_loc = 0;
-  for (int u = 0; u < per; ++u) {
+  double cent = 0.0;
+  float cmin = kPosInf;
+#pragma unroll
+  for (int u = 0; u < kFinalPerThread; ++u) {
     const int r = r0 + u;
-    if (r >= n2) break;
+    if (u >= per || r >= n2) continue;
     uint8_t keep = surv[u];
     if (keep && mlx && k_lim > 0) {
       keep = ((int64_t)info.count_above + surv_excl) < k_lim ? 1 : 0;
       ++surv_excl;
     }
-    L.b.keep[r] = keep;
-    kc_loc += keep;
+    F.keep[r] = keep;
+    if (keep) {
+      const float y = key_y(F.keys[r]);
+      const uint64_t wgt = weight(y, y_max, c.scale);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&F.rowchunk[key_id(F.keys[r]) / kChunk]),
+                (unsigned long long)wgt);
+      cent += (double)wgt * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
+      cmin = __builtin_fminf(cmin, y);
+      ++kc_loc;
+    }
   }
-  // row chunk sums (published by every slice)
-  for (int i = tid; i < nch_row; i += kThreads) L.b.rowchunk[i] = ld_coherent(&rowchunks[i]);
-  __syncthreads();
+  cent = block_sum(cent, L.redd);
+  cmin = block_min(cmin, L.redf);
+  int32_t kept_c = 0;
+  int32_t kexcl = block_excl_scan(kc_loc, L.redi, &kept_c);
+  // persist kept candidates (MTP residual pass) and the keep bytes of every
+  // candidate (parity output; the select phase leaves candidates' bytes alone)
   for (int u = 0; u < per; ++u) {
     const int r = r0 + u;
-    if (r >= nc || !L.b.keep[r]) continue;
-    const float y = key_to_float((uint32_t)(L.b.keys[r] >> 32));
-    const int32_t id = (int32_t)(0xffffffffu - (uint32_t)(L.b.keys[r] & 0xffffffffull));
-    const uint64_t w = weight(y, y_max, c.scale);
-    atomicAdd(reinterpret_cast<unsigned long long*>(&L.b.rowchunk[id / kChunk]),
-              (unsigned long long)w);
-  }
-  // entropy / min / count contributions of kept candidates
-  double cent = 0.0;
-  float cmin = kPosInf;
-  for (int u = 0; u < per; ++u) {
-    const int r = r0 + u;
-    if (r >= nc || !L.b.keep[r]) continue;
-    const float y = key_to_float((uint32_t)(L.b.keys[r] >> 32));
-    const uint64_t w = weight(y, y_max, c.scale);
-    cent += (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
-    cmin = __builtin_fminf(cmin, y);
-  }
-  cent = block_sum(cent, s_redd);
-  cmin = block_min(cmin, s_redf);
-  const int32_t kept_c = block_sum(kc_loc, s_redi);
-
-  // persist kept candidates (ids) for the MTP residual pass
-  if (!overflow) {
-    int32_t kexcl_tot = 0;
-    int32_t kexcl = block_excl_scan(kc_loc, s_redi, &kexcl_tot);
-    for (int u = 0; u < per; ++u) {
-      const int r = r0 + u;
-      if (r >= nc || !L.b.keep[r]) continue;
-      const float y = key_to_float((uint32_t)(L.b.keys[r] >> 32));
-      const int32_t id = (int32_t)(0xffffffffu - (uint32_t)(L.b.keys[r] & 0xffffffffull));
-      rc[kexcl].y = y;
-      rc[kexcl].id = id;
+    if (r >= nc) break;
+    if (F.keep[r]) {
+      rc[kexcl].y = key_y(F.keys[r]);
+      rc[kexcl].id = key_id(F.keys[r]);
       ++kexcl;
     }
-    if (P.keep) {
-      for (int r = tid; r < nc; r += kThreads) {
-        const int32_t id = (int32_t)(0xffffffffu - (uint32_t)(L.b.keys[r] & 0xffffffffull));
-        P.keep[(size_t)row * (size_t)V + id] = L.b.keep[r];
-      }
-    }
+    if (P.keep) P.keep[(size_t)row * (size_t)V + key_id(F.keys[r])] = F.keep[r];
   }
 
-  // total weight and the chunk that holds the target
-  uint64_t wt = tid < nch_row ? L.b.rowchunk[tid] : 0ull;
+  // ---- total weight and the chunk holding the target
+  const uint64_t wt = F.rowchunk[tid];
   uint64_t W = 0ull;
-  const uint64_t wexcl = block_excl_scan(wt, s_redu, &W);
-  float u_draw = 0.0f;
-  if (P.uniforms)
-    u_draw = P.uniforms[row];
-  else if (P.philox_keys)
-    u_draw = philox_uniform(P.philox_keys[row], 0u);
+  const uint64_t wexcl = block_excl_scan(wt, L.redu, &W);
   const uint64_t target = W ? scaled_target(uniform_u32(u_draw), W) : 0ull;
   if (tid == 0) {
-    s_misc[1] = -1;
-    s_misc[2] = -1;
+    L.misc[2] = -1;
+    L.misc[3] = -1;
   }
   __syncthreads();
-  if (W && tid < nch_row && wt && wexcl <= target && target < wexcl + wt) {
-    s_misc[1] = tid;
-    s_misc64[0] = target - wexcl;
+  if (W && wt && wexcl <= target && target < wexcl + wt) {
+    L.misc[2] = tid;
+    L.misc64[0] = target - wexcl;
   }
   __syncthreads();
-  const int cstar = (overflow || !active) ? -1 : s_misc[1];
-  const uint64_t ltarget = s_misc64[0];
+  const int cstar = (overflow || !active) ? -1 : L.misc[2];
+  const uint64_t ltarget = L.misc64[0];
 
-  // scan the chosen chunk in token order
   if (cstar >= 0) {
     const int64_t cb = (int64_t)cstar * kChunk;
     const int64_t ce = cb + kChunk < V ? cb + kChunk : V;
-    for (int i = tid; i < kChunk; i += kThreads) {
-      L.b.cent[i] = 0;
-      L.b.cflag[i] = 0;
+    const int cps = P.slice_len / kChunk;
+    const int sc = cstar / cps;
+    const bool list_ok = L.part[sc].n_list <= kKeptCap;
+    if (tid == 0) L.nitems = 0;
+    __syncthreads();
+    if (list_ok) {
+      // fast path: the kept tokens of this chunk are all listed
+      const KeptItem* kl = ws.klist + ((size_t)row * kMaxSlices + sc) * kKeptCap;
+      const int nl = L.part[sc].n_list;
+      static_assert(kKeptCap <= kThreads, "one listed item per thread");
+      if (tid < nl) {
+        const int32_t id = ld_coherent(&kl[tid].id);
+        if (id >= cb && id < ce) {
+          const int slot = atomicAdd(&L.nitems, 1);
+          F.did[slot] = id;
+          F.dw[slot] = ld_coherent(&kl[tid].w);
+        }
+      }
+      for (int r = tid; r < nc; r += kThreads) {
+        if (!F.keep[r]) continue;
+        const int32_t id = key_id(F.keys[r]);
+        if (id >= cb && id < ce) {
+          const int slot = atomicAdd(&L.nitems, 1);
+          F.did[slot] = id;
+          F.dw[slot] = weight(key_y(F.keys[r]), y_max, c.scale);
+        }
+      }
+      __syncthreads();
+      const int ni = L.nitems;
+      int m2 = 1;
+      while (m2 < ni) m2 <<= 1;
+      for (int i = ni + tid; i < m2; i += kThreads) {
+        F.did[i] = 0x7fffffff;
+        F.dw[i] = 0ull;
+      }
+      __syncthreads();
+      for (int kk = 2; kk <= m2; kk <<= 1) {
+        for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+          for (int i = tid; i < m2; i += kThreads) {
+            const int ixj = i ^ jj;
+            if (ixj > i) {
+              const int32_t a = F.did[i], b = F.did[ixj];
+              const bool asc = (i & kk) == 0;
+              if (asc ? (a > b) : (a < b)) {
+                F.did[i] = b;
+                F.did[ixj] = a;
+                const uint64_t t = F.dw[i];
+                F.dw[i] = F.dw[ixj];
+                F.dw[ixj] = t;
+              }
+            }
+          }
+          __syncthreads();
+        }
+      }
+      // items 2t, 2t+1 per thread, in id order
+      const uint64_t w0 = 2 * tid < ni ? F.dw[2 * tid] : 0ull;
+      const uint64_t w1 = 2 * tid + 1 < ni ? F.dw[2 * tid + 1] : 0ull;
+      uint64_t tot = 0ull;
+      const uint64_t ex = block_excl_scan(w0 + w1, L.redu, &tot);
+      if (w0 && ex <= ltarget && ltarget < ex + w0) L.misc[3] = F.did[2 * tid];
+      if (w1 && ex + w0 <= ltarget && ltarget < ex + w0 + w1) L.misc[3] = F.did[2 * tid + 1];
+      __syncthreads();
+    } else {
+      // scan the chunk in token order (re-read from L2 / HBM)
+      for (int i = tid; i < kChunk; i += kThreads) {
+        F.cent[i] = 0;
+        F.cflag[i] = 0;
+      }
+      __syncthreads();
+      for (int r = tid; r < nc; r += kThreads) {
+        if (!F.keep[r]) continue;
+        const int32_t id = key_id(F.keys[r]);
+        if (id >= cb && id < ce) F.cflag[id - cb] = 1;
+      }
+      int32_t e0 = 0, e1 = 0;
+      if (P.row_ptr && P.entries) {
+        e0 = P.row_ptr[row];
+        e1 = P.row_ptr[row + 1];
+      }
+      for (int32_t e = e0 + tid; e < e1; e += kThreads) {
+        const lsamp_penalty_entry ent = P.entries[e];
+        if (ent.token < cb || ent.token >= ce) continue;
+        float x = load_scalar<DT>(rowp, ent.token);
+        x = patch_value(c, prm, x, ent, DT);
+        if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, ent.token)) x = kNegInf;
+        if (x != x) x = kNegInf;
+        F.cx[ent.token - cb] = x;
+        F.cent[ent.token - cb] = 1;
+      }
+      __syncthreads();
+      uint64_t wl[2] = {0ull, 0ull};
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int li = 2 * tid + u;
+        const int64_t i = cb + li;
+        if (i >= ce) continue;
+        const float x = token_value<DT>(P, c, prm, row, rowp, mrow, i, &F.cx[li], &F.cent[li]);
+        const int cls = classify(info, c, x);
+        if (cls == kKept || (cls == kCand && F.cflag[li]))
+          wl[u] = weight(to_filter(c, x), y_max, c.scale);
+      }
+      uint64_t ctot = 0ull;
+      const uint64_t cex = block_excl_scan(wl[0] + wl[1], L.redu, &ctot);
+      if (wl[0] && cex <= ltarget && ltarget < cex + wl[0]) L.misc[3] = (int)(cb + 2 * tid);
+      if (wl[1] && cex + wl[0] <= ltarget && ltarget < cex + wl[0] + wl[1])
+        L.misc[3] = (int)(cb + 2 * tid + 1);
+      __syncthreads();
+    }
+  }
+  const int token = cstar >= 0 ? L.misc[3] : -1;
+
+  // ---- probe token (MTP acceptance): its kept weight
+  uint64_t probe_w = 0ull;
+  if (probe >= 0 && probe < V && !overflow && active) {
+    if (tid == 0) {
+      L.misc[4] = 0;
+      L.misc[5] = 0;
     }
     __syncthreads();
-    for (int i = tid; i < nc; i += kThreads) {
-      if (!L.b.keep[i]) continue;
-      const int32_t id = (int32_t)(0xffffffffu - (uint32_t)(L.b.keys[i] & 0xffffffffull));
-      if (id >= cb && id < ce) L.b.cflag[id - cb] = 1;
-    }
+    for (int r = tid; r < nc; r += kThreads)
+      if (F.keep[r] && key_id(F.keys[r]) == probe) L.misc[4] = 1;
     int32_t e0 = 0, e1 = 0;
     if (P.row_ptr && P.entries) {
       e0 = P.row_ptr[row];
       e1 = P.row_ptr[row + 1];
     }
     for (int32_t e = e0 + tid; e < e1; e += kThreads) {
-      const lsamp_penalty_entry ent2 = P.entries[e];
-      if (ent2.token < cb || ent2.token >= ce) continue;
-      float x = load_logit(DT, rowp, ent2.token);
-      x = patch_value(c, prm, x, ent2, DT);
-      if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, ent2.token)) x = kNegInf;
-      if (x != x) x = kNegInf;
-      L.b.cx[ent2.token - cb] = x;
-      L.b.cent[ent2.token - cb] = 1;
+      const lsamp_penalty_entry ent = P.entries[e];
+      if (ent.token != probe) continue;
+      const float x = patch_value(c, prm, load_scalar<DT>(rowp, probe), ent, DT);
+      F.cx[0] = x;
+      L.misc[5] = 1;
     }
     __syncthreads();
-    uint64_t wl[2] = {0ull, 0ull};
-    for (int u = 0; u < 2; ++u) {
-      const int64_t i = cb + 2 * tid + u;
-      if (i >= ce) continue;
-      const int li = (int)(i - cb);
-      float x;
-      if (L.b.cent[li]) {
-        x = L.b.cx[li];
-      } else {
-        x = load_logit(DT, rowp, i);
-        if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, i) || x != x) x = kNegInf;
-      }
+    if (tid == 0) {
+      float x = L.misc[5] ? F.cx[0] : load_scalar<DT>(rowp, probe);
+      if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, probe) || x != x) x = kNegInf;
       const int cls = classify(info, c, x);
-      if (cls == kKept || (cls == kCand && L.b.cflag[li]))
-        wl[u] = weight(to_filter(c, x), y_max, c.scale);
+      L.misc64[2] = (cls == kKept || (cls == kCand && L.misc[4]))
+                        ? weight(to_filter(c, x), y_max, c.scale)
+                        : 0ull;
     }
-    uint64_t ctot = 0ull;
-    const uint64_t cex = block_excl_scan(wl[0] + wl[1], s_redu, &ctot);
-    if (wl[0] && cex <= ltarget && ltarget < cex + wl[0]) s_misc[2] = (int)(cb + 2 * tid);
-    if (wl[1] && cex + wl[0] <= ltarget && ltarget < cex + wl[0] + wl[1])
-      s_misc[2] = (int)(cb + 2 * tid + 1);
     __syncthreads();
-  }
-  const int token = cstar >= 0 ? s_misc[2] : -1;
-
-  // probe token (MTP acceptance): its kept weight
-  uint64_t probe_w = 0ull;
-  if (P.probe_tokens) {
-    const int32_t pt = P.probe_tokens[row];
-    if (tid == 0) s_misc[3] = 0;
-    __syncthreads();
-    if (pt >= 0 && pt < V && !overflow && active) {
-      for (int i = tid; i < nc; i += kThreads) {
-        if (!L.b.keep[i]) continue;
-        const int32_t id = (int32_t)(0xffffffffu - (uint32_t)(L.b.keys[i] & 0xffffffffull));
-        if (id == pt) s_misc[3] = 1;
-      }
-      __syncthreads();
-      if (tid == 0) {
-        float x = load_logit(DT, rowp, pt);
-        int32_t e0 = 0, e1 = 0;
-        if (P.row_ptr && P.entries) {
-          e0 = P.row_ptr[row];
-          e1 = P.row_ptr[row + 1];
-        }
-        for (int32_t e = e0; e < e1; ++e)
-          if (P.entries[e].token == pt) {
-            x = patch_value(c, prm, x, P.entries[e], DT);
-            break;
-          }
-        if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, pt) || x != x) x = kNegInf;
-        const int cls = classify(info, c, x);
-        if (cls == kKept || (cls == kCand && s_misc[3])) {
-          s_misc64[1] = weight(to_filter(c, x), y_max, c.scale);
-        } else {
-          s_misc64[1] = 0ull;
-        }
-      }
-      __syncthreads();
-      probe_w = s_misc64[1];
-    }
+    probe_w = L.misc64[2];
   }
 
   if (tid == 0) {
     uint32_t flags = info.flags;
     if (overflow) flags |= LSAMP_ROW_OVERFLOW;
     if (!overflow && (token < 0 || W == 0ull)) flags |= LSAMP_ROW_EMPTY;
-    P.tokens[row] = overflow ? -1 : token;
+    const int tok = overflow ? -1 : token;
+    P.tokens[row] = tok;
     if (P.row_flags) P.row_flags[row] = flags;
     if (P.stats) {
       lsamp_row_stats st;
       st.max_value = y_max;
-      st.log_normalizer = info.z > 0.0 ? (float)(log(info.z) + ((double)info.q_top - (double)y_max)) : 0.0f;
+      st.log_normalizer =
+          info.z > 0.0 ? (float)(log(info.z) + ((double)info.q_top - (double)y_max)) : 0.0f;
       st.kept = kept_all + kept_c;
-      st.token = overflow ? -1 : token;
+      st.token = tok;
       st.kept_weight = W;
       st.probe_weight = probe_w;
       st.cut_value = __builtin_fminf(min_all, cmin);
@@ -1078,42 +925,438 @@ __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P)
       st.probe_prob = W ? (float)((double)probe_w / (double)W) : 0.0f;
       P.stats[row] = st;
     }
-    RowInfo* ri = ws.rows + row;
-    ri->kept_cands = overflow ? 0 : kept_c;
+    ws.rows[row].kept_cands = overflow ? 0 : kept_c;
     ws.cand_count[row] = 0u;
     ws.arrive_select[row] = 0u;
+    if (fused) ws.arrive_stats[row] = 0u;
   }
+}
+
+// ================================================================ one task
+template <int DT, int MODE>
+__device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& P, int row, int slice,
+                         TaskLds& L) {
+  constexpr int N = Vec<DT>::N;
+  constexpr int NV = kElemsPerThread / N;
+  constexpr uint32_t FULL = (1u << N) - 1u;
+  const int tid = threadIdx.x;
+  const int G = P.slices;
+  const lsamp_row_params prm = P.params[row];
+  const RowCtx c = make_ctx(P.semantics, prm);
+  const int64_t V = P.vocab;
+  const int64_t base = (int64_t)slice * P.slice_len;
+  const int64_t end = (base + P.slice_len < V) ? base + P.slice_len : V;
+  const char* rowp = row_base(P, row);
+  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
+  const bool aligned = P.aligned != 0;
+
+  // ---------------------------------------------------- A: loads + entries
+  // Token positions within a row fit in 32 bits (vocab <= kMaxVocab).
+  const int32_t base32 = (int32_t)base, end32 = (int32_t)end;
+  uint4 raw[NV];
+  constexpr uint32_t NEG_WORD =
+      DT == LSAMP_DTYPE_F32 ? Vec<DT>::NEG_INF_BITS : Vec<DT>::NEG_INF_BITS * 0x10001u;
+  const int32_t tid_a = fresh_tid();
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int32_t i0 = base32 + (tid_a + k * kThreads) * N;
+    raw[k] = i0 < end32 ? load_vec<DT>(rowp, i0, end, aligned)
+                        : make_uint4(NEG_WORD, NEG_WORD, NEG_WORD, NEG_WORD);
+  }
+  if (MODE != kSelectOnly)
+    for (int i = tid; i < kHist; i += kThreads) L.u.hist[i] = 0ull;
+  if (tid == 0) L.flags = 0u;
+  SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
+  bool ent_overflow = false;
+  const int n_ent = build_slice_entries<DT>(P, c, prm, row, rowp, base, end, se, &ent_overflow);
+  // Masked tokens and tokens of the entry table (their patched values live in
+  // L.ex) become -inf in the register copy; lanes past the slice end already
+  // are.  From here on "excluded" is simply "not > -inf".
+  uint32_t fl = 0u;
+  const int32_t tid_x = fresh_tid();
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const int32_t i0 = base32 + (tid_x + k * kThreads) * N;
+    if (i0 >= end32) continue;
+    if (MODE != kSelectOnly) {
+      const int32_t nvalid = end32 - i0 < N ? end32 - i0 : N;
+#pragma unroll
+      for (int q = 0; q < N; ++q)
+        if (q < nvalid && !__builtin_isfinite(vec_elem<DT>(raw[k], q))) fl |= LSAMP_ROW_NONFINITE;
+    }
+    const uint32_t allow = mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N);
+    const int32_t li0 = i0 - base32;
+    const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
+    exclude_elems<DT>(raw[k], (~allow | pen) & FULL);
+  }
+
+  RowInfo info;
+  if (MODE != kSelectOnly) {
+    // ------------------------------------------------ B: max, histogram
+    float xmax = kNegInf;
+    int32_t nfin = 0;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+#pragma unroll
+      for (int q = 0; q < N; ++q) {
+        const float x = vec_elem<DT>(raw[k], q);
+        if (!(x > kNegInf)) continue;
+        if (x == kPosInf) {
+          fl |= kSlicePosInf;
+          continue;
+        }
+        xmax = __builtin_fmaxf(xmax, x);
+        ++nfin;
+      }
+    }
+    for (int j = tid; j < n_ent; j += kThreads) {
+      const float x = L.ex[j];
+      if (!(x > kNegInf)) continue;
+      if (x == kPosInf) {
+        fl |= kSlicePosInf;
+        continue;
+      }
+      xmax = __builtin_fmaxf(xmax, x);
+      ++nfin;
+    }
+    if (fl) atomicOr(&L.flags, fl);
+    xmax = block_max(xmax, L.redf);
+    nfin = block_sum(nfin, L.redi);
+    const uint32_t sflags = L.flags | (ent_overflow ? kSliceEntryOverflow : 0u);
+    const int32_t top = nfin > 0 ? bin_of(xmax, c.c32) : 0;
+    const bool want_hist = nfin > 0 && c.kind != LSAMP_KIND_ARGMAX;
+    opaque_regs(raw);
+    if (want_hist) {
+      const float Lg = 1.4426950408889634f / 32.0f;
+      const float tail_edge = (float)(top - kBins + 1);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+#pragma unroll
+        for (int q = 0; q < N; ++q) {
+          const float x = vec_elem<DT>(raw[k], q);
+          if (!(x > kNegInf) || x == kPosInf) continue;
+          const float s = bin_pos(x, c.c32);
+          const float fb = __builtin_floorf(s);
+          const int j = top - (int)fb;
+          const bool in_win = j < kBins;
+          const float e = __builtin_amdgcn_exp2f((s - (in_win ? fb : tail_edge)) * Lg + 30.0f);
+          atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.hist[in_win ? j : kTail]),
+                    (unsigned long long)((1ull << kCountShift) | (uint64_t)(uint32_t)e));
+        }
+      }
+      for (int j2 = tid; j2 < n_ent; j2 += kThreads) {
+        const float x = L.ex[j2];
+        if (!(x > kNegInf) || x == kPosInf) continue;
+        const float s = bin_pos(x, c.c32);
+        const float fb = __builtin_floorf(s);
+        const int j = top - (int)fb;
+        const bool in_win = j < kBins;
+        const float e = __builtin_amdgcn_exp2f((s - (in_win ? fb : tail_edge)) * Lg + 30.0f);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.hist[in_win ? j : kTail]),
+                  (unsigned long long)((1ull << kCountShift) | (uint64_t)(uint32_t)e));
+      }
+    }
+    __syncthreads();
+    if (P.processed) {
+      float* out = P.processed + (size_t)row * (size_t)V;
+      const int32_t tid_p = fresh_tid();
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        const int32_t i0 = base32 + (tid_p + k * kThreads) * N;
+        if (i0 >= end32) continue;
+        const int32_t li0 = i0 - base32;
+        const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
+#pragma unroll
+        for (int q = 0; q < N; ++q) {
+          if (i0 + q >= end32 || ((pen >> q) & 1u)) continue;
+          const float x = vec_elem<DT>(raw[k], q);
+          out[i0 + q] = (x != x) ? kNegInf : to_filter(c, x);
+        }
+      }
+      for (int j = tid; j < n_ent; j += kThreads) out[L.etok[j]] = to_filter(c, L.ex[j]);
+    }
+    // publish the slice summary
+    SliceSummary* S = ws.summaries + ((size_t)row * kMaxSlices + slice);
+    if (tid == 0) {
+      st_coherent_f32(&S->x_max, xmax);
+      st_coherent(&S->top_bin, top);
+      st_coherent(&S->flags, sflags);
+      st_coherent(&S->n_finite, nfin);
+    }
+    if (want_hist)
+      for (int i = tid; i < kHist; i += kThreads) st_coherent(&S->hist[i], L.u.hist[i]);
+    const bool is_last = arrive_last(&ws.arrive_stats[row], (uint32_t)G, &L.last);
+    if (is_last) {
+      merge_row(ws, P, row, c, prm, L);
+      info = L.info;
+      if (MODE == kFused) {
+        if (tid == 0) publish_rowinfo(ws.rows + row, info);
+        drain_memory();
+        __syncthreads();
+        if (tid == 0)
+          (void)__hip_atomic_fetch_add(&ws.arrive_stats[row], kReady, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        if (tid == 0) {
+          ws.rows[row] = info;
+          ws.arrive_stats[row] = 0u;
+        }
+        return;
+      }
+    } else {
+      if (MODE != kFused) return;
+      // wait for the row's merge (bounded: the grid always drains)
+      if (tid == 0) {
+        int it = 0;
+        while (ld_coherent(&ws.arrive_stats[row]) < kReady) {
+          if (++it >= kSpinLimit) {
+            atomicOr(ws.status, kStatusSpinTimeout);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(4);
+        }
+        L.info = read_rowinfo(ws.rows + row);
+      }
+      __syncthreads();
+      info = L.info;
+    }
+  } else {
+    if (tid == 0) L.info = ws.rows[row];
+    __syncthreads();
+    info = L.info;
+  }
+
+  // ------------------------------------------- C: classify against the cut
+  // values derived from the logits in phase B must not stay live across the
+  // wait: the select phase recomputes them from the packed registers
+  if (MODE == kFused) opaque_regs(raw);
+  const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
+  const bool active = info.mode != kModeEmpty;
+  if (tid < kSliceChunks) L.u.s.chunk[tid] = 0ull;
+  if (tid == 0) {
+    L.ncand = 0;
+    L.nlist = 0;
+  }
+  __syncthreads();
+  double ent = 0.0;
+  float min_kept = kPosInf;
+  int32_t n_kept = 0;
+  uint8_t* kout = P.keep ? P.keep + (size_t)row * (size_t)V : nullptr;
+  if (!active && kout)
+    for (int64_t i = base + tid; i < end; i += kThreads) kout[i] = 0;
+  // Kept tokens are listed (fast draw path) only when the whole row keeps at
+  // most kKeptCap tokens above the cut bin; otherwise the draw scans a chunk.
+  const bool list_on = info.count_above <= kKeptCap;
+  if (active) {
+    // The per-element body stays small so that the loop over the thread's
+    // vectors unrolls completely and raw[] stays in registers; the rare
+    // kept / candidate tokens are appended with per-lane LDS atomics.
+    const int32_t tid_c = fresh_tid();
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int32_t i0 = base32 + (tid_c + k * kThreads) * N;
+      uint64_t part = 0ull;
+      if (i0 < end32) {
+#pragma unroll
+        for (int q = 0; q < N; ++q) {
+          const float x = vec_elem<DT>(raw[k], q);
+          const int cls = classify(info, c, x);
+          if (cls == kKept) {
+            const float y = to_filter(c, x);
+            const uint64_t wq = weight(y, y_max, c.scale);
+            part += wq;
+            ent += (double)wq * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
+            min_kept = __builtin_fminf(min_kept, y);
+            ++n_kept;
+            if (list_on) {
+              const int ks = atomicAdd(&L.nlist, 1);
+              if (ks < kKeptCap) {
+                L.u.s.klist[ks].w = wq;
+                L.u.s.klist[ks].id = i0 + q;
+              }
+            }
+          } else if (cls == kCand) {
+            const int cs = atomicAdd(&L.ncand, 1);
+            if (cs < kWgCandCap) {
+              L.u.s.cand[cs].y = to_filter(c, x);
+              L.u.s.cand[cs].id = i0 + q;
+            }
+          }
+        }
+      }
+      // chunk sums: a wave's vectors lie in one 1024-token chunk
+      if (__ballot(part != 0ull)) {
+        const uint64_t sum = wave_sum(part);
+        if ((tid & 63) == 0) {
+          const int32_t wi0 = ((tid_c & ~63) + k * kThreads) * N;
+          atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.s.chunk[wi0 / kChunk]),
+                    (unsigned long long)sum);
+        }
+      }
+    }
+    if (kout) {
+      // keep bytes of tokens outside the entry table (re-read; an output for
+      // parity checks only); candidates' bytes are written by the finalize
+      const int32_t tid_k = fresh_tid();
+#pragma nounroll
+      for (int k = 0; k < NV; ++k) {
+        const int32_t i0 = base32 + (tid_k + k * kThreads) * N;
+        if (i0 >= end32) continue;
+        const int32_t li0 = i0 - base32;
+        const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
+        const uint32_t allow = mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N);
+#pragma nounroll
+        for (int q = 0; q < N && i0 + q < end32; ++q) {
+          if ((pen >> q) & 1u) continue;
+          const int cls = ((allow >> q) & 1u) ? classify(info, c, load_scalar<DT>(rowp, i0 + q)) : kDrop;
+          if (cls != kCand) kout[i0 + q] = cls == kKept ? 1 : 0;
+        }
+      }
+    }
+    for (int j2 = tid; j2 < n_ent; j2 += kThreads) {
+      const float x = L.ex[j2];
+      const int cls = classify(info, c, x);
+      const int32_t t = L.etok[j2];
+      if (kout && cls != kCand) kout[t] = cls == kKept ? 1 : 0;
+      if (cls == kKept) {
+        const float y = to_filter(c, x);
+        const uint64_t w = weight(y, y_max, c.scale);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.s.chunk[(t - base) / kChunk]),
+                  (unsigned long long)w);
+        ent += (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
+        min_kept = __builtin_fminf(min_kept, y);
+        ++n_kept;
+        if (list_on) {
+          const int ks = atomicAdd(&L.nlist, 1);
+          if (ks < kKeptCap) {
+            L.u.s.klist[ks].w = w;
+            L.u.s.klist[ks].id = t;
+          }
+        }
+      } else if (cls == kCand) {
+        const int cs = atomicAdd(&L.ncand, 1);
+        if (cs < kWgCandCap) {
+          L.u.s.cand[cs].y = to_filter(c, x);
+          L.u.s.cand[cs].id = t;
+        }
+      }
+    }
+  }
+  ent = block_sum(ent, L.redd);
+  min_kept = block_min(min_kept, L.redf);
+  n_kept = block_sum(n_kept, L.redi);
+
+  // publish chunk sums, candidates, kept list, partials
+  const int64_t chunk0 = base / kChunk;
+  const int nch = (int)((end - base + kChunk - 1) / kChunk);
+  uint64_t* rowchunks = ws.chunk_w + (size_t)row * (size_t)ws.max_chunks;
+  if (tid < nch) st_coherent(&rowchunks[chunk0 + tid], L.u.s.chunk[tid]);
+  const int ncand = L.ncand;
+  const int nlist = list_on ? L.nlist : kKeptCap + 1;
+  if (tid == 0)
+    L.misc[0] = ncand > 0 ? (int)__hip_atomic_fetch_add(&ws.cand_count[row], (uint32_t)ncand,
+                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : 0;
+  __syncthreads();
+  const int gbase = L.misc[0];
+  Candidate* rc = ws.cands + (size_t)row * kCandCap;
+  const int ncopy = ncand < kWgCandCap ? ncand : kWgCandCap;
+  for (int i = tid; i < ncopy; i += kThreads)
+    if (gbase + i < kCandCap) {
+      st_coherent_f32(&rc[gbase + i].y, L.u.s.cand[i].y);
+      st_coherent(&rc[gbase + i].id, L.u.s.cand[i].id);
+    }
+  KeptItem* kl = ws.klist + ((size_t)row * kMaxSlices + slice) * kKeptCap;
+  if (tid < nlist && tid < kKeptCap) {
+    st_coherent(&kl[tid].w, L.u.s.klist[tid].w);
+    st_coherent(&kl[tid].id, L.u.s.klist[tid].id);
+  }
+  if (tid == 0) {
+    SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + slice;
+    st_coherent_f64(&sp->ent, ent);
+    st_coherent_f32(&sp->min_kept, min_kept);
+    st_coherent(&sp->n_kept, n_kept);
+    st_coherent(&sp->n_cand, ncand);
+    st_coherent(&sp->n_list, nlist);
+    st_coherent(&sp->overflow, ent_overflow ? 1 : 0);
+  }
+  if (!arrive_last(&ws.arrive_select[row], (uint32_t)G, &L.last)) return;
+  finalize_row<DT>(ws, P, row, c, prm, info, L, rowp, mrow, MODE == kFused);
+}
+
+// ================================================================ kernels
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_fused(Workspace ws, SamplePlan P) {
+  __shared__ TaskLds L;
+  const int G = P.slices;
+  const int rowslot = (int)blockIdx.x / G;
+  const int slice = (int)blockIdx.x % G;
+  for (int r0 = 0; r0 < P.rows; r0 += P.rows_per_round) {
+    const int row = r0 + rowslot;
+    if (row < P.rows) run_task<DT, kFused>(ws, P, row, slice, L);
+    __syncthreads();
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_stats(Workspace ws, SamplePlan P) {
+  __shared__ TaskLds L;
+  run_task<DT, kStatsOnly>(ws, P, (int)blockIdx.y, (int)blockIdx.x, L);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P) {
+  __shared__ TaskLds L;
+  run_task<DT, kSelectOnly>(ws, P, (int)blockIdx.y, (int)blockIdx.x, L);
+}
+
+template <int DT>
+int launch_dt(const Workspace& ws, const SamplePlan& P, hipStream_t st, void* const* events) {
+  auto mark = [&](int i) {
+    if (events) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), st);
+  };
+  mark(0);
+  if (P.fused) {
+    const int rounds_rows = P.rows < P.rows_per_round ? P.rows : P.rows_per_round;
+    hipLaunchKernelGGL(k_fused<DT>, dim3((unsigned)(rounds_rows * P.slices)), dim3(kThreads), 0, st,
+                       ws, P);
+    mark(1);
+  } else {
+    const dim3 grid((unsigned)P.slices, (unsigned)P.rows);
+    hipLaunchKernelGGL(k_stats<DT>, grid, dim3(kThreads), 0, st, ws, P);
+    mark(1);
+    hipLaunchKernelGGL(k_select<DT>, grid, dim3(kThreads), 0, st, ws, P);
+  }
+  mark(2);
+  return (int)hipGetLastError();
 }
 
 }  // namespace
 
 int launch_sample(const Workspace& ws, const SamplePlan& P, void* stream, void* const* events) {
-  const dim3 grid((unsigned)P.slices, (unsigned)P.rows);
-  const dim3 block(kThreads);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  auto mark = [&](int i) {
-    if (events) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), st);
-  };
-  mark(0);
   switch (P.dtype) {
+    case LSAMP_DTYPE_F32: return launch_dt<LSAMP_DTYPE_F32>(ws, P, st, events);
+    case LSAMP_DTYPE_BF16: return launch_dt<LSAMP_DTYPE_BF16>(ws, P, st, events);
+    default: return launch_dt<LSAMP_DTYPE_F16>(ws, P, st, events);
+  }
+}
+
+int fused_blocks_per_cu(int dtype) {
+  int n = 0;
+  hipError_t e;
+  switch (dtype) {
     case LSAMP_DTYPE_F32:
-      hipLaunchKernelGGL(k_stats<LSAMP_DTYPE_F32>, grid, block, 0, st, ws, P);
-      mark(1);
-      hipLaunchKernelGGL(k_select<LSAMP_DTYPE_F32>, grid, block, 0, st, ws, P);
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_F32>, kThreads, 0);
       break;
     case LSAMP_DTYPE_BF16:
-      hipLaunchKernelGGL(k_stats<LSAMP_DTYPE_BF16>, grid, block, 0, st, ws, P);
-      mark(1);
-      hipLaunchKernelGGL(k_select<LSAMP_DTYPE_BF16>, grid, block, 0, st, ws, P);
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_BF16>, kThreads, 0);
       break;
     default:
-      hipLaunchKernelGGL(k_stats<LSAMP_DTYPE_F16>, grid, block, 0, st, ws, P);
-      mark(1);
-      hipLaunchKernelGGL(k_select<LSAMP_DTYPE_F16>, grid, block, 0, st, ws, P);
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_F16>, kThreads, 0);
       break;
   }
-  mark(2);
-  return (int)hipGetLastError();
+  return e == hipSuccess ? n : 0;
 }
 
 }  // namespace lsamp

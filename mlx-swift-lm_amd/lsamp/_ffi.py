@@ -30,6 +30,8 @@ MASK_TAIL_KEEP, MASK_TAIL_FORBID = 0, 1
 PEN_REPETITION, PEN_PRESENCE = 1, 2
 ROW_NONFINITE, ROW_EMPTY, ROW_OVERFLOW = 1, 2, 4
 VERIFY_RESIDUAL, VERIFY_EXACT, VERIFY_TYPICAL = 0, 1, 2
+MODE_AUTO, MODE_FUSED, MODE_SPLIT = 0, 1, 2
+STATUS_SPIN_TIMEOUT = 1
 
 
 class RowParams(Structure):
@@ -173,6 +175,10 @@ def load_library(path: str | None = None):
     lib.lsamp_context_destroy.restype = None
     lib.lsamp_sample.argtypes = [c_void_p, POINTER(SampleArgs), c_void_p]
     lib.lsamp_sample.restype = c_int32
+    lib.lsamp_context_set_mode.argtypes = [c_void_p, c_int32]
+    lib.lsamp_context_set_mode.restype = c_int32
+    lib.lsamp_context_read_status.argtypes = [c_void_p, POINTER(c_uint32)]
+    lib.lsamp_context_read_status.restype = c_int32
     lib.lsamp_context_set_timing.argtypes = [c_void_p, c_int32]
     lib.lsamp_context_set_timing.restype = c_int32
     lib.lsamp_context_read_timing.argtypes = [c_void_p, POINTER(c_double), POINTER(c_double),

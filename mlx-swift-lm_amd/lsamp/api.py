@@ -84,6 +84,16 @@ class Context:
         except Exception:
             pass
 
+    def set_mode(self, mode: int) -> None:
+        """_ffi.MODE_AUTO / MODE_FUSED / MODE_SPLIT."""
+        _ffi.check(self.lib.lsamp_context_set_mode(self.handle, mode), "lsamp_context_set_mode")
+
+    def read_status(self) -> int:
+        v = ctypes.c_uint32()
+        _ffi.check(self.lib.lsamp_context_read_status(self.handle, ctypes.byref(v)),
+                   "lsamp_context_read_status")
+        return v.value
+
     # ----------------------------------------------------------------- timing
     def set_timing(self, enable: bool) -> None:
         _ffi.check(self.lib.lsamp_context_set_timing(self.handle, 1 if enable else 0),

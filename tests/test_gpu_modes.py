@@ -1,0 +1,78 @@
+"""The two execution modes of lsamp_sample agree bit for bit.
+
+Fused mode runs the whole step as one co-resident kernel whose work-groups
+wait for their row's histogram merge; split mode runs it as two kernels.  Both
+must give identical tokens, flags, processed logits, keep sets and statistics
+(integer histogram and weight sums make the result independent of the order in
+which work-groups finish), and a fused step must never leave the device's
+spin-timeout status bit set.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from common import run_gpu
+from lsamp import _ffi
+from lsamp import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    import torch
+    from lsamp.api import Context
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    c = Context(0, max_rows=512, max_vocab=262144)
+    yield c
+    c.close()
+
+
+def _both_modes(ctx, cfg):
+    outs = {}
+    for mode in (_ffi.MODE_FUSED, _ffi.MODE_SPLIT):
+        ctx.set_mode(mode)
+        try:
+            outs[mode] = run_gpu(ctx, cfg)
+        finally:
+            ctx.set_mode(_ffi.MODE_AUTO)
+        assert ctx.read_status() == 0, f"device status bits set after mode {mode}"
+    return outs[_ffi.MODE_FUSED], outs[_ffi.MODE_SPLIT]
+
+
+def _assert_same(a, b, label):
+    assert np.array_equal(a["tokens"], b["tokens"]), f"{label}: tokens differ"
+    assert np.array_equal(a["row_flags"], b["row_flags"]), f"{label}: flags differ"
+    assert np.array_equal(a["processed"].view(np.uint32), b["processed"].view(np.uint32)), \
+        f"{label}: processed logits differ"
+    assert np.array_equal(a["keep"], b["keep"]), f"{label}: keep sets differ"
+    assert a["stats"].tobytes() == b["stats"].tobytes(), f"{label}: stats differ"
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4])
+def test_fused_equals_split_full_configs(ctx, n):
+    cfg = W.CONFIGS[n]()
+    f, s = _both_modes(ctx, cfg)
+    _assert_same(f, s, f"config{n}")
+
+
+def test_fused_equals_split_many_rounds(ctx):
+    # 512 rows of a 40,001-token vocabulary: several rounds of the fused grid
+    rng = np.random.default_rng(21)
+    V, B = 40001, 512
+    x = rng.normal(0, 3, (B, V)).astype(np.float32)
+    params = [W.resolve_cbv2(temperature=[0.0, 0.7, 1.0, 1.3][r % 4],
+                             top_k=[0, 40, 5, 400][(r // 4) % 4],
+                             top_p=[1.0, 0.9, 0.5][r % 3], min_p=[0.0, 0.05][r % 2], vocab=V)
+              for r in range(B)]
+    cfg = dict(semantics=_ffi.SEM_CBV2, dtype=_ffi.DTYPE_F32, rows=B, vocab=V, logits=x,
+               params=W._params(params), uniforms=rng.random(B, dtype=np.float32))
+    f, s = _both_modes(ctx, cfg)
+    _assert_same(f, s, "many rounds")
+
+
+def test_status_clear_after_default_mode(ctx):
+    cfg = W.config2(rows=16)
+    run_gpu(ctx, cfg)
+    assert ctx.read_status() == 0
