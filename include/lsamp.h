@@ -236,10 +236,11 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* args, voi
 /* Per-kernel timing hook, off by default (the role CBv2StepProfiler plays for
  * the reference, StepProfilerV2.swift:15-60).  While enabled, each
  * lsamp_sample call that is not under graph capture records three HIP events
- * on its stream: before the stats kernel, between the two kernels, after the
- * select kernel (up to 4096 calls).  lsamp_context_read_timing waits for them,
- * returns the summed milliseconds per kernel and the number of timed calls,
- * and starts a new window. */
+ * on its stream: before the first kernel, after it, and after the second
+ * kernel of a split step (a fused step has one kernel: its second interval is
+ * empty), up to 4096 calls.  lsamp_context_read_timing waits for them,
+ * returns the summed milliseconds of the two intervals and the number of
+ * timed calls, and starts a new window. */
 lsamp_status lsamp_context_set_timing(lsamp_context* ctx, int32_t enable);
 lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, double* select_ms,
                                        int64_t* calls);
@@ -260,6 +261,18 @@ lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode);
  * outputs are unreliable. */
 #define LSAMP_STATUS_SPIN_TIMEOUT 1u
 lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
+
+/* Launch shape of the context's last lsamp_sample call (diagnostics; no
+ * device work): fused (1) or split (0), slices per row, tokens per slice,
+ * rows per round of the fused grid, work-groups per kernel launch. */
+typedef struct lsamp_launch_info {
+  int32_t fused;
+  int32_t slices;
+  int32_t slice_len;
+  int32_t rows_per_round;
+  int32_t grid;
+} lsamp_launch_info;
+lsamp_status lsamp_context_last_launch(lsamp_context* ctx, lsamp_launch_info* out);
 
 /* Enqueue one MTP verification on `stream`. */
 lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* args, void* stream);

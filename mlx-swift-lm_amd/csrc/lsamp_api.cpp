@@ -64,6 +64,7 @@ struct lsamp_context {
   bool timing = false;
   int timed = 0;
   hipEvent_t* events = nullptr;  // [kTimedCalls * 3]
+  lsamp_launch_info last{};      // shape of the last sample launch
 };
 
 namespace {
@@ -230,6 +231,12 @@ lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits) {
   return ok();
 }
 
+lsamp_status lsamp_context_last_launch(lsamp_context* ctx, lsamp_launch_info* out) {
+  if (!ctx || !out) return fail(LSAMP_ERR_INVALID_ARGUMENT, "NULL argument");
+  *out = ctx->last;
+  return ok();
+}
+
 lsamp_status lsamp_context_set_timing(lsamp_context* ctx, int32_t enable) {
   if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
   DeviceGuard guard(ctx->device);
@@ -343,6 +350,12 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
       ++ctx->timed;
     }
   }
+  ctx->last.fused = P.fused;
+  ctx->last.slices = P.slices;
+  ctx->last.slice_len = P.slice_len;
+  ctx->last.rows_per_round = P.rows_per_round;
+  ctx->last.grid = P.fused ? (P.rows < P.rows_per_round ? P.rows : P.rows_per_round) * P.slices
+                           : P.rows * P.slices;
   const int err = launch_sample(ctx->ws, P, stream, ev);
   if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                             hipGetErrorString((hipError_t)err));

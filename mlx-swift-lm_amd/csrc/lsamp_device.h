@@ -43,6 +43,23 @@ __device__ __forceinline__ float vec_elem(const uint4& r, int k) {
   }
 }
 
+// Element e of a 16-byte vector, e not known at compile time.
+template <int DT>
+__device__ __forceinline__ float vec_elem_dyn(const uint4& r, int e) {
+  if constexpr (DT == LSAMP_DTYPE_F32) {
+    const uint32_t v = e == 0 ? r.x : (e == 1 ? r.y : (e == 2 ? r.z : r.w));
+    return __uint_as_float(v);
+  } else {
+    const int q = e >> 1;
+    const uint32_t word = q == 0 ? r.x : (q == 1 ? r.y : (q == 2 ? r.z : r.w));
+    const uint32_t h = (e & 1) ? (word >> 16) : (word & 0xffffu);
+    if constexpr (DT == LSAMP_DTYPE_BF16)
+      return __uint_as_float(h << 16);
+    else
+      return half_bits_to_f32(h);
+  }
+}
+
 // Replace the elements of a 16-byte vector whose bit is set in `excl` by -inf
 // (branch-free: one mask per 32-bit word).
 template <int DT>

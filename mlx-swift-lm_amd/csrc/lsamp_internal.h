@@ -10,26 +10,26 @@ namespace lsamp {
 
 // Work-group shape: one 512-thread work-group (8 wave64s, up to 256 VGPRs per
 // lane) owns one slice of one row and holds the slice's logits in registers,
-// 80 per thread at most (10 bf16 or 20 fp32 16-byte vectors).
+// 128 per thread at most (two 32-dword banks of 16-bit logits, four of fp32).
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kElemsPerThread = 80;
-constexpr int kMaxSliceLen = kThreads * kElemsPerThread;  // 40960 tokens
+constexpr int kElemsPerThread = 128;
+constexpr int kMaxSliceLen = kThreads * kElemsPerThread;  // 65536 tokens
 constexpr int kChunk = 1024;                              // draw granularity (tokens)
-constexpr int kMaxSlices = 12;                            // slices per row
-constexpr int kMaxVocab = kMaxSlices * kMaxSliceLen;      // 491520
-constexpr int kMaxRowChunks = kMaxVocab / kChunk;         // 480 <= one per thread
-constexpr int kSliceChunks = kMaxSliceLen / kChunk;       // 40
+constexpr int kMaxSlices = 8;                             // slices per row
+constexpr int kMaxVocab = kMaxSlices * kMaxSliceLen;      // 524288
+constexpr int kMaxRowChunks = kMaxVocab / kChunk;         // 512 <= one per thread
+constexpr int kSliceChunks = kMaxSliceLen / kChunk;       // 64
 // Histogram: bins of 1/32 nat of the filter-space logit, kBins of them below
 // the slice's top bin (a 32-nat window), plus one tail bin for the rest.
 constexpr int kBins = 1024;
 constexpr int kTail = kBins;
 constexpr int kHist = kBins + 1;
 // Packed histogram word of a slice: count in bits 46..63, fixed-point mass in
-// 0..45 (mass = sum exp(q - bin edge) * 2^30 < 2^46 for <= 40960 tokens).
+// 0..45 (mass = sum exp(q - bin edge) * 2^29 <= 65536 * e^(1/32) * 2^29 < 2^46).
 constexpr int kCountShift = 46;
 constexpr uint64_t kMassMask = (1ull << kCountShift) - 1;
-constexpr int kMassFracBits = 30;
+constexpr int kMassFracBits = 29;
 // Candidates (tokens in the cut bin) per row, and per work-group in LDS.
 constexpr int kCandCap = 4096;
 constexpr int kWgCandCap = 2048;
@@ -58,7 +58,8 @@ struct SliceSummary {
   float x_max;       // largest finite transformed logit (pre-temperature)
   int32_t top_bin;   // bin of x_max
   uint32_t flags;    // LSAMP_ROW_NONFINITE | kSlice*
-  int32_t n_finite;  // tokens with a finite transformed logit
+  int32_t n_finite;  // histogram token count; without a histogram, 1 when the
+                     // slice holds a finite (or +inf) transformed logit
   uint64_t hist[kHist];
 };
 

@@ -150,38 +150,65 @@ __device__ __forceinline__ float load_logit(int dt, const char* rowp, int64_t i)
   return load_scalar<LSAMP_DTYPE_F16>(rowp, i);
 }
 
-// The thread index through an empty asm statement: index arithmetic derived
-// from it cannot be merged with that of another phase, so per-element
-// conditions (lane masks) are recomputed where used instead of being kept
-// live across the phase boundary.
-__device__ __forceinline__ int32_t fresh_tid() {
-  int32_t t = (int32_t)threadIdx.x;
+// The thread index through an empty asm statement: values derived from it
+// cannot be hoisted out of the fused kernel's loop over rounds (where they
+// would stay live, and spill, across the whole task).
+__device__ __forceinline__ int fresh_tid() {
+  int t = (int)threadIdx.x;
   asm volatile("" : "+v"(t));
   return t;
-}
-
-// Makes the register copy of the logits opaque: values derived from it
-// (converted floats, comparisons) are recomputed after this point rather than
-// kept live.  Used only where the registers have already been consumed.
-template <int NV>
-__device__ __forceinline__ void opaque_regs(uint4 (&raw)[NV]) {
-#pragma unroll
-  for (int k = 0; k < NV; ++k)
-    asm volatile("" : "+v"(raw[k].x), "+v"(raw[k].y), "+v"(raw[k].z), "+v"(raw[k].w));
 }
 
 // Token classes relative to the row's cut.
 constexpr int kDrop = 0, kKept = 1, kCand = 2;
 
-__device__ __forceinline__ int classify(const RowInfo& info, const RowCtx& c, float x) {
-  if (info.mode == kModePosInf) return x == kPosInf ? kKept : kDrop;
-  if (!(x > kNegInf) || x == kPosInf) return kDrop;
-  if (info.mode != kModeNormal) return kDrop;
-  if (info.cut == kCutNone) return kKept;
-  int j = info.top_bin - bin_of(x, c.c32);
-  if (j > kBins || j < 0) j = j < 0 ? 0 : kBins;
-  if (info.cut == kCutTail) return j < kBins ? kKept : kCand;
-  return j < info.cut ? kKept : (j == info.cut ? kCand : kDrop);
+// Classification rule of a row, resolved once per task: with
+// j = top - floor(x * c32) (clamped at 0), a finite token is kept when
+// j < kc and a candidate when kc <= j < kd; in +inf mode exactly the +inf
+// tokens are kept.
+struct ClassRule {
+  int32_t top, kc, kd;
+  float c32;
+  float screen;  // x * c32 < screen: neither kept nor candidate
+  bool posinf;
+};
+
+__device__ __forceinline__ ClassRule make_rule(const RowInfo& info, const RowCtx& c) {
+  ClassRule r;
+  r.top = info.top_bin;
+  r.c32 = c.c32;
+  r.posinf = info.mode == kModePosInf;
+  if (info.mode != kModeNormal) {
+    r.kc = r.kd = -1;
+  } else if (info.cut == kCutNone) {
+    r.kc = r.kd = 0x7fffffff;
+  } else if (info.cut == kCutTail) {
+    r.kc = kBins;
+    r.kd = 0x7fffffff;
+  } else {
+    r.kc = info.cut;
+    r.kd = info.cut + 1;
+  }
+  // j < kd  <=>  floor(clamp(s)) >= top - kd + 1 =: n, implied by s >= n when
+  // n > -1e9; the threshold is n rounded up to a float (s is a float).
+  const int64_t n = (int64_t)r.top - (int64_t)r.kd + 1;
+  if (r.posinf)
+    r.screen = kPosInf;
+  else if (r.kd < 0)
+    r.screen = __builtin_nanf("");
+  else if (n <= -1000000000ll)
+    r.screen = -__FLT_MAX__;
+  else
+    r.screen = __int2float_ru((int)(n > 1000000001ll ? 1000000001ll : n));
+  return r;
+}
+
+__device__ __forceinline__ int classify(const ClassRule& r, float x) {
+  if (r.posinf) return x == kPosInf ? kKept : kDrop;
+  if (!__builtin_isfinite(x)) return kDrop;
+  int j = r.top - bin_of(x, r.c32);
+  j = j < 0 ? 0 : j;
+  return j < r.kc ? kKept : (j < r.kd ? kCand : kDrop);
 }
 
 // Penalty bitmap of the slice + the slice's entries, patched.  Shared by both
@@ -853,7 +880,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
         const int64_t i = cb + li;
         if (i >= ce) continue;
         const float x = token_value<DT>(P, c, prm, row, rowp, mrow, i, &F.cx[li], &F.cent[li]);
-        const int cls = classify(info, c, x);
+        const int cls = classify(make_rule(info, c), x);
         if (cls == kKept || (cls == kCand && F.cflag[li]))
           wl[u] = weight(to_filter(c, x), y_max, c.scale);
       }
@@ -893,7 +920,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
     if (tid == 0) {
       float x = L.misc[5] ? F.cx[0] : load_scalar<DT>(rowp, probe);
       if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, probe) || x != x) x = kNegInf;
-      const int cls = classify(info, c, x);
+      const int cls = classify(make_rule(info, c), x);
       L.misc64[2] = (cls == kKept || (cls == kCand && L.misc[4]))
                         ? weight(to_filter(c, x), y_max, c.scale)
                         : 0ull;
@@ -933,13 +960,72 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
 }
 
 // ================================================================ one task
+// Register copy of one thread's share of a slice: banks of 32 dwords (8
+// quads of 16 bytes).  The loops over quads stay rolled, indexing a bank with
+// the uniform loop counter (register-relative moves), so each pass over the
+// slice is a short loop body instead of straight-line code per token.
+typedef uint32_t bank_t __attribute__((ext_vector_type(32)));
+constexpr int kQuadsPerBank = 8;
+
+template <int DT>
+struct Slab {
+  static constexpr int N = Vec<DT>::N;                  // tokens per quad
+  static constexpr int Q = kElemsPerThread / N;         // quads per thread
+  static constexpr int NB = Q / kQuadsPerBank;          // banks
+  static_assert(Q % kQuadsPerBank == 0, "whole banks");
+  bank_t bank[NB];
+};
+
+__device__ __forceinline__ uint4 quad_get(const bank_t& b, int s) {
+  return make_uint4(b[4 * s], b[4 * s + 1], b[4 * s + 2], b[4 * s + 3]);
+}
+__device__ __forceinline__ void quad_set(bank_t& b, int s, const uint4& v) {
+  b[4 * s] = v.x;
+  b[4 * s + 1] = v.y;
+  b[4 * s + 2] = v.z;
+  b[4 * s + 3] = v.w;
+}
+
+// f(g, v) for the thread's quads g < nq (g is uniform); when f returns true
+// the quad is written back.
+template <int DT, typename F>
+__device__ __forceinline__ void for_quads(Slab<DT>& S, int nq, F&& f) {
+#pragma unroll
+  for (int b = 0; b < Slab<DT>::NB; ++b) {
+    const int n = nq - b * kQuadsPerBank;
+    if (n <= 0) break;
+    const int m = n < kQuadsPerBank ? n : kQuadsPerBank;
+#pragma unroll 1
+    for (int s = 0; s < m; ++s) {
+      uint4 v = quad_get(S.bank[b], s);
+      if (f(b * kQuadsPerBank + s, v)) quad_set(S.bank[b], s, v);
+    }
+  }
+}
+
+// Accumulates a probe of the quad's exponent fields: bit 15 / 31 (16-bit
+// types) or bit 31 (fp32) of the result is set when some element is inf/NaN.
+template <int DT>
+__device__ __forceinline__ uint32_t nonfinite_probe(const uint4& v) {
+  constexpr uint32_t M = DT == LSAMP_DTYPE_F32 ? 0x7f800000u
+                                               : (DT == LSAMP_DTYPE_BF16 ? 0x7f807f80u : 0x7c007c00u);
+  constexpr uint32_t A = DT == LSAMP_DTYPE_F32 ? 0x00800000u
+                                               : (DT == LSAMP_DTYPE_BF16 ? 0x00800080u : 0x04000400u);
+  return ((v.x & M) + A) | ((v.y & M) + A) | ((v.z & M) + A) | ((v.w & M) + A);
+}
+template <int DT>
+__device__ __forceinline__ bool nonfinite_seen(uint32_t acc) {
+  return (acc & (DT == LSAMP_DTYPE_F32 ? 0x80000000u : 0x80008000u)) != 0u;
+}
+
 template <int DT, int MODE>
 __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& P, int row, int slice,
-                         TaskLds& L) {
+                                         TaskLds& L) {
   constexpr int N = Vec<DT>::N;
-  constexpr int NV = kElemsPerThread / N;
+  constexpr int Q = Slab<DT>::Q;
   constexpr uint32_t FULL = (1u << N) - 1u;
-  const int tid = threadIdx.x;
+  constexpr int ES = Vec<DT>::ESIZE;
+  const int tid = fresh_tid();
   const int G = P.slices;
   const lsamp_row_params prm = P.params[row];
   const RowCtx c = make_ctx(P.semantics, prm);
@@ -949,19 +1035,42 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   const char* rowp = row_base(P, row);
   const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
   const bool aligned = P.aligned != 0;
-
-  // ---------------------------------------------------- A: loads + entries
   // Token positions within a row fit in 32 bits (vocab <= kMaxVocab).
   const int32_t base32 = (int32_t)base, end32 = (int32_t)end;
-  uint4 raw[NV];
-  constexpr uint32_t NEG_WORD =
-      DT == LSAMP_DTYPE_F32 ? Vec<DT>::NEG_INF_BITS : Vec<DT>::NEG_INF_BITS * 0x10001u;
-  const int32_t tid_a = fresh_tid();
+  const int nq = (P.slice_len + kThreads * N - 1) / (kThreads * N);  // quads per thread
+
+  // ---------------------------------------------------- A: loads + entries
+  // Aligned whole quads are read as 16-byte vectors, all in flight at once;
+  // lanes past the slice end read as zero until the exclusion pass.
+  // (uniform base address per quad + the lane's 32-bit byte offset)
+  Slab<DT> S;
+  const uint32_t lane_off = (uint32_t)tid * 16u;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int32_t i0 = base32 + (tid_a + k * kThreads) * N;
-    raw[k] = i0 < end32 ? load_vec<DT>(rowp, i0, end, aligned)
-                        : make_uint4(NEG_WORD, NEG_WORD, NEG_WORD, NEG_WORD);
+  for (int g = 0; g < Q; ++g) {
+    if (g < nq) {
+      const int32_t i0 = base32 + (tid + g * kThreads) * N;
+      const char* qbase = rowp + ((size_t)base32 + (size_t)g * kThreads * N) * ES;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (aligned && i0 + N <= end32) v = *reinterpret_cast<const uint4*>(qbase + lane_off);
+      quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, v);
+    }
+  }
+  if (!aligned || (end32 & (N - 1)) != 0) {
+    // unaligned rows, or the row's last partial quad: element by element
+    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+      const int32_t i0 = base32 + (tid + g * kThreads) * N;
+      if (i0 >= end32 || (aligned && i0 + N <= end32)) return false;
+      uint32_t b[N];
+#pragma unroll
+      for (int e = 0; e < N; ++e) b[e] = i0 + e < end32 ? load_raw_bits<DT>(rowp, i0 + e) : 0u;
+      if constexpr (N == 4) {
+        v = make_uint4(b[0], b[1], b[2], b[3]);
+      } else {
+        v = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
+                       b[6] | (b[7] << 16));
+      }
+      return true;
+    });
   }
   if (MODE != kSelectOnly)
     for (int i = tid; i < kHist; i += kThreads) L.u.hist[i] = 0ull;
@@ -969,122 +1078,117 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
   bool ent_overflow = false;
   const int n_ent = build_slice_entries<DT>(P, c, prm, row, rowp, base, end, se, &ent_overflow);
-  // Masked tokens and tokens of the entry table (their patched values live in
-  // L.ex) become -inf in the register copy; lanes past the slice end already
-  // are.  From here on "excluded" is simply "not > -inf".
-  uint32_t fl = 0u;
-  const int32_t tid_x = fresh_tid();
-#pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int32_t i0 = base32 + (tid_x + k * kThreads) * N;
-    if (i0 >= end32) continue;
-    if (MODE != kSelectOnly) {
-      const int32_t nvalid = end32 - i0 < N ? end32 - i0 : N;
-#pragma unroll
-      for (int q = 0; q < N; ++q)
-        if (q < nvalid && !__builtin_isfinite(vec_elem<DT>(raw[k], q))) fl |= LSAMP_ROW_NONFINITE;
+
+  // Masked tokens, tokens of the entry table (their patched values live in
+  // L.ex) and lanes past the slice end become -inf in the register copy, and
+  // so do NaNs.  From here on "excluded" is simply "not > -inf".  The same
+  // pass takes the thread's maximum.
+  uint32_t nf_acc = 0u;
+  float xmax = kNegInf;
+  for_quads(S, nq, [&](int g, uint4& v) -> bool {
+    const int32_t i0 = base32 + (tid + g * kThreads) * N;
+    const uint32_t probe = nonfinite_probe<DT>(v);
+    nf_acc |= probe;
+    uint32_t ex = FULL;
+    if (i0 < end32) {
+      const int32_t nvalid = end32 - i0;
+      const uint32_t valid = nvalid >= N ? FULL : ((1u << nvalid) - 1u);
+      const uint32_t allow = mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N);
+      const int32_t li0 = i0 - base32;
+      const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
+      ex = (~allow | pen | ~valid) & FULL;
     }
-    const uint32_t allow = mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N);
-    const int32_t li0 = i0 - base32;
-    const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
-    exclude_elems<DT>(raw[k], (~allow | pen) & FULL);
-  }
+    if (nonfinite_seen<DT>(probe)) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float x = vec_elem<DT>(v, e);
+        if (x != x) ex |= 1u << e;
+      }
+    }
+    if (ex != 0u) exclude_elems<DT>(v, ex);
+    if (MODE != kSelectOnly) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) xmax = __builtin_fmaxf(xmax, vec_elem<DT>(v, e));
+    }
+    return ex != 0u;
+  });
+  const bool nonfinite = nonfinite_seen<DT>(nf_acc);
 
   RowInfo info;
   if (MODE != kSelectOnly) {
     // ------------------------------------------------ B: max, histogram
-    float xmax = kNegInf;
-    int32_t nfin = 0;
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-#pragma unroll
-      for (int q = 0; q < N; ++q) {
-        const float x = vec_elem<DT>(raw[k], q);
-        if (!(x > kNegInf)) continue;
-        if (x == kPosInf) {
-          fl |= kSlicePosInf;
-          continue;
-        }
-        xmax = __builtin_fmaxf(xmax, x);
-        ++nfin;
-      }
-    }
-    for (int j = tid; j < n_ent; j += kThreads) {
-      const float x = L.ex[j];
-      if (!(x > kNegInf)) continue;
-      if (x == kPosInf) {
-        fl |= kSlicePosInf;
-        continue;
-      }
-      xmax = __builtin_fmaxf(xmax, x);
-      ++nfin;
-    }
-    if (fl) atomicOr(&L.flags, fl);
+    for (int j = tid; j < n_ent; j += kThreads) xmax = __builtin_fmaxf(xmax, L.ex[j]);
+    if (nonfinite) atomicOr(&L.flags, LSAMP_ROW_NONFINITE);
     xmax = block_max(xmax, L.redf);
-    nfin = block_sum(nfin, L.redi);
-    const uint32_t sflags = L.flags | (ent_overflow ? kSliceEntryOverflow : 0u);
-    const int32_t top = nfin > 0 ? bin_of(xmax, c.c32) : 0;
-    const bool want_hist = nfin > 0 && c.kind != LSAMP_KIND_ARGMAX;
-    opaque_regs(raw);
+    const bool posinf = xmax == kPosInf;
+    const bool has_finite = xmax > kNegInf && !posinf;
+    const uint32_t sflags = L.flags | (ent_overflow ? kSliceEntryOverflow : 0u) |
+                            (posinf ? kSlicePosInf : 0u);
+    const int32_t top = has_finite ? bin_of(xmax, c.c32) : 0;
+    const bool want_hist = has_finite && c.kind != LSAMP_KIND_ARGMAX;
     if (want_hist) {
       const float Lg = 1.4426950408889634f / 32.0f;
       const float tail_edge = (float)(top - kBins + 1);
-#pragma unroll
-      for (int k = 0; k < NV; ++k) {
-#pragma unroll
-        for (int q = 0; q < N; ++q) {
-          const float x = vec_elem<DT>(raw[k], q);
-          if (!(x > kNegInf) || x == kPosInf) continue;
-          const float s = bin_pos(x, c.c32);
-          const float fb = __builtin_floorf(s);
-          const int j = top - (int)fb;
-          const bool in_win = j < kBins;
-          const float e = __builtin_amdgcn_exp2f((s - (in_win ? fb : tail_edge)) * Lg + 30.0f);
-          atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.hist[in_win ? j : kTail]),
-                    (unsigned long long)((1ull << kCountShift) | (uint64_t)(uint32_t)e));
-        }
-      }
-      for (int j2 = tid; j2 < n_ent; j2 += kThreads) {
-        const float x = L.ex[j2];
-        if (!(x > kNegInf) || x == kPosInf) continue;
+      auto add = [&](float x) {
         const float s = bin_pos(x, c.c32);
         const float fb = __builtin_floorf(s);
         const int j = top - (int)fb;
         const bool in_win = j < kBins;
-        const float e = __builtin_amdgcn_exp2f((s - (in_win ? fb : tail_edge)) * Lg + 30.0f);
+        const float e =
+            __builtin_amdgcn_exp2f((s - (in_win ? fb : tail_edge)) * Lg + (float)kMassFracBits);
         atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.hist[in_win ? j : kTail]),
                   (unsigned long long)((1ull << kCountShift) | (uint64_t)(uint32_t)e));
+      };
+      for_quads(S, nq, [&](int g, uint4& v) -> bool {
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          const float x = vec_elem<DT>(v, e);
+          if (x > kNegInf) add(x);
+        }
+        return false;
+      });
+      for (int j2 = tid; j2 < n_ent; j2 += kThreads) {
+        const float x = L.ex[j2];
+        if (x > kNegInf && x != kPosInf) add(x);
       }
     }
     __syncthreads();
     if (P.processed) {
       float* out = P.processed + (size_t)row * (size_t)V;
-      const int32_t tid_p = fresh_tid();
-#pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        const int32_t i0 = base32 + (tid_p + k * kThreads) * N;
-        if (i0 >= end32) continue;
+      for_quads(S, nq, [&](int g, uint4& v) -> bool {
+        const int32_t i0 = base32 + (tid + g * kThreads) * N;
+        if (i0 >= end32) return false;
         const int32_t li0 = i0 - base32;
         const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
 #pragma unroll
-        for (int q = 0; q < N; ++q) {
-          if (i0 + q >= end32 || ((pen >> q) & 1u)) continue;
-          const float x = vec_elem<DT>(raw[k], q);
-          out[i0 + q] = (x != x) ? kNegInf : to_filter(c, x);
+        for (int e = 0; e < N; ++e) {
+          if (i0 + e >= end32 || ((pen >> e) & 1u)) continue;
+          out[i0 + e] = to_filter(c, vec_elem<DT>(v, e));
         }
-      }
+        return false;
+      });
       for (int j = tid; j < n_ent; j += kThreads) out[L.etok[j]] = to_filter(c, L.ex[j]);
     }
-    // publish the slice summary
-    SliceSummary* S = ws.summaries + ((size_t)row * kMaxSlices + slice);
-    if (tid == 0) {
-      st_coherent_f32(&S->x_max, xmax);
-      st_coherent(&S->top_bin, top);
-      st_coherent(&S->flags, sflags);
-      st_coherent(&S->n_finite, nfin);
+    // publish the slice summary; n_finite is the histogram's token count
+    // (rows that build one) or whether the slice holds a finite logit
+    SliceSummary* Ssum = ws.summaries + ((size_t)row * kMaxSlices + slice);
+    int32_t nfin = 0;
+    if (want_hist) {
+      for (int i = tid; i < kHist; i += kThreads) {
+        const uint64_t w = L.u.hist[i];
+        nfin += (int32_t)(w >> kCountShift);
+        st_coherent(&Ssum->hist[i], w);
+      }
+      nfin = block_sum(nfin, L.redi);
+    } else {
+      nfin = (has_finite || posinf) ? 1 : 0;
     }
-    if (want_hist)
-      for (int i = tid; i < kHist; i += kThreads) st_coherent(&S->hist[i], L.u.hist[i]);
+    if (tid == 0) {
+      st_coherent_f32(&Ssum->x_max, xmax);
+      st_coherent(&Ssum->top_bin, top);
+      st_coherent(&Ssum->flags, sflags);
+      st_coherent(&Ssum->n_finite, nfin);
+    }
     const bool is_last = arrive_last(&ws.arrive_stats[row], (uint32_t)G, &L.last);
     if (is_last) {
       merge_row(ws, P, row, c, prm, L);
@@ -1127,9 +1231,6 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   }
 
   // ------------------------------------------- C: classify against the cut
-  // values derived from the logits in phase B must not stay live across the
-  // wait: the select phase recomputes them from the packed registers
-  if (MODE == kFused) opaque_regs(raw);
   const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
   const bool active = info.mode != kModeEmpty;
   if (tid < kSliceChunks) L.u.s.chunk[tid] = 0ull;
@@ -1147,60 +1248,72 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   // Kept tokens are listed (fast draw path) only when the whole row keeps at
   // most kKeptCap tokens above the cut bin; otherwise the draw scans a chunk.
   const bool list_on = info.count_above <= kKeptCap;
+  auto keep_token = [&](float x, int32_t id, uint64_t& part) {
+    const float y = to_filter(c, x);
+    const uint64_t wq = weight(y, y_max, c.scale);
+    part += wq;
+    ent += (double)wq * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
+    min_kept = __builtin_fminf(min_kept, y);
+    ++n_kept;
+    if (list_on) {
+      const int ks = atomicAdd(&L.nlist, 1);
+      if (ks < kKeptCap) {
+        L.u.s.klist[ks].w = wq;
+        L.u.s.klist[ks].id = id;
+      }
+    }
+  };
+  auto cand_token = [&](float x, int32_t id) {
+    const int cs = atomicAdd(&L.ncand, 1);
+    if (cs < kWgCandCap) {
+      L.u.s.cand[cs].y = to_filter(c, x);
+      L.u.s.cand[cs].id = id;
+    }
+  };
+  const ClassRule rule = make_rule(info, c);
   if (active) {
-    // The per-element body stays small so that the loop over the thread's
-    // vectors unrolls completely and raw[] stays in registers; the rare
-    // kept / candidate tokens are appended with per-lane LDS atomics.
-    const int32_t tid_c = fresh_tid();
+    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+      const int32_t i0 = base32 + (tid + g * kThreads) * N;
+      // screen the quad by its largest element; the rare quads that hold a
+      // kept or candidate token are classified element by element
+      float qm = vec_elem<DT>(v, 0);
 #pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      const int32_t i0 = base32 + (tid_c + k * kThreads) * N;
+      for (int e = 1; e < N; ++e) qm = __builtin_fmaxf(qm, vec_elem<DT>(v, e));
       uint64_t part = 0ull;
-      if (i0 < end32) {
+      if (qm * rule.c32 >= rule.screen) {
+        uint32_t kb = 0u, cb = 0u;
 #pragma unroll
-        for (int q = 0; q < N; ++q) {
-          const float x = vec_elem<DT>(raw[k], q);
-          const int cls = classify(info, c, x);
-          if (cls == kKept) {
-            const float y = to_filter(c, x);
-            const uint64_t wq = weight(y, y_max, c.scale);
-            part += wq;
-            ent += (double)wq * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
-            min_kept = __builtin_fminf(min_kept, y);
-            ++n_kept;
-            if (list_on) {
-              const int ks = atomicAdd(&L.nlist, 1);
-              if (ks < kKeptCap) {
-                L.u.s.klist[ks].w = wq;
-                L.u.s.klist[ks].id = i0 + q;
-              }
-            }
-          } else if (cls == kCand) {
-            const int cs = atomicAdd(&L.ncand, 1);
-            if (cs < kWgCandCap) {
-              L.u.s.cand[cs].y = to_filter(c, x);
-              L.u.s.cand[cs].id = i0 + q;
-            }
-          }
+        for (int e = 0; e < N; ++e) {
+          const int cls = classify(rule, vec_elem<DT>(v, e));
+          kb |= (uint32_t)(cls == kKept) << e;
+          cb |= (uint32_t)(cls == kCand) << e;
+        }
+        for (uint32_t bits = kb | cb; bits != 0u; bits &= bits - 1u) {
+          const int e = __builtin_ctz(bits);
+          const float x = vec_elem_dyn<DT>(v, e);
+          if ((kb >> e) & 1u)
+            keep_token(x, i0 + e, part);
+          else
+            cand_token(x, i0 + e);
         }
       }
-      // chunk sums: a wave's vectors lie in one 1024-token chunk
+      // chunk sums: a wave's quads lie in one 1024-token chunk
       if (__ballot(part != 0ull)) {
         const uint64_t sum = wave_sum(part);
         if ((tid & 63) == 0) {
-          const int32_t wi0 = ((tid_c & ~63) + k * kThreads) * N;
+          const int32_t wi0 = ((tid & ~63) + g * kThreads) * N;
           atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.s.chunk[wi0 / kChunk]),
                     (unsigned long long)sum);
         }
       }
-    }
+      return false;
+    });
     if (kout) {
       // keep bytes of tokens outside the entry table (re-read; an output for
       // parity checks only); candidates' bytes are written by the finalize
-      const int32_t tid_k = fresh_tid();
 #pragma nounroll
-      for (int k = 0; k < NV; ++k) {
-        const int32_t i0 = base32 + (tid_k + k * kThreads) * N;
+      for (int g = 0; g < nq; ++g) {
+        const int32_t i0 = base32 + (tid + g * kThreads) * N;
         if (i0 >= end32) continue;
         const int32_t li0 = i0 - base32;
         const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
@@ -1208,37 +1321,24 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
 #pragma nounroll
         for (int q = 0; q < N && i0 + q < end32; ++q) {
           if ((pen >> q) & 1u) continue;
-          const int cls = ((allow >> q) & 1u) ? classify(info, c, load_scalar<DT>(rowp, i0 + q)) : kDrop;
+          const float x = load_scalar<DT>(rowp, i0 + q);
+          const int cls = ((allow >> q) & 1u) ? classify(rule, x) : kDrop;
           if (cls != kCand) kout[i0 + q] = cls == kKept ? 1 : 0;
         }
       }
     }
     for (int j2 = tid; j2 < n_ent; j2 += kThreads) {
       const float x = L.ex[j2];
-      const int cls = classify(info, c, x);
+      const int cls = classify(rule, x);
       const int32_t t = L.etok[j2];
       if (kout && cls != kCand) kout[t] = cls == kKept ? 1 : 0;
       if (cls == kKept) {
-        const float y = to_filter(c, x);
-        const uint64_t w = weight(y, y_max, c.scale);
-        atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.s.chunk[(t - base) / kChunk]),
+        uint64_t w = 0ull;
+        keep_token(x, t, w);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.s.chunk[(t - base32) / kChunk]),
                   (unsigned long long)w);
-        ent += (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
-        min_kept = __builtin_fminf(min_kept, y);
-        ++n_kept;
-        if (list_on) {
-          const int ks = atomicAdd(&L.nlist, 1);
-          if (ks < kKeptCap) {
-            L.u.s.klist[ks].w = w;
-            L.u.s.klist[ks].id = t;
-          }
-        }
       } else if (cls == kCand) {
-        const int cs = atomicAdd(&L.ncand, 1);
-        if (cs < kWgCandCap) {
-          L.u.s.cand[cs].y = to_filter(c, x);
-          L.u.s.cand[cs].id = t;
-        }
+        cand_token(x, t);
       }
     }
   }

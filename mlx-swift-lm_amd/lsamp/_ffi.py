@@ -153,6 +153,11 @@ class Cbv2Params(Structure):
 _lib = None
 
 
+class LaunchInfo(Structure):
+    _fields_ = [("fused", c_int32), ("slices", c_int32), ("slice_len", c_int32),
+                ("rows_per_round", c_int32), ("grid", c_int32)]
+
+
 class LibraryMissing(RuntimeError):
     pass
 
@@ -179,6 +184,8 @@ def load_library(path: str | None = None):
     lib.lsamp_context_set_mode.restype = c_int32
     lib.lsamp_context_read_status.argtypes = [c_void_p, POINTER(c_uint32)]
     lib.lsamp_context_read_status.restype = c_int32
+    lib.lsamp_context_last_launch.argtypes = [c_void_p, POINTER(LaunchInfo)]
+    lib.lsamp_context_last_launch.restype = c_int32
     lib.lsamp_context_set_timing.argtypes = [c_void_p, c_int32]
     lib.lsamp_context_set_timing.restype = c_int32
     lib.lsamp_context_read_timing.argtypes = [c_void_p, POINTER(c_double), POINTER(c_double),

@@ -94,13 +94,22 @@ class Context:
                    "lsamp_context_read_status")
         return v.value
 
+    def last_launch(self) -> dict:
+        """Shape of the last lsamp_sample launch: fused, slices, slice_len,
+        rows_per_round, grid."""
+        li = _ffi.LaunchInfo()
+        _ffi.check(self.lib.lsamp_context_last_launch(self.handle, ctypes.byref(li)),
+                   "lsamp_context_last_launch")
+        return {f: getattr(li, f) for f, _ in _ffi.LaunchInfo._fields_}
+
     # ----------------------------------------------------------------- timing
     def set_timing(self, enable: bool) -> None:
         _ffi.check(self.lib.lsamp_context_set_timing(self.handle, 1 if enable else 0),
                    "lsamp_context_set_timing")
 
     def read_timing(self):
-        """(stats kernel ms, select kernel ms, timed calls) since the last read."""
+        """(first-kernel ms, second-kernel ms, timed calls) since the last read;
+        a fused step has one kernel and an empty second interval."""
         a, b, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
         _ffi.check(self.lib.lsamp_context_read_timing(self.handle, ctypes.byref(a), ctypes.byref(b),
                                                       ctypes.byref(n)), "lsamp_context_read_timing")
