@@ -5,6 +5,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <limits>
+
 #include "lsamp_internal.h"
 
 namespace lsamp {
@@ -244,33 +246,80 @@ __device__ __forceinline__ int bin_of(float x, float c32) {
   return (int)__builtin_floorf(bin_pos(x, c32));
 }
 
-// ------------------------------------------------------------ block ops
-// All helpers assume blockDim.x == kThreads and are called by every thread.
+// ------------------------------------------------------------ wave ops
+// Wave64 scans and reductions on DPP lane moves (row_shr within 16-lane rows,
+// then row_bcast:15 / row_bcast:31 across rows).  All 64 lanes must be active.
+// `id` is the operation's identity, read by lanes without a source.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v, uint32_t id) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, CTRL, ROWS, 0xf, false);
+}
+template <int CTRL, int ROWS, typename T>
+__device__ __forceinline__ T dpp_move(T v, T id) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, dpp32<CTRL, ROWS>(__builtin_bit_cast(uint32_t, v),
+                                                   __builtin_bit_cast(uint32_t, id)));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v), i = __builtin_bit_cast(uint64_t, id);
+    const uint32_t lo = dpp32<CTRL, ROWS>((uint32_t)b, (uint32_t)i);
+    const uint32_t hi = dpp32<CTRL, ROWS>((uint32_t)(b >> 32), (uint32_t)(i >> 32));
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+template <typename T>
+__device__ __forceinline__ T read_lane(T v, int lane) {
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+  } else {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), lane);
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+struct OpAdd {
+  template <typename T> static __device__ __forceinline__ T f(T a, T b) { return a + b; }
+};
+struct OpMax {
+  template <typename T> static __device__ __forceinline__ T f(T a, T b) { return a > b ? a : b; }
+};
+struct OpMin {
+  template <typename T> static __device__ __forceinline__ T f(T a, T b) { return a < b ? a : b; }
+};
+// Inclusive scan in lane order.
+template <typename Op, typename T>
+__device__ __forceinline__ T wave_scan(T v, T id) {
+  v = Op::f(v, dpp_move<0x111, 0xf>(v, id));
+  v = Op::f(v, dpp_move<0x112, 0xf>(v, id));
+  v = Op::f(v, dpp_move<0x114, 0xf>(v, id));
+  v = Op::f(v, dpp_move<0x118, 0xf>(v, id));
+  v = Op::f(v, dpp_move<0x142, 0xa>(v, id));
+  v = Op::f(v, dpp_move<0x143, 0xc>(v, id));
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  return wave_scan<OpAdd>(v, T(0));
+}
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  return read_lane(wave_scan<OpAdd>(v, T(0)), 63);
 }
 template <typename T>
 __device__ __forceinline__ T wave_max(T v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    T o = __shfl_xor(v, off, 64);
-    v = o > v ? o : v;
-  }
-  return v;
+  const T id = std::numeric_limits<T>::has_infinity ? -std::numeric_limits<T>::infinity()
+                                                    : std::numeric_limits<T>::lowest();
+  return read_lane(wave_scan<OpMax>(v, id), 63);
 }
 template <typename T>
 __device__ __forceinline__ T wave_min(T v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    T o = __shfl_xor(v, off, 64);
-    v = o < v ? o : v;
-  }
-  return v;
+  const T id = std::numeric_limits<T>::has_infinity ? std::numeric_limits<T>::infinity()
+                                                    : std::numeric_limits<T>::max();
+  return read_lane(wave_scan<OpMin>(v, id), 63);
 }
 
+// ------------------------------------------------------------ block ops
+// All helpers assume blockDim.x == kThreads and are called by every thread.
 // scratch: at least kWaves elements of T.
 template <typename T>
 __device__ __forceinline__ T block_sum(T v, T* scratch) {
@@ -310,18 +359,6 @@ __device__ __forceinline__ T block_min(T v, T* scratch) {
   for (int i = 1; i < kWaves; ++i) r = scratch[i] < r ? scratch[i] : r;
   __syncthreads();
   return r;
-}
-
-// Inclusive scan within a wave.
-template <typename T>
-__device__ __forceinline__ T wave_incl_scan(T v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    T o = __shfl_up(v, off, 64);
-    if (lane >= off) v += o;
-  }
-  return v;
 }
 
 // Exclusive block scan in thread order; returns the exclusive prefix and

@@ -60,6 +60,7 @@ struct SliceSummary {
   uint32_t flags;    // LSAMP_ROW_NONFINITE | kSlice*
   int32_t n_finite;  // histogram token count; without a histogram, 1 when the
                      // slice holds a finite (or +inf) transformed logit
+  double z;          // histogram mass relative to the floor of bin top_bin
   uint64_t hist[kHist];
 };
 

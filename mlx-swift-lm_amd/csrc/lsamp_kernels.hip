@@ -1,16 +1,16 @@
 // lsamp_kernels.hip — gfx950 kernels of the logits-to-token stage.
 //
 // A sampling step runs over tasks (row, slice): one 512-thread work-group
-// owns one slice (<= 40960 tokens) of one row and keeps the slice's logits in
+// owns one slice (<= 65536 tokens) of one row and keeps the slice's logits in
 // registers from the moment they arrive from HBM until the token is drawn.
 //
 //  stats phase   16-byte vector loads of the slice, the grammar mask and the
 //                sparse penalties applied exactly as the reference orders
 //                them, then a histogram of the filter-space logit in 1/32-nat
 //                bins (count + fixed-point mass, one packed 64-bit LDS atomic
-//                per token).  The last work-group of the row merges the
-//                slices' histograms and locates the bin holding the
-//                top-k / top-p / min-p cut.
+//                per token).  The slices' histograms are merged on the
+//                absolute bin grid and the bin holding the top-k / top-p /
+//                min-p cut is located.
 //  select phase  every work-group keeps the tokens above the cut bin (fixed-
 //                point draw weight per 1024-token chunk, and a short list of
 //                them) and lists the tokens inside it.  The last work-group of
@@ -19,11 +19,13 @@
 //                token-id order.
 //
 // Fused mode runs both phases in one kernel whose grid fits on the device at
-// once: the slices of a row wait for the merge on a bounded spin (a wait that
-// runs out sets a status bit and the work-group carries on, so the grid always
-// drains).  Split mode runs the phases as two kernels, the second re-reading
-// its slice from L2; it needs no co-residency.  Neither mode uses MFMA: the
-// stage is a bandwidth- and reduction-bound pass, not a contraction.
+// once: each slice of a row waits (bounded spin) until all slices have
+// published their histograms, then merges them itself, so no second hand-off
+// is needed; a wait that runs out sets a status bit and the work-group carries
+// on, so the grid always drains.  Split mode runs the phases as two kernels
+// (the last stats work-group of a row merges; the second kernel re-reads its
+// slice from L2) and needs no co-residency.  Neither mode uses MFMA: the stage
+// is a bandwidth- and reduction-bound pass, not a contraction.
 #include <hip/hip_runtime.h>
 
 #include "lsamp_device.h"
@@ -36,10 +38,18 @@ using namespace dev;
 
 constexpr int kSliceWords = kMaxSliceLen / 32;       // penalty bitmap words
 constexpr int kFinalPerThread = kCandCap / kThreads;  // sorted candidates per thread
-constexpr uint32_t kReady = 1u << 16;                 // merge-done bias on arrive_stats
 constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
 
 enum TaskMode { kFused = 0, kStatsOnly = 1, kSelectOnly = 2 };
+
+// The thread index through an empty asm statement: values derived from it
+// cannot be hoisted out of the fused kernel's loop over rounds (where they
+// would stay live, and spill, across the whole task).
+__device__ __forceinline__ int fresh_tid() {
+  int t = (int)threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
 
 // ------------------------------------------------------------ row context
 struct RowCtx {
@@ -148,15 +158,6 @@ __device__ __forceinline__ float load_logit(int dt, const char* rowp, int64_t i)
   if (dt == LSAMP_DTYPE_F32) return load_scalar<LSAMP_DTYPE_F32>(rowp, i);
   if (dt == LSAMP_DTYPE_BF16) return load_scalar<LSAMP_DTYPE_BF16>(rowp, i);
   return load_scalar<LSAMP_DTYPE_F16>(rowp, i);
-}
-
-// The thread index through an empty asm statement: values derived from it
-// cannot be hoisted out of the fused kernel's loop over rounds (where they
-// would stay live, and spill, across the whole task).
-__device__ __forceinline__ int fresh_tid() {
-  int t = (int)threadIdx.x;
-  asm volatile("" : "+v"(t));
-  return t;
 }
 
 // Token classes relative to the row's cut.
@@ -275,8 +276,7 @@ struct FinalLds {
   uint64_t keys[kCandCap];
   uint8_t keep[kCandCap];
   uint64_t rowchunk[kMaxRowChunks];
-  uint64_t dw[kChunk];
-  int32_t did[kChunk];
+  uint64_t dw[kChunk + kChunk / 16];  // draw slots (padded), or rank-sort scratch
   float cx[kChunk];
   uint8_t cent[kChunk];
   uint8_t cflag[kChunk];
@@ -346,36 +346,56 @@ __device__ __forceinline__ float token_value(const SamplePlan& P, const RowCtx& 
 }
 
 // ============================================================ merge (stats)
-// Last stats work-group of a row: merges the G slice histograms (integer
-// sums on the absolute bin grid) and locates the cut bin.  Result in L.info.
-__device__ __forceinline__ void merge_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
-                          const lsamp_row_params& prm, TaskLds& L) {
-  const int tid = threadIdx.x;
+// Merges the G slice histograms of a row (integer sums on the absolute bin
+// grid) and locates the cut bin; result in L.info.  Split mode runs it in the
+// last stats work-group of the row; fused mode in every work-group of the row
+// once all slices have published (each computes the same result).
+//
+// One wave does the work with wave-level scans (no work-group barriers): one
+// round trip fetches the slice headers and the top 256 bins of every slice,
+// which are aligned through LDS; the bins are scanned from the top in blocks
+// of 64 and the scan stops at the block holding the cut.  Deeper cuts read
+// further bins, already aligned, 256 at a time.  Slices publish their own
+// total mass, so the scan never needs the bins below the cut.
+__device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan& P, int row,
+                                           const RowCtx& c, const lsamp_row_params& prm, TaskLds& L) {
+  const int l = fresh_tid();  // lane, wave 0
   const int G = P.slices;
   const int64_t V = P.vocab;
   const SliceSummary* summ = ws.summaries + (size_t)row * kMaxSlices;
-  if (tid < G) {
-    L.hx[tid] = ld_coherent(&summ[tid].x_max);
-    L.htop[tid] = ld_coherent(&summ[tid].top_bin);
-    L.hfl[tid] = ld_coherent(&summ[tid].flags);
-    L.hn[tid] = ld_coherent(&summ[tid].n_finite);
+  const bool hist_row = c.kind != LSAMP_KIND_ARGMAX;
+  constexpr int kBlk = 4;  // blocks of 64 bins per batch
+  float hx = kNegInf;
+  int32_t htop = 0, hn = 0;
+  uint32_t hfl = 0u;
+  double hz = 0.0;
+  if (l < G) {
+    hx = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&summ[l].x_max)));
+    htop = ld_coherent(&summ[l].top_bin);
+    hfl = ld_coherent(&summ[l].flags);
+    hn = ld_coherent(&summ[l].n_finite);
+    hz = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&summ[l].z)));
   }
-  const uint64_t wtail = tid < G ? ld_coherent(&summ[tid].hist[kTail]) : 0ull;
-  L.u.m.mass[2 * tid] = 0ull;
-  L.u.m.mass[2 * tid + 1] = 0ull;
-  L.u.m.cnt[2 * tid] = 0u;
-  L.u.m.cnt[2 * tid + 1] = 0u;
-  __syncthreads();
+  uint64_t w[kMaxSlices][kBlk];
+#pragma unroll
+  for (int s = 0; s < kMaxSlices; ++s)
+#pragma unroll
+    for (int k = 0; k < kBlk; ++k)
+      w[s][k] = (hist_row && s < G) ? ld_coherent(&summ[s].hist[64 * k + l]) : 0ull;
+
   float row_max = kNegInf;
   int32_t row_top = 0, n_total = 0;
   uint32_t rflags = 0u;
   bool first = true;
   for (int s = 0; s < G; ++s) {
-    rflags |= L.hfl[s];
-    n_total += L.hn[s];
-    if (L.hn[s] > 0) {
-      if (first || L.hx[s] > row_max) row_max = L.hx[s];
-      if (first || L.htop[s] > row_top) row_top = L.htop[s];
+    const float xs = __shfl(hx, s, 64);
+    const int32_t ts = __shfl(htop, s, 64);
+    const int32_t ns = __shfl(hn, s, 64);
+    rflags |= (uint32_t)__shfl((int)hfl, s, 64);
+    n_total += ns;
+    if (ns > 0) {
+      if (first || xs > row_max) row_max = xs;
+      if (first || ts > row_top) row_top = ts;
       first = false;
     }
   }
@@ -401,64 +421,11 @@ __device__ __forceinline__ void merge_row(const Workspace& ws, const SamplePlan&
     info.count_above = 0;
   } else if (info.mode == kModeNormal) {
     const double inv_frac = 1.0 / (double)(1ull << kMassFracBits);
-    int32_t tcnt = 0;
-    double tmass = 0.0;
-    // slice-local bin i of slice s is row bin i + (row_top - top_s); the
-    // slices are read four at a time (eight independent loads per thread)
-    for (int s0 = 0; s0 < G; s0 += 4) {
-      uint64_t w[4][2];
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-          w[d][u] = (s0 + d < G && L.hn[s0 + d] > 0) ? ld_coherent(&summ[s0 + d].hist[2 * tid + u])
-                                                     : 0ull;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          if (w[d][u] == 0ull) continue;
-          const int s = s0 + d;
-          const int i = 2 * tid + u;
-          const int j = i + (row_top - L.htop[s]);
-          const uint32_t wc = (uint32_t)(w[d][u] >> kCountShift);
-          const uint64_t wm = w[d][u] & kMassMask;
-          if (j < kBins) {
-            atomicAdd(&L.u.m.cnt[j], wc);
-            atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.m.mass[j]), (unsigned long long)wm);
-          } else {
-            const int b = L.htop[s] - i;  // absolute bin
-            tcnt += (int32_t)wc;
-            tmass += (double)wm * inv_frac * exp(((double)b - (double)s_top) / 32.0);
-          }
-        }
-      }
-    }
-    if (tid < G && L.hn[tid] > 0 && wtail) {
-      const double edge = (double)(L.htop[tid] - kBins + 1);
-      tcnt += (int32_t)(wtail >> kCountShift);
-      tmass += (double)(wtail & kMassMask) * inv_frac * exp((edge - (double)s_top) / 32.0);
-    }
-    __syncthreads();
-    int32_t cnt[2];
-    double mass[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int j = 2 * tid + u;
-      cnt[u] = (int32_t)L.u.m.cnt[j];
-      mass[u] = cnt[u] ? (double)L.u.m.mass[j] * inv_frac *
-                             exp(((double)(row_top - j) - (double)s_top) / 32.0)
-                       : 0.0;
-    }
-    tcnt = block_sum(tcnt, L.redi);
-    tmass = block_sum(tmass, L.redd);
-    int32_t tot_cnt = 0;
-    double tot_mass = 0.0;
-    const int32_t excl_cnt = block_excl_scan(cnt[0] + cnt[1], L.redi, &tot_cnt);
-    const double excl_mass = block_excl_scan(mass[0] + mass[1], L.redd, &tot_mass);
-    const double z = tot_mass + tmass;
+    // total mass relative to the row top: each slice's total is relative to
+    // its own top bin
+    const double z = wave_sum((l < G && hn > 0) ? hz * exp(((double)htop - (double)s_top) / 32.0)
+                                                : 0.0);
     info.z = z;
-
     const int32_t k_lim = (prm.top_k > 0 && (int64_t)prm.top_k < V) ? prm.top_k : 0;
     bool p_on;
     double P_lim;
@@ -484,40 +451,108 @@ __device__ __forceinline__ void merge_row(const Workspace& ws, const SamplePlan&
       if (j_t > kBins) j_t = kBins;
     }
     info.p_limit = p_on ? P_lim : -1.0;
-    int my_cut = 0x7fffffff;
-    int32_t C = excl_cnt;
-    double M = excl_mass;
+
+    // batch 0: align the top 256 bins of every slice in LDS
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int j = 2 * tid + u;
-      if (cnt[u] > 0 || (m_on && j == j_t)) {
-        const bool tk = k_on && C + cnt[u] >= k_lim;
-        const bool tp = p_on && cnt[u] > 0 &&
-                        (strict ? (M + mass[u] >= P_lim) : (M + mass[u] > P_lim));
-        const bool tm = m_on && j >= j_t;
-        if ((tk || tp || tm) && j < my_cut) my_cut = j;
-      }
-      C += cnt[u];
-      M += mass[u];
+    for (int k = 0; k < kBlk; ++k) {
+      L.u.m.cnt[64 * k + l] = 0u;
+      L.u.m.mass[64 * k + l] = 0ull;
     }
-    const int cut = block_min(my_cut, L.redi);
-    if (cut != 0x7fffffff) {
-      if (cut / 2 == tid) {
-        L.misc[0] = excl_cnt + ((cut & 1) ? cnt[0] : 0);
-        L.misc64[0] = __builtin_bit_cast(uint64_t, excl_mass + ((cut & 1) ? mass[0] : 0.0));
+#pragma unroll
+    for (int s = 0; s < kMaxSlices; ++s) {
+      if (s >= G) break;
+      const int32_t off = row_top - __shfl(htop, s, 64);
+#pragma unroll
+      for (int k = 0; k < kBlk; ++k) {
+        const int j = 64 * k + l + off;
+        if (w[s][k] != 0ull && j < 64 * kBlk) {
+          atomicAdd(&L.u.m.cnt[j], (uint32_t)(w[s][k] >> kCountShift));
+          atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.m.mass[j]),
+                    (unsigned long long)(w[s][k] & kMassMask));
+        }
       }
-      __syncthreads();
+    }
+    int32_t carry_c = 0;
+    double carry_m = 0.0;
+    int cut = -1;
+    int32_t cut_c = 0;
+    double cut_m = 0.0;
+    for (int b = 0; b < kBins / (64 * kBlk) && cut < 0; ++b) {
+      uint32_t cnt[kBlk];
+      uint64_t msum[kBlk];
+      if (b == 0) {
+#pragma unroll
+        for (int k = 0; k < kBlk; ++k) {
+          cnt[k] = L.u.m.cnt[64 * k + l];
+          msum[k] = L.u.m.mass[64 * k + l];
+        }
+      } else {
+        // deeper batch: read the slices' bins already aligned
+#pragma unroll
+        for (int k = 0; k < kBlk; ++k) {
+          cnt[k] = 0u;
+          msum[k] = 0ull;
+        }
+        for (int s = 0; s < G; ++s) {
+          const int32_t off = row_top - __shfl(htop, s, 64);
+          if (__shfl(hn, s, 64) <= 0) continue;
+          uint64_t ws4[kBlk];
+#pragma unroll
+          for (int k = 0; k < kBlk; ++k) {
+            const int i = 64 * kBlk * b + 64 * k + l - off;
+            ws4[k] = (i >= 0 && i < kBins) ? ld_coherent(&summ[s].hist[i]) : 0ull;
+          }
+#pragma unroll
+          for (int k = 0; k < kBlk; ++k) {
+            cnt[k] += (uint32_t)(ws4[k] >> kCountShift);
+            msum[k] += ws4[k] & kMassMask;
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kBlk; ++k) {
+        if (cut >= 0) break;
+        const int j = 64 * kBlk * b + 64 * k + l;
+        const int32_t cj = (int32_t)cnt[k];
+        const double mj = cj ? (double)msum[k] * inv_frac *
+                                   exp(((double)(row_top - j) - (double)s_top) / 32.0)
+                             : 0.0;
+        const int32_t ic = wave_incl_scan(cj);
+        const double im = wave_incl_scan(mj);
+        const int32_t C = carry_c + ic - cj;
+        const double M = carry_m + im - mj;
+        bool hit = false;
+        if (cj > 0 || (m_on && j == j_t)) {
+          const bool tk = k_on && C + cj >= k_lim;
+          const bool tp = p_on && cj > 0 && (strict ? (M + mj >= P_lim) : (M + mj > P_lim));
+          const bool tm = m_on && j >= j_t;
+          hit = tk || tp || tm;
+        }
+        const uint64_t hits = __ballot(hit);
+        if (hits) {
+          const int f = __builtin_ctzll(hits);
+          cut = 64 * kBlk * b + 64 * k + f;
+          cut_c = __shfl(C, f, 64);
+          cut_m = __shfl(M, f, 64);
+        } else {
+          carry_c += __shfl(ic, 63, 64);
+          carry_m += __shfl(im, 63, 64);
+        }
+      }
+    }
+    if (cut >= 0) {
       info.cut = cut;
-      info.count_above = L.misc[0];
-      info.mass_above = __builtin_bit_cast(double, L.misc64[0]);
+      info.count_above = cut_c;
+      info.mass_above = cut_m;
     } else {
-      const bool tk = k_on && tot_cnt + tcnt >= k_lim;
-      const bool tp = p_on && tcnt > 0 && (strict ? (z >= P_lim) : (z > P_lim));
+      // carry_* now hold the whole window; the rest of the row is the tail
+      const bool tk = k_on && n_total >= k_lim;
+      const bool tp = p_on && n_total > carry_c && (strict ? (z >= P_lim) : (z > P_lim));
       const bool tm = m_on && j_t >= kBins;
       if (tk || tp || tm) {
         info.cut = kCutTail;
-        info.count_above = tot_cnt;
-        info.mass_above = tot_mass;
+        info.count_above = carry_c;
+        info.mass_above = carry_m;
       } else {
         info.cut = kCutNone;
         info.count_above = n_total;
@@ -525,52 +560,38 @@ __device__ __forceinline__ void merge_row(const Workspace& ws, const SamplePlan&
       }
     }
   }
-  __syncthreads();
-  if (tid == 0) L.info = info;
-  __syncthreads();
+  if (l == 0) L.info = info;
 }
 
-__device__ __forceinline__ void publish_rowinfo(RowInfo* dst, const RowInfo& v) {
-  st_coherent_f32(&dst->x_max, v.x_max);
-  st_coherent_f32(&dst->q_top, v.q_top);
-  st_coherent(&dst->top_bin, v.top_bin);
-  st_coherent(&dst->cut, v.cut);
-  st_coherent(&dst->mode, v.mode);
-  st_coherent(&dst->flags, v.flags);
-  st_coherent(&dst->count_above, v.count_above);
-  st_coherent(&dst->n_finite, v.n_finite);
-  st_coherent_f64(&dst->mass_above, v.mass_above);
-  st_coherent_f64(&dst->z, v.z);
-  st_coherent_f64(&dst->p_limit, v.p_limit);
-  st_coherent(&dst->kept_cands, v.kept_cands);
-}
-
-__device__ __forceinline__ RowInfo read_rowinfo(const RowInfo* src) {
-  RowInfo v;
-  v.x_max = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&src->x_max)));
-  v.q_top = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&src->q_top)));
-  v.top_bin = ld_coherent(&src->top_bin);
-  v.cut = ld_coherent(&src->cut);
-  v.mode = ld_coherent(&src->mode);
-  v.flags = ld_coherent(&src->flags);
-  v.count_above = ld_coherent(&src->count_above);
-  v.n_finite = ld_coherent(&src->n_finite);
-  v.mass_above = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&src->mass_above)));
-  v.z = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&src->z)));
-  v.p_limit = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&src->p_limit)));
-  v.kept_cands = ld_coherent(&src->kept_cands);
-  v.pad = 0;
-  return v;
+__device__ __forceinline__ void merge_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
+                          const lsamp_row_params& prm, TaskLds& L) {
+  if (threadIdx.x < 64) merge_wave(ws, P, row, c, prm, L);
+  __syncthreads();
 }
 
 // ========================================================= finalize (select)
 // Last select work-group of a row: exact cut among the candidates, kept
-// weights per chunk, and the inverse-CDF draw.
+// weights per chunk, and the inverse-CDF draw.  Only the sort of more than 64
+// candidates uses the whole work-group; everything else runs in wave 0 with
+// wave-level scans (no work-group barriers), and the other waves leave.
+constexpr int kChunksPerLane = kMaxRowChunks / 64;  // chunk sums held per lane
+constexpr int kSlotsPerLane = kChunk / 64;           // draw slots per lane
+
+// LDS slot of offset o (0..1023) within the drawn chunk: lane-contiguous runs
+// of kSlotsPerLane with one pad word per run (no bank conflicts).
+__device__ __forceinline__ int draw_slot(int o) { return o + (o >> 4); }
+
+__device__ __forceinline__ uint64_t cand_key(float y, int32_t id) {
+  return ((uint64_t)ordered_key(y == 0.0f ? 0.0f : y) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+}
+
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
                              const lsamp_row_params& prm, const RowInfo& info, TaskLds& L,
                              const char* rowp, const uint32_t* mrow, bool fused) {
-  const int tid = threadIdx.x;
+  const int tid = fresh_tid();
+  const int l = tid & 63;
+  const bool wave0 = tid < 64;
   const int G = P.slices;
   const int64_t V = P.vocab;
   const int nch_row = P.nchunks;
@@ -580,81 +601,109 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   Candidate* rc = ws.cands + (size_t)row * kCandCap;
   FinalLds& F = L.u.f;
 
-  // ---- every independent load first
-  if (tid < G) {
-    const SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + tid;
-    SelectPartial v;
-    v.ent = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&sp->ent)));
-    v.min_kept = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&sp->min_kept)));
-    v.n_kept = ld_coherent(&sp->n_kept);
-    v.n_cand = ld_coherent(&sp->n_cand);
-    v.n_list = ld_coherent(&sp->n_list);
-    v.overflow = ld_coherent(&sp->overflow);
-    v.pad = 0;
-    L.part[tid] = v;
-  }
-  F.rowchunk[tid] = tid < nch_row ? ld_coherent(&rowchunks[tid]) : 0ull;
-  if (tid == 0) {
-    L.misc[0] = (int32_t)ld_coherent(&ws.cand_count[row]);
+  // ---- wave 0 issues every independent load at once
+  SelectPartial part{};
+  uint64_t rch[kChunksPerLane];
+  uint64_t key0 = 0ull;
+  float u_draw = 0.0f;
+  int32_t probe = -1, total_cand = 0;
+  if (wave0) {
+    if (l < G) {
+      const SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + l;
+      part.ent = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&sp->ent)));
+      part.min_kept = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&sp->min_kept)));
+      part.n_kept = ld_coherent(&sp->n_kept);
+      part.n_cand = ld_coherent(&sp->n_cand);
+      part.n_list = ld_coherent(&sp->n_list);
+      part.overflow = ld_coherent(&sp->overflow);
+    }
+#pragma unroll
+    for (int i = 0; i < kChunksPerLane; ++i) {
+      const int ci = kChunksPerLane * l + i;
+      rch[i] = ci < nch_row ? ld_coherent(&rowchunks[ci]) : 0ull;
+    }
+    // candidate l, read before the count is known (slots past it are ignored)
+    const float cy = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[l].y)));
+    const int32_t cid = ld_coherent(&rc[l].id);
+    key0 = cand_key(cy, cid);
+    int32_t tc = 0;
     float u = 0.0f;
-    if (P.uniforms)
-      u = P.uniforms[row];
-    else if (P.philox_keys)
-      u = philox_uniform(P.philox_keys[row], 0u);
-    L.misc64[1] = (uint64_t)__float_as_uint(u);
-    L.misc[1] = P.probe_tokens ? P.probe_tokens[row] : -1;
+    int32_t pr = -1;
+    if (l == 0) {
+      tc = (int32_t)ld_coherent(&ws.cand_count[row]);
+      if (P.uniforms)
+        u = P.uniforms[row];
+      else if (P.philox_keys)
+        u = philox_uniform(P.philox_keys[row], 0u);
+      pr = P.probe_tokens ? P.probe_tokens[row] : -1;
+    }
+    total_cand = read_lane(tc, 0);
+    u_draw = read_lane(u, 0);
+    probe = read_lane(pr, 0);
   }
-  __syncthreads();
+  // ---- row-wide partials (wave 0), shared through LDS with the other waves
   double ent_all = 0.0;
   float min_all = kPosInf;
   int32_t kept_all = 0;
-  bool overflow = (info.flags & LSAMP_ROW_OVERFLOW) != 0;
-  for (int s = 0; s < G; ++s) {
-    ent_all += L.part[s].ent;
-    min_all = __builtin_fminf(min_all, L.part[s].min_kept);
-    kept_all += L.part[s].n_kept;
-    if (L.part[s].n_cand > kWgCandCap || L.part[s].overflow) overflow = true;
-  }
-  const int total_cand = L.misc[0];
-  if (total_cand > kCandCap) overflow = true;
-  const float u_draw = __uint_as_float((uint32_t)L.misc64[1]);
-  const int32_t probe = L.misc[1];
-  const int nc = (overflow || !active) ? 0 : total_cand;
-
-  // ---- sort candidates: value descending, id ascending (-0 == +0)
-  int n2 = 1;
-  while (n2 < nc) n2 <<= 1;
-  for (int i = tid; i < n2; i += kThreads) {
-    uint64_t key = 0ull;
-    if (i < nc) {
-      const float y = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[i].y)));
-      const int32_t id = ld_coherent(&rc[i].id);
-      key = ((uint64_t)ordered_key(y == 0.0f ? 0.0f : y) << 32) |
-            (uint64_t)(0xffffffffu - (uint32_t)id);
-    }
-    F.keys[i] = key;
+  bool overflow = false;
+  int nc = 0;
+  if (wave0) {
+    const bool in = l < G;
+    ent_all = wave_sum(in ? part.ent : 0.0);
+    min_all = wave_min(in ? part.min_kept : kPosInf);
+    kept_all = wave_sum(in ? part.n_kept : 0);
+    const int32_t ov = wave_max(in && (part.n_cand > kWgCandCap || part.overflow) ? 1 : 0);
+    overflow = (info.flags & LSAMP_ROW_OVERFLOW) != 0 || ov != 0 || total_cand > kCandCap;
+    nc = (overflow || !active) ? 0 : total_cand;
+    if (l == 0) L.misc[1] = nc;
   }
   __syncthreads();
-  for (int kk = 2; kk <= n2; kk <<= 1) {
-    for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-      for (int i = tid; i < n2; i += kThreads) {
-        const int ixj = i ^ jj;
-        if (ixj > i) {
-          const uint64_t a = F.keys[i], b = F.keys[ixj];
-          const bool desc = (i & kk) == 0;
-          if (desc ? (a < b) : (a > b)) {
-            F.keys[i] = b;
-            F.keys[ixj] = a;
+  nc = L.misc[1];
+
+  // ---- sort candidates: value descending, id ascending (-0 == +0)
+  if (nc > 64) {
+    int n2 = 1;
+    while (n2 < nc) n2 <<= 1;
+    for (int i = tid; i < n2; i += kThreads) {
+      uint64_t key = 0ull;
+      if (i < nc) {
+        const float y = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[i].y)));
+        key = cand_key(y, ld_coherent(&rc[i].id));
+      }
+      F.keys[i] = key;
+    }
+    __syncthreads();
+    for (int kk = 2; kk <= n2; kk <<= 1) {
+      for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+        for (int i = tid; i < n2; i += kThreads) {
+          const int ixj = i ^ jj;
+          if (ixj > i) {
+            const uint64_t a = F.keys[i], b = F.keys[ixj];
+            const bool desc = (i & kk) == 0;
+            if (desc ? (a < b) : (a > b)) {
+              F.keys[i] = b;
+              F.keys[ixj] = a;
+            }
           }
         }
+        __syncthreads();
       }
-      __syncthreads();
     }
   }
+  if (!wave0) return;
+  if (nc > 0 && nc <= 64) {
+    // rank sort of the wave's own keys (keys are distinct: ids are)
+    const uint64_t key = l < nc ? key0 : 0ull;
+    F.dw[l] = key;
+    __builtin_amdgcn_wave_barrier();
+    int rank = 0;
+    for (int i = 0; i < nc; ++i) rank += F.dw[i] > key ? 1 : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (l < nc) F.keys[rank] = key;
+    __builtin_amdgcn_wave_barrier();
+  }
 
-  // ---- keep rule over the sorted candidates (thread t owns a contiguous run)
-  const int per = (n2 + kThreads - 1) / kThreads;  // <= kFinalPerThread
-  const int r0 = tid * per;
+  // ---- keep rule over the sorted candidates, 64 at a time
   const double P_lim = info.p_limit;
   const bool p_on = P_lim >= 0.0;
   const int32_t k_lim = (c.kind == LSAMP_KIND_FILTERED && prm.top_k > 0 && (int64_t)prm.top_k < V)
@@ -664,50 +713,45 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   const bool m_on = c.kind == LSAMP_KIND_FILTERED && mp > 0.0f;
   const float ln_mp = m_on ? __builtin_logf(mp) : 0.0f;
   const bool mlx = P.semantics == LSAMP_SEM_MLXLM;
-  // the per-thread arrays are indexed by unrolled constants only (registers)
-  double e_loc[kFinalPerThread];
-  double e_sum = 0.0;
 #pragma unroll
-  for (int u = 0; u < kFinalPerThread; ++u) {
-    const int r = r0 + u;
-    double e = 0.0;
-    if (u < per && r < nc) e = (double)__builtin_expf(key_y(F.keys[r]) - info.q_top);
-    e_loc[u] = e;
-    e_sum += e;
-  }
-  double e_tot = 0.0;
-  double e_excl = block_excl_scan(e_sum, L.redd, &e_tot);
-  int32_t surv_loc = 0;
-  uint8_t surv[kFinalPerThread];
-#pragma unroll
-  for (int u = 0; u < kFinalPerThread; ++u) {
-    const int r = r0 + u;
-    surv[u] = 0;
-    if (u >= per || r >= nc) continue;
-    const uint32_t kr = (uint32_t)(F.keys[r] >> 32);
+  for (int i = 0; i < kChunksPerLane; ++i) F.rowchunk[kChunksPerLane * l + i] = rch[i];
+  __builtin_amdgcn_wave_barrier();
+  double carry_e = 0.0;
+  int32_t carry_s = 0, carry_k = 0;
+  double cent = 0.0;
+  float cmin = kPosInf;
+  for (int r0 = 0; r0 < nc; r0 += 64) {
+    const int r = r0 + l;
+    const bool in = r < nc;
+    const uint64_t key = in ? F.keys[r] : 0ull;
+    const uint32_t kr = (uint32_t)(key >> 32);
     const float y = key_to_float(kr);
+    const double e = in ? (double)__builtin_expf(y - info.q_top) : 0.0;
+    const double ie = wave_incl_scan(e);
+    const double e_excl = carry_e + ie - e;
     bool keep_p = true, keep_m = true;
     if (mlx) {
-      // tie group [g0, g1) of equal values (sorted by id ascending)
-      int lo = 0, hi = r;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if ((uint32_t)(F.keys[mid] >> 32) == kr) hi = mid; else lo = mid + 1;
+      if (in) {
+        // tie group [g0, g1) of equal values (sorted by id ascending)
+        int lo = 0, hi = r;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if ((uint32_t)(F.keys[mid] >> 32) == kr) hi = mid; else lo = mid + 1;
+        }
+        const int g0 = lo;
+        lo = r;
+        hi = nc - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if ((uint32_t)(F.keys[mid] >> 32) == kr) lo = mid; else hi = mid - 1;
+        }
+        const int g1 = lo + 1;
+        // mass ranked strictly before r when equal values put higher ids first
+        // (ascending stable argsort, Evaluate.swift:463-469)
+        const double sp = info.mass_above + e_excl - (double)(r - g0) * e + (double)(g1 - 1 - r) * e;
+        if (p_on) keep_p = sp < P_lim;
+        if (m_on) keep_m = (y - y_max) >= ln_mp;
       }
-      const int g0 = lo;
-      lo = r;
-      hi = nc - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if ((uint32_t)(F.keys[mid] >> 32) == kr) lo = mid; else hi = mid - 1;
-      }
-      const int g1 = lo + 1;
-      // mass ranked strictly before r when equal values put higher ids first
-      // (ascending stable argsort, Evaluate.swift:463-469)
-      const double sp = info.mass_above + e_excl - (double)(r - g0) * e_loc[u] +
-                        (double)(g1 - 1 - r) * e_loc[u];
-      if (p_on) keep_p = sp < P_lim;
-      if (m_on) keep_m = (y - y_max) >= ln_mp;
     } else {
       const double sr = info.mass_above + e_excl;
       if (p_on) keep_p = sr <= P_lim;
@@ -715,144 +759,101 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
       const int64_t rank = (int64_t)info.count_above + r;
       if (k_lim > 0 && rank >= k_lim) keep_p = false;
     }
-    surv[u] = (keep_p && keep_m) ? 1 : 0;
-    surv_loc += surv[u];
-    e_excl += e_loc[u];
-  }
-  int32_t surv_tot = 0;
-  int32_t surv_excl = block_excl_scan(surv_loc, L.redi, &surv_tot);
-  int32_t kc_loc = 0;
-  double cent = 0.0;
-  float cmin = kPosInf;
-#pragma unroll
-  for (int u = 0; u < kFinalPerThread; ++u) {
-    const int r = r0 + u;
-    if (u >= per || r >= n2) continue;
-    uint8_t keep = surv[u];
-    if (keep && mlx && k_lim > 0) {
-      keep = ((int64_t)info.count_above + surv_excl) < k_lim ? 1 : 0;
-      ++surv_excl;
-    }
-    F.keep[r] = keep;
+    const int32_t surv = (in && keep_p && keep_m) ? 1 : 0;
+    const int32_t is = wave_incl_scan(surv);
+    bool keep = surv != 0;
+    if (keep && mlx && k_lim > 0) keep = ((int64_t)info.count_above + carry_s + is - 1) < k_lim;
+    const int32_t kk = keep ? 1 : 0;
+    const int32_t ik = wave_incl_scan(kk);
+    if (in) F.keep[r] = keep ? 1 : 0;
     if (keep) {
-      const float y = key_y(F.keys[r]);
+      const int32_t id = key_id(key);
       const uint64_t wgt = weight(y, y_max, c.scale);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&F.rowchunk[key_id(F.keys[r]) / kChunk]),
-                (unsigned long long)wgt);
+      atomicAdd(reinterpret_cast<unsigned long long*>(&F.rowchunk[id / kChunk]), (unsigned long long)wgt);
       cent += (double)wgt * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
       cmin = __builtin_fminf(cmin, y);
-      ++kc_loc;
+      // kept candidates persist (sorted) for the MTP residual pass
+      const int32_t slot = carry_k + ik - 1;
+      rc[slot].y = y;
+      rc[slot].id = id;
     }
+    if (in && P.keep) P.keep[(size_t)row * (size_t)V + key_id(key)] = keep ? 1 : 0;
+    carry_e += read_lane(ie, 63);
+    carry_s += read_lane(is, 63);
+    carry_k += read_lane(ik, 63);
   }
-  cent = block_sum(cent, L.redd);
-  cmin = block_min(cmin, L.redf);
-  int32_t kept_c = 0;
-  int32_t kexcl = block_excl_scan(kc_loc, L.redi, &kept_c);
-  // persist kept candidates (MTP residual pass) and the keep bytes of every
-  // candidate (parity output; the select phase leaves candidates' bytes alone)
-  for (int u = 0; u < per; ++u) {
-    const int r = r0 + u;
-    if (r >= nc) break;
-    if (F.keep[r]) {
-      rc[kexcl].y = key_y(F.keys[r]);
-      rc[kexcl].id = key_id(F.keys[r]);
-      ++kexcl;
-    }
-    if (P.keep) P.keep[(size_t)row * (size_t)V + key_id(F.keys[r])] = F.keep[r];
-  }
+  cent = wave_sum(cent);
+  cmin = wave_min(cmin);
+  const int32_t kept_c = carry_k;
+  __builtin_amdgcn_wave_barrier();
 
   // ---- total weight and the chunk holding the target
-  const uint64_t wt = F.rowchunk[tid];
-  uint64_t W = 0ull;
-  const uint64_t wexcl = block_excl_scan(wt, L.redu, &W);
+  uint64_t lane_w = 0ull;
+#pragma unroll
+  for (int i = 0; i < kChunksPerLane; ++i) {
+    rch[i] = F.rowchunk[kChunksPerLane * l + i];
+    lane_w += rch[i];
+  }
+  const uint64_t iw = wave_incl_scan(lane_w);
+  const uint64_t W = read_lane(iw, 63);
   const uint64_t target = W ? scaled_target(uniform_u32(u_draw), W) : 0ull;
-  if (tid == 0) {
-    L.misc[2] = -1;
-    L.misc[3] = -1;
+  int my_c = -1;
+  uint64_t my_t = 0ull;
+  {
+    uint64_t pre = iw - lane_w;
+#pragma unroll
+    for (int i = 0; i < kChunksPerLane; ++i) {
+      if (rch[i] && pre <= target && target < pre + rch[i]) {
+        my_c = kChunksPerLane * l + i;
+        my_t = target - pre;
+      }
+      pre += rch[i];
+    }
   }
-  __syncthreads();
-  if (W && wt && wexcl <= target && target < wexcl + wt) {
-    L.misc[2] = tid;
-    L.misc64[0] = target - wexcl;
+  const uint64_t hitc = __ballot(my_c >= 0);
+  int cstar = -1;
+  uint64_t ltarget = 0ull;
+  if (W && hitc && !overflow && active) {
+    const int f = __builtin_ctzll(hitc);
+    cstar = read_lane(my_c, f);
+    ltarget = read_lane(my_t, f);
   }
-  __syncthreads();
-  const int cstar = (overflow || !active) ? -1 : L.misc[2];
-  const uint64_t ltarget = L.misc64[0];
 
+  // ---- the token inside the chunk: inverse CDF in id order over draw slots
+  int token = -1;
   if (cstar >= 0) {
-    const int64_t cb = (int64_t)cstar * kChunk;
-    const int64_t ce = cb + kChunk < V ? cb + kChunk : V;
+    const int32_t cb = cstar * kChunk;
+    const int32_t ce = cb + kChunk < V ? cb + kChunk : (int32_t)V;
     const int cps = P.slice_len / kChunk;
     const int sc = cstar / cps;
-    const bool list_ok = L.part[sc].n_list <= kKeptCap;
-    if (tid == 0) L.nitems = 0;
-    __syncthreads();
-    if (list_ok) {
+    const int32_t n_list = __shfl(part.n_list, sc, 64);
+#pragma unroll
+    for (int i = 0; i < kSlotsPerLane; ++i) F.dw[draw_slot(kSlotsPerLane * l + i)] = 0ull;
+    __builtin_amdgcn_wave_barrier();
+    if (n_list <= kKeptCap) {
       // fast path: the kept tokens of this chunk are all listed
       const KeptItem* kl = ws.klist + ((size_t)row * kMaxSlices + sc) * kKeptCap;
-      const int nl = L.part[sc].n_list;
-      static_assert(kKeptCap <= kThreads, "one listed item per thread");
-      if (tid < nl) {
-        const int32_t id = ld_coherent(&kl[tid].id);
-        if (id >= cb && id < ce) {
-          const int slot = atomicAdd(&L.nitems, 1);
-          F.did[slot] = id;
-          F.dw[slot] = ld_coherent(&kl[tid].w);
+#pragma unroll
+      for (int k = 0; k < kKeptCap / 64; ++k) {
+        const int i = 64 * k + l;
+        if (i < n_list) {
+          const int32_t id = ld_coherent(&kl[i].id);
+          if (id >= cb && id < ce) F.dw[draw_slot(id - cb)] = ld_coherent(&kl[i].w);
         }
       }
-      for (int r = tid; r < nc; r += kThreads) {
+      for (int r = l; r < nc; r += 64) {
         if (!F.keep[r]) continue;
         const int32_t id = key_id(F.keys[r]);
-        if (id >= cb && id < ce) {
-          const int slot = atomicAdd(&L.nitems, 1);
-          F.did[slot] = id;
-          F.dw[slot] = weight(key_y(F.keys[r]), y_max, c.scale);
-        }
+        if (id >= cb && id < ce) F.dw[draw_slot(id - cb)] = weight(key_y(F.keys[r]), y_max, c.scale);
       }
-      __syncthreads();
-      const int ni = L.nitems;
-      int m2 = 1;
-      while (m2 < ni) m2 <<= 1;
-      for (int i = ni + tid; i < m2; i += kThreads) {
-        F.did[i] = 0x7fffffff;
-        F.dw[i] = 0ull;
-      }
-      __syncthreads();
-      for (int kk = 2; kk <= m2; kk <<= 1) {
-        for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-          for (int i = tid; i < m2; i += kThreads) {
-            const int ixj = i ^ jj;
-            if (ixj > i) {
-              const int32_t a = F.did[i], b = F.did[ixj];
-              const bool asc = (i & kk) == 0;
-              if (asc ? (a > b) : (a < b)) {
-                F.did[i] = b;
-                F.did[ixj] = a;
-                const uint64_t t = F.dw[i];
-                F.dw[i] = F.dw[ixj];
-                F.dw[ixj] = t;
-              }
-            }
-          }
-          __syncthreads();
-        }
-      }
-      // items 2t, 2t+1 per thread, in id order
-      const uint64_t w0 = 2 * tid < ni ? F.dw[2 * tid] : 0ull;
-      const uint64_t w1 = 2 * tid + 1 < ni ? F.dw[2 * tid + 1] : 0ull;
-      uint64_t tot = 0ull;
-      const uint64_t ex = block_excl_scan(w0 + w1, L.redu, &tot);
-      if (w0 && ex <= ltarget && ltarget < ex + w0) L.misc[3] = F.did[2 * tid];
-      if (w1 && ex + w0 <= ltarget && ltarget < ex + w0 + w1) L.misc[3] = F.did[2 * tid + 1];
-      __syncthreads();
     } else {
-      // scan the chunk in token order (re-read from L2 / HBM)
-      for (int i = tid; i < kChunk; i += kThreads) {
-        F.cent[i] = 0;
-        F.cflag[i] = 0;
+      // re-read the chunk: every token's transformed value and class
+      for (int i = l; i < kChunk / 4; i += 64) {
+        reinterpret_cast<uint32_t*>(F.cent)[i] = 0u;
+        reinterpret_cast<uint32_t*>(F.cflag)[i] = 0u;
       }
-      __syncthreads();
-      for (int r = tid; r < nc; r += kThreads) {
+      __builtin_amdgcn_wave_barrier();
+      for (int r = l; r < nc; r += 64) {
         if (!F.keep[r]) continue;
         const int32_t id = key_id(F.keys[r]);
         if (id >= cb && id < ce) F.cflag[id - cb] = 1;
@@ -862,7 +863,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
         e0 = P.row_ptr[row];
         e1 = P.row_ptr[row + 1];
       }
-      for (int32_t e = e0 + tid; e < e1; e += kThreads) {
+      for (int32_t e = e0 + l; e < e1; e += 64) {
         const lsamp_penalty_entry ent = P.entries[e];
         if (ent.token < cb || ent.token >= ce) continue;
         float x = load_scalar<DT>(rowp, ent.token);
@@ -872,64 +873,67 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
         F.cx[ent.token - cb] = x;
         F.cent[ent.token - cb] = 1;
       }
-      __syncthreads();
-      uint64_t wl[2] = {0ull, 0ull};
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int li = 2 * tid + u;
-        const int64_t i = cb + li;
-        if (i >= ce) continue;
-        const float x = token_value<DT>(P, c, prm, row, rowp, mrow, i, &F.cx[li], &F.cent[li]);
-        const int cls = classify(make_rule(info, c), x);
-        if (cls == kKept || (cls == kCand && F.cflag[li]))
-          wl[u] = weight(to_filter(c, x), y_max, c.scale);
+      __builtin_amdgcn_wave_barrier();
+      const ClassRule rule = make_rule(info, c);
+      for (int i = 0; i < kSlotsPerLane; ++i) {
+        const int o = kSlotsPerLane * l + i;
+        if (cb + o >= ce) break;
+        const float x = token_value<DT>(P, c, prm, row, rowp, mrow, cb + o, &F.cx[o], &F.cent[o]);
+        const int cls = classify(rule, x);
+        if (cls == kKept || (cls == kCand && F.cflag[o]))
+          F.dw[draw_slot(o)] = weight(to_filter(c, x), y_max, c.scale);
       }
-      uint64_t ctot = 0ull;
-      const uint64_t cex = block_excl_scan(wl[0] + wl[1], L.redu, &ctot);
-      if (wl[0] && cex <= ltarget && ltarget < cex + wl[0]) L.misc[3] = (int)(cb + 2 * tid);
-      if (wl[1] && cex + wl[0] <= ltarget && ltarget < cex + wl[0] + wl[1])
-        L.misc[3] = (int)(cb + 2 * tid + 1);
-      __syncthreads();
     }
+    __builtin_amdgcn_wave_barrier();
+    uint64_t sw[kSlotsPerLane];
+    uint64_t lane_s = 0ull;
+#pragma unroll
+    for (int i = 0; i < kSlotsPerLane; ++i) {
+      sw[i] = F.dw[draw_slot(kSlotsPerLane * l + i)];
+      lane_s += sw[i];
+    }
+    const uint64_t is = wave_incl_scan(lane_s);
+    uint64_t pre = is - lane_s;
+    int my_tok = -1;
+#pragma unroll
+    for (int i = 0; i < kSlotsPerLane; ++i) {
+      if (sw[i] && pre <= ltarget && ltarget < pre + sw[i]) my_tok = cb + kSlotsPerLane * l + i;
+      pre += sw[i];
+    }
+    const uint64_t hitt = __ballot(my_tok >= 0);
+    if (hitt) token = read_lane(my_tok, __builtin_ctzll(hitt));
   }
-  const int token = cstar >= 0 ? L.misc[3] : -1;
 
   // ---- probe token (MTP acceptance): its kept weight
   uint64_t probe_w = 0ull;
   if (probe >= 0 && probe < V && !overflow && active) {
-    if (tid == 0) {
-      L.misc[4] = 0;
-      L.misc[5] = 0;
-    }
-    __syncthreads();
-    for (int r = tid; r < nc; r += kThreads)
-      if (F.keep[r] && key_id(F.keys[r]) == probe) L.misc[4] = 1;
+    bool kc = false;
+    for (int r = l; r < nc; r += 64)
+      if (F.keep[r] && key_id(F.keys[r]) == probe) kc = true;
+    const bool kept_cand = __ballot(kc) != 0ull;
     int32_t e0 = 0, e1 = 0;
     if (P.row_ptr && P.entries) {
       e0 = P.row_ptr[row];
       e1 = P.row_ptr[row + 1];
     }
-    for (int32_t e = e0 + tid; e < e1; e += kThreads) {
-      const lsamp_penalty_entry ent = P.entries[e];
-      if (ent.token != probe) continue;
-      const float x = patch_value(c, prm, load_scalar<DT>(rowp, probe), ent, DT);
-      F.cx[0] = x;
-      L.misc[5] = 1;
+    int32_t pe = -1;
+    for (int32_t e = e0 + l; e < e1; e += 64)
+      if (P.entries[e].token == probe) pe = e;
+    const uint64_t hp = __ballot(pe >= 0);
+    float x;
+    if (hp) {
+      const int32_t e = read_lane(pe, __builtin_ctzll(hp));
+      x = patch_value(c, prm, load_scalar<DT>(rowp, probe), P.entries[e], DT);
+    } else {
+      x = load_scalar<DT>(rowp, probe);
     }
-    __syncthreads();
-    if (tid == 0) {
-      float x = L.misc[5] ? F.cx[0] : load_scalar<DT>(rowp, probe);
-      if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, probe) || x != x) x = kNegInf;
-      const int cls = classify(make_rule(info, c), x);
-      L.misc64[2] = (cls == kKept || (cls == kCand && L.misc[4]))
-                        ? weight(to_filter(c, x), y_max, c.scale)
-                        : 0ull;
-    }
-    __syncthreads();
-    probe_w = L.misc64[2];
+    if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, probe) || x != x) x = kNegInf;
+    const int cls = classify(make_rule(info, c), x);
+    probe_w = (cls == kKept || (cls == kCand && kept_cand)) ? weight(to_filter(c, x), y_max, c.scale)
+                                                             : 0ull;
   }
 
-  if (tid == 0) {
+  if (l == 0) {
     uint32_t flags = info.flags;
     if (overflow) flags |= LSAMP_ROW_OVERFLOW;
     if (!overflow && (token < 0 || W == 0ull)) flags |= LSAMP_ROW_EMPTY;
@@ -952,7 +956,9 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
       st.probe_prob = W ? (float)((double)probe_w / (double)W) : 0.0f;
       P.stats[row] = st;
     }
-    ws.rows[row].kept_cands = overflow ? 0 : kept_c;
+    RowInfo out = info;
+    out.kept_cands = overflow ? 0 : kept_c;
+    ws.rows[row] = out;
     ws.cand_count[row] = 0u;
     ws.arrive_select[row] = 0u;
     if (fused) ws.arrive_stats[row] = 0u;
@@ -1173,13 +1179,33 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     // (rows that build one) or whether the slice holds a finite logit
     SliceSummary* Ssum = ws.summaries + ((size_t)row * kMaxSlices + slice);
     int32_t nfin = 0;
+    double zs = 0.0;  // total mass relative to the slice's top bin
     if (want_hist) {
+      const double inv_frac = 1.0 / (double)(1ull << kMassFracBits);
       for (int i = tid; i < kHist; i += kThreads) {
         const uint64_t w = L.u.hist[i];
-        nfin += (int32_t)(w >> kCountShift);
         st_coherent(&Ssum->hist[i], w);
+        if (w == 0ull) continue;
+        nfin += (int32_t)(w >> kCountShift);
+        // the tail bin's mass is relative to the window's lowest bin edge
+        zs += (double)(w & kMassMask) * inv_frac *
+              exp(-(double)(i < kBins ? i : kBins - 1) / 32.0);
       }
-      nfin = block_sum(nfin, L.redi);
+      nfin = wave_sum(nfin);
+      zs = wave_sum(zs);
+      const int wv = tid >> 6;
+      if ((tid & 63) == 0) {
+        L.redi[wv] = nfin;
+        L.redd[wv] = zs;
+      }
+      __syncthreads();
+      nfin = 0;
+      zs = 0.0;
+#pragma unroll
+      for (int i = 0; i < kWaves; ++i) {
+        nfin += L.redi[i];
+        zs += L.redd[i];
+      }
     } else {
       nfin = (has_finite || posinf) ? 1 : 0;
     }
@@ -1188,41 +1214,39 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       st_coherent(&Ssum->top_bin, top);
       st_coherent(&Ssum->flags, sflags);
       st_coherent(&Ssum->n_finite, nfin);
+      st_coherent_f64(&Ssum->z, zs);
     }
-    const bool is_last = arrive_last(&ws.arrive_stats[row], (uint32_t)G, &L.last);
-    if (is_last) {
-      merge_row(ws, P, row, c, prm, L);
-      info = L.info;
-      if (MODE == kFused) {
-        if (tid == 0) publish_rowinfo(ws.rows + row, info);
-        drain_memory();
-        __syncthreads();
-        if (tid == 0)
-          (void)__hip_atomic_fetch_add(&ws.arrive_stats[row], kReady, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-        if (tid == 0) {
-          ws.rows[row] = info;
-          ws.arrive_stats[row] = 0u;
-        }
-        return;
-      }
-    } else {
-      if (MODE != kFused) return;
-      // wait for the row's merge (bounded: the grid always drains)
+    if (MODE == kFused) {
+      // all-gather: wait until every slice of the row has published, then
+      // merge here (the merge is deterministic, so all slices agree)
+      drain_memory();
+      __syncthreads();
       if (tid == 0) {
-        int it = 0;
-        while (ld_coherent(&ws.arrive_stats[row]) < kReady) {
-          if (++it >= kSpinLimit) {
-            atomicOr(ws.status, kStatusSpinTimeout);
-            break;
+        const uint32_t prev = __hip_atomic_fetch_add(&ws.arrive_stats[row], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        if (prev + 1u < (uint32_t)G) {
+          // bounded: a wait that runs out sets a status bit, so the grid drains
+          int it = 0;
+          while (ld_coherent(&ws.arrive_stats[row]) < (uint32_t)G) {
+            if (++it >= kSpinLimit) {
+              atomicOr(ws.status, kStatusSpinTimeout);
+              break;
+            }
+            __builtin_amdgcn_s_sleep(2);
           }
-          __builtin_amdgcn_s_sleep(4);
         }
-        L.info = read_rowinfo(ws.rows + row);
       }
       __syncthreads();
+      merge_row(ws, P, row, c, prm, L);
       info = L.info;
+    } else {
+      if (!arrive_last(&ws.arrive_stats[row], (uint32_t)G, &L.last)) return;
+      merge_row(ws, P, row, c, prm, L);
+      if (tid == 0) {
+        ws.rows[row] = L.info;
+        ws.arrive_stats[row] = 0u;
+      }
+      return;
     }
   } else {
     if (tid == 0) L.info = ws.rows[row];
