@@ -239,8 +239,7 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
 // Histogram bin of a transformed logit: floor(x * c32) with c32 = 32 / T,
 // clamped so the integer conversion is defined for any finite x.
 __device__ __forceinline__ float bin_pos(float x, float c32) {
-  const float s = x * c32;
-  return __builtin_fminf(__builtin_fmaxf(s, -1.0e9f), 1.0e9f);
+  return __builtin_amdgcn_fmed3f(x * c32, -1.0e9f, 1.0e9f);
 }
 __device__ __forceinline__ int bin_of(float x, float c32) {
   return (int)__builtin_floorf(bin_pos(x, c32));

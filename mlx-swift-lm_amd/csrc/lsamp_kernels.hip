@@ -1140,8 +1140,8 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         const float fb = __builtin_floorf(s);
         const int j = top - (int)fb;
         const bool in_win = j < kBins;
-        const float e =
-            __builtin_amdgcn_exp2f((s - (in_win ? fb : tail_edge)) * Lg + (float)kMassFracBits);
+        const float e = __builtin_amdgcn_exp2f(
+            __builtin_fmaf(s - (in_win ? fb : tail_edge), Lg, (float)kMassFracBits));
         atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.hist[in_win ? j : kTail]),
                   (unsigned long long)((1ull << kCountShift) | (uint64_t)(uint32_t)e));
       };
@@ -1366,9 +1366,29 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       }
     }
   }
-  ent = block_sum(ent, L.redd);
-  min_kept = block_min(min_kept, L.redf);
-  n_kept = block_sum(n_kept, L.redi);
+  {
+    // one exchange for the three work-group reductions
+    ent = wave_sum(ent);
+    min_kept = wave_min(min_kept);
+    n_kept = wave_sum(n_kept);
+    const int wv = tid >> 6;
+    __syncthreads();
+    if ((tid & 63) == 0) {
+      L.redd[wv] = ent;
+      L.redf[wv] = min_kept;
+      L.redi[wv] = n_kept;
+    }
+    __syncthreads();
+    ent = 0.0;
+    min_kept = kPosInf;
+    n_kept = 0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      ent += L.redd[i];
+      min_kept = __builtin_fminf(min_kept, L.redf[i]);
+      n_kept += L.redi[i];
+    }
+  }
 
   // publish chunk sums, candidates, kept list, partials
   const int64_t chunk0 = base / kChunk;
