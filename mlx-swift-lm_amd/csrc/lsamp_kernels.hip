@@ -57,7 +57,9 @@ struct RowCtx {
   int32_t kind;
   float T;        // temperature dividing the filter space (CBv2 sampled rows)
   bool tempered;  // filter space is x / T
-  float c32;      // histogram scale: bin = floor(x * c32)
+  float c32;      // histogram scale: bin = floor(x * c32), x the transformed logit
+  float lg;       // log2(e) / (32 * T_f): bin units -> log2 of filter-space mass
+  double tf;      // T_f, the filter space's temperature (T when tempered, else 1)
   float scale;    // draw scale (mlx-lm: fl(1 / T))
 };
 
@@ -79,7 +81,12 @@ __device__ __forceinline__ RowCtx make_ctx(int32_t sem, const lsamp_row_params& 
       c.scale = 1.0f / p.temperature;
     }
   }
-  c.c32 = c.tempered ? 32.0f / c.T : 32.0f;
+  // Bins are 1/32 of the transformed logit x itself (not of x / T): the
+  // window of kBins bins then spans 32 logit units at every temperature, and
+  // a low temperature cannot push a top-k cut out of it.  Masses carry T.
+  c.c32 = 32.0f;
+  c.tf = c.tempered ? (double)c.T : 1.0;
+  c.lg = (float)(1.4426950408889634 / (32.0 * c.tf));
   return c;
 }
 
@@ -282,7 +289,7 @@ struct FinalLds {
   uint8_t cflag[kChunk];
 };
 union PhaseLds {
-  uint64_t hist[kHist];
+  uint64_t hist[kHist + 64];  // + one discard word per lane
   MergeLds m;
   SelectLds s;
   FinalLds f;
@@ -414,7 +421,10 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
   info.kept_cands = 0;
   info.pad = 0;
   const float s_top = bin_pos(row_max, c.c32);
-  info.q_top = s_top * (1.0f / 32.0f);
+  // masses are relative to e^q_top, q_top the row's top in filter units
+  info.q_top = (float)((double)s_top / (32.0 * c.tf));
+  const double q_ref = (double)info.q_top;
+  const double bin_t = 1.0 / (32.0 * c.tf);  // filter units per bin
 
   if (info.mode == kModeNormal && c.kind == LSAMP_KIND_ARGMAX) {
     info.cut = 0;
@@ -423,7 +433,7 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
     const double inv_frac = 1.0 / (double)(1ull << kMassFracBits);
     // total mass relative to the row top: each slice's total is relative to
     // its own top bin
-    const double z = wave_sum((l < G && hn > 0) ? hz * exp(((double)htop - (double)s_top) / 32.0)
+    const double z = wave_sum((l < G && hn > 0) ? hz * exp((double)(htop + 1) * bin_t - q_ref)
                                                 : 0.0);
     info.z = z;
     const int32_t k_lim = (prm.top_k > 0 && (int64_t)prm.top_k < V) ? prm.top_k : 0;
@@ -445,7 +455,7 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
     const bool m_on = c.kind == LSAMP_KIND_FILTERED && mp > 0.0f;
     int32_t j_t = kBins + 1;
     if (m_on) {
-      const float st = s_top + 32.0f * __builtin_logf(mp);
+      const float st = s_top + (float)(32.0 * c.tf) * __builtin_logf(mp);
       j_t = row_top - (int32_t)__builtin_floorf(__builtin_fmaxf(st, -1.0e9f));
       if (j_t < 0) j_t = 0;
       if (j_t > kBins) j_t = kBins;
@@ -515,7 +525,7 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
         const int j = 64 * kBlk * b + 64 * k + l;
         const int32_t cj = (int32_t)cnt[k];
         const double mj = cj ? (double)msum[k] * inv_frac *
-                                   exp(((double)(row_top - j) - (double)s_top) / 32.0)
+                                   exp((double)(row_top - j + 1) * bin_t - q_ref)
                              : 0.0;
         const int32_t ic = wave_incl_scan(cj);
         const double im = wave_incl_scan(mj);
@@ -1133,24 +1143,29 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     const int32_t top = has_finite ? bin_of(xmax, c.c32) : 0;
     const bool want_hist = has_finite && c.kind != LSAMP_KIND_ARGMAX;
     if (want_hist) {
-      const float Lg = 1.4426950408889634f / 32.0f;
       const float tail_edge = (float)(top - kBins + 1);
+      // Branch-free per token (excluded tokens add zero to a discard word of
+      // their lane), so the tokens of a quad interleave.
+      const int discard = kHist + (tid & 63);
+      // Masses are relative to the top edge of the token's bin (in-window,
+      // j < kBins, i.e. floor(s) >= tail_edge) or to tail_edge (the tail):
+      // both are s - max(floor(s) + 1, tail_edge) <= 0, so every token adds
+      // at most 2^kMassFracBits.  A -inf token's mass is 0.
       auto add = [&](float x) {
+        const bool ok = x > kNegInf;
         const float s = bin_pos(x, c.c32);
         const float fb = __builtin_floorf(s);
         const int j = top - (int)fb;
-        const bool in_win = j < kBins;
-        const float e = __builtin_amdgcn_exp2f(
-            __builtin_fmaf(s - (in_win ? fb : tail_edge), Lg, (float)kMassFracBits));
-        atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.hist[in_win ? j : kTail]),
-                  (unsigned long long)((1ull << kCountShift) | (uint64_t)(uint32_t)e));
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(
+            s - __builtin_amdgcn_fmed3f(fb + 1.0f, tail_edge, 3.0e9f), c.lg, (float)kMassFracBits));
+        const int idx = ok ? (j < kTail ? j : kTail) : discard;
+        const uint32_t hi = ok ? (1u << (kCountShift - 32)) : 0u;
+        atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.hist[idx]),
+                  (unsigned long long)(((uint64_t)hi << 32) | (uint64_t)(uint32_t)e));
       };
       for_quads(S, nq, [&](int g, uint4& v) -> bool {
 #pragma unroll
-        for (int e = 0; e < N; ++e) {
-          const float x = vec_elem<DT>(v, e);
-          if (x > kNegInf) add(x);
-        }
+        for (int e = 0; e < N; ++e) add(vec_elem<DT>(v, e));
         return false;
       });
       for (int j2 = tid; j2 < n_ent; j2 += kThreads) {
@@ -1179,7 +1194,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     // (rows that build one) or whether the slice holds a finite logit
     SliceSummary* Ssum = ws.summaries + ((size_t)row * kMaxSlices + slice);
     int32_t nfin = 0;
-    double zs = 0.0;  // total mass relative to the slice's top bin
+    double zs = 0.0;  // total mass relative to the top edge of the slice's top bin
     if (want_hist) {
       const double inv_frac = 1.0 / (double)(1ull << kMassFracBits);
       for (int i = tid; i < kHist; i += kThreads) {
@@ -1187,9 +1202,9 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         st_coherent(&Ssum->hist[i], w);
         if (w == 0ull) continue;
         nfin += (int32_t)(w >> kCountShift);
-        // the tail bin's mass is relative to the window's lowest bin edge
-        zs += (double)(w & kMassMask) * inv_frac *
-              exp(-(double)(i < kBins ? i : kBins - 1) / 32.0);
+        // bin i's top edge lies i bins below the slice's; the tail's mass is
+        // relative to the window's lowest edge, kBins below
+        zs += (double)(w & kMassMask) * inv_frac * exp(-(double)i / (32.0 * c.tf));
       }
       nfin = wave_sum(nfin);
       zs = wave_sum(zs);

@@ -172,6 +172,29 @@ def test_odd_vocab_sizes(ctx, V):
     compare(cfg, run_gpu(ctx, cfg), run_oracle(cfg), label=f"V={V}")
 
 
+@pytest.mark.parametrize("semantics", [_ffi.SEM_MLXLM, _ffi.SEM_CBV2])
+@pytest.mark.parametrize("T,top_k,top_p,min_p", [
+    (0.1, 50, 1.0, 0.0), (0.05, 1000, 1.0, 0.0), (0.2, 40, 0.9, 0.05),
+    (2.0, 0, 0.95, 0.0), (5.0, 0, 0.99, 0.0), (3.0, 200, 0.9, 0.01)])
+def test_temperature_extremes(ctx, semantics, T, top_k, top_p, min_p):
+    """Low temperatures stretch the filter space (a top-k cut lies tens of
+    nats below the maximum); high ones flatten it (a top-p cut lies deep in
+    the distribution).  Full-vocabulary rows, both semantics."""
+    rng = np.random.default_rng(int(T * 1000) + top_k)
+    V, B = 151936, 6
+    prior = -1.1 * np.log(np.arange(1, V + 1, dtype=np.float64))
+    x = np.stack([rng.normal(0.0, 3.0, V) + prior[rng.permutation(V)] for _ in range(B)])
+    x = x.astype(np.float32)
+    if semantics == _ffi.SEM_MLXLM:
+        p = W.resolve_mlxlm(temperature=T, top_p=top_p, top_k=top_k, min_p=min_p)
+    else:
+        p = W.resolve_cbv2(temperature=T, top_p=top_p, top_k=top_k, min_p=min_p, vocab=V)
+    cfg = small_cfg(semantics, x, [p] * B, rng.random(B, dtype=np.float32))
+    g = run_gpu(ctx, cfg)
+    assert not (g["row_flags"] & _ffi.ROW_OVERFLOW).any(), "no row may overflow"
+    compare(cfg, g, run_oracle(cfg), label=f"T={T} k={top_k} p={top_p} m={min_p}")
+
+
 @pytest.mark.parametrize("n", [1, 2, 3, 4])
 def test_configs_reduced(ctx, n):
     kw = {1: {}, 2: {"rows": 8}, 3: {"rows": 16}, 4: {"rows": 8}}
