@@ -108,6 +108,7 @@ int64_t lsamp_abi_sizeof(const char* name) {
   if (!strcmp(name, "lsamp_verify_args")) return (int64_t)sizeof(lsamp_verify_args);
   if (!strcmp(name, "lsamp_generate_parameters")) return (int64_t)sizeof(lsamp_generate_parameters);
   if (!strcmp(name, "lsamp_cbv2_params")) return (int64_t)sizeof(lsamp_cbv2_params);
+  if (!strcmp(name, "lsamp_launch_info")) return (int64_t)sizeof(lsamp_launch_info);
   return -1;
 }
 

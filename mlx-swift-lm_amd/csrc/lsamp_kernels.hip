@@ -179,6 +179,8 @@ struct ClassRule {
   float c32;
   float screen;  // x * c32 < screen: neither kept nor candidate
   bool posinf;
+  int32_t pinf_cls;  // class of a +inf token in +inf mode: kept, or (argmax
+                     // rows: the first one wins) candidate
 };
 
 __device__ __forceinline__ ClassRule make_rule(const RowInfo& info, const RowCtx& c) {
@@ -186,6 +188,7 @@ __device__ __forceinline__ ClassRule make_rule(const RowInfo& info, const RowCtx
   r.top = info.top_bin;
   r.c32 = c.c32;
   r.posinf = info.mode == kModePosInf;
+  r.pinf_cls = c.kind == LSAMP_KIND_ARGMAX ? kCand : kKept;
   if (info.mode != kModeNormal) {
     r.kc = r.kd = -1;
   } else if (info.cut == kCutNone) {
@@ -212,7 +215,7 @@ __device__ __forceinline__ ClassRule make_rule(const RowInfo& info, const RowCtx
 }
 
 __device__ __forceinline__ int classify(const ClassRule& r, float x) {
-  if (r.posinf) return x == kPosInf ? kKept : kDrop;
+  if (r.posinf) return x == kPosInf ? r.pinf_cls : kDrop;
   if (!__builtin_isfinite(x)) return kDrop;
   int j = r.top - bin_of(x, r.c32);
   j = j < 0 ? 0 : j;
@@ -426,7 +429,9 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
   const double q_ref = (double)info.q_top;
   const double bin_t = 1.0 / (32.0 * c.tf);  // filter units per bin
 
-  if (info.mode == kModeNormal && c.kind == LSAMP_KIND_ARGMAX) {
+  if (c.kind == LSAMP_KIND_ARGMAX && info.mode != kModeEmpty) {
+    // the first maximum: every token of the top bin (in +inf mode every +inf
+    // token) is a candidate and the finalize keeps the first in id order
     info.cut = 0;
     info.count_above = 0;
   } else if (info.mode == kModeNormal) {

@@ -647,14 +647,16 @@ static void sample_row(const lso_sample_args* a, int32_t r, scratch_t* s) {
   const float* y = x;
   if (x_max == -INFINITY) {
     memset(s->keep, 0, (size_t)V);
-  } else if (x_max == INFINITY) {
-    /* +inf logits: the limit of the softmax is uniform over the +inf ids. */
-    for (int32_t i = 0; i < V; ++i) s->keep[i] = (uint8_t)(x[i] == INFINITY);
-  } else if (p->kind == LSAMP_KIND_ARGMAX) {
+  } else if (p->kind == LSAMP_KIND_ARGMAX || !(p->temperature > 0.0f && p->temperature < INFINITY)) {
     /* ArgMaxSampler (Evaluate.swift:394-396); CBv2 greedy rows
-     * (SamplerV2.swift:92) */
+     * (SamplerV2.swift:92); the first maximum, +inf included.  A sampled row
+     * whose temperature defines no distribution is drawn the same way. */
     memset(s->keep, 0, (size_t)V);
     s->keep[argmax_lowest(V, x)] = 1;
+  } else if (x_max == INFINITY) {
+    /* +inf logits in a sampled row: the limit of the softmax is uniform over
+     * the +inf ids. */
+    for (int32_t i = 0; i < V; ++i) s->keep[i] = (uint8_t)(x[i] == INFINITY);
   } else if (a->semantics == LSAMP_SEM_CBV2) {
     cbv2_filter(p, V, x, s, tpm, mpm, tpx);
   } else if (p->kind == LSAMP_KIND_CATEGORICAL) {
