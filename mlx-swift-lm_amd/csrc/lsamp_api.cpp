@@ -149,11 +149,6 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   const size_t o_vstats = take(R * sizeof(lsamp_row_stats));
   const size_t o_vtok = take(R * sizeof(int32_t));
   const size_t o_vfl = take(R * sizeof(uint32_t));
-  const size_t o_vprobe = take(R * sizeof(int32_t));
-  const size_t o_vu = take(R * sizeof(float));
-  const size_t o_vparams = take(R * sizeof(lsamp_row_params));
-  const size_t o_vres = take(R * chunks * sizeof(uint64_t));
-  const size_t o_ares = take(R * sizeof(uint32_t));
   const size_t total = off;
 
   void* block = nullptr;
@@ -189,11 +184,6 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   ws.vstats = reinterpret_cast<lsamp_row_stats*>(b + o_vstats);
   ws.vtokens = reinterpret_cast<int32_t*>(b + o_vtok);
   ws.vflags = reinterpret_cast<uint32_t*>(b + o_vfl);
-  ws.vprobe = reinterpret_cast<int32_t*>(b + o_vprobe);
-  ws.vuniform = reinterpret_cast<float*>(b + o_vu);
-  ws.vparams = reinterpret_cast<lsamp_row_params*>(b + o_vparams);
-  ws.vres_chunk = reinterpret_cast<uint64_t*>(b + o_vres);
-  ws.arrive_resid = reinterpret_cast<uint32_t*>(b + o_ares);
   *out = ctx;
   return ok();
 }
@@ -472,9 +462,80 @@ float lsamp_rng_uniform(uint64_t key, uint32_t purpose) {
 }
 
 lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* stream) {
-  (void)stream;
   if (!ctx || !a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "NULL argument");
-  return fail(LSAMP_ERR_INVALID_ARGUMENT, "lsamp_verify: not available in this build");
+  if (a->mode != LSAMP_VERIFY_RESIDUAL && a->mode != LSAMP_VERIFY_EXACT &&
+      a->mode != LSAMP_VERIFY_TYPICAL)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown verify mode %d", a->mode);
+  if (a->dtype != LSAMP_DTYPE_F32 && a->dtype != LSAMP_DTYPE_BF16 && a->dtype != LSAMP_DTYPE_F16)
+    return fail(LSAMP_ERR_DTYPE, "unsupported dtype %d", a->dtype);
+  if (a->sequences <= 0 || a->window < 2 || a->vocab <= 0)
+    return fail(LSAMP_ERR_SHAPE, "sequences %d / window %d / vocab %d invalid", a->sequences,
+                a->window, a->vocab);
+  if (a->vocab > ctx->ws.max_vocab)
+    return fail(LSAMP_ERR_CAPACITY, "vocab %d above the context's %d", a->vocab,
+                ctx->ws.max_vocab);
+  if (!a->target_logits || !a->draft_tokens || !a->params || !a->uniforms || !a->accepted ||
+      !a->tokens)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT,
+                "target_logits, draft_tokens, params, uniforms, accepted and tokens are required");
+  const bool residual = a->mode == LSAMP_VERIFY_RESIDUAL;
+  if (residual && !a->draft_logits)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "RESIDUAL mode needs draft_logits");
+  if (a->mode == LSAMP_VERIFY_TYPICAL && !(a->typical_delta > 0.0f))
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "TYPICAL mode needs typical_delta > 0");
+  const int64_t S = a->sequences, W = a->window, D = W - 1;
+  const int64_t rows = S * W + (residual ? S * D : 0);
+  if (rows > ctx->ws.max_rows)
+    return fail(LSAMP_ERR_CAPACITY, "verify needs %lld rows, the context holds %d",
+                (long long)rows, ctx->ws.max_rows);
+
+  // every target (and, for RESIDUAL, draft) position is one sampling row
+  SamplePlan P{};
+  P.semantics = LSAMP_SEM_CBV2;
+  P.rows = (int32_t)rows;
+  P.vocab = a->vocab;
+  P.dtype = a->dtype;
+  P.row_stride = a->vocab;
+  const int32_t bpc = ctx->blocks_per_cu[a->dtype];
+  const int32_t slots = ctx->cus * (bpc > 0 ? bpc : 1);
+  plan_slices(P.rows, P.vocab, slots, &P.slices, &P.slice_len, &P.nchunks);
+  P.fused = ctx->mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;
+  P.rows_per_round = P.fused ? slots / P.slices : P.rows;
+  const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
+  P.aligned = aligned16(a->target_logits) && (!residual || aligned16(a->draft_logits)) &&
+              ((size_t)a->vocab * es) % 16 == 0;
+  P.logits = a->target_logits;
+  P.logits2 = residual ? a->draft_logits : a->target_logits;
+  P.rows_split = (int32_t)(S * W);
+  P.vwin = (int32_t)W;
+  P.params = a->params;
+  P.uniforms = a->uniforms;
+  P.probe_tokens = a->draft_tokens;
+  P.tokens = ctx->ws.vtokens;
+  P.row_flags = ctx->ws.vflags;
+  P.stats = ctx->ws.vstats;
+  VerifyPlan Q{};
+  Q.mode = a->mode;
+  Q.sequences = a->sequences;
+  Q.window = a->window;
+  Q.vocab = a->vocab;
+  Q.dtype = a->dtype;
+  Q.semantics = LSAMP_SEM_CBV2;
+  Q.typical_delta = a->typical_delta;
+  Q.target = a->target_logits;
+  Q.draft = a->draft_logits;
+  Q.draft_tokens = a->draft_tokens;
+  Q.params = a->params;
+  Q.uniforms = a->uniforms;
+  Q.accepted = a->accepted;
+  Q.tokens = a->tokens;
+  Q.accept_mask = a->accept_mask;
+  DeviceGuard guard(ctx->device);
+  int err = launch_sample(ctx->ws, P, stream, nullptr);
+  if (err == 0) err = launch_verify_finish(ctx->ws, Q, stream);
+  if (err != 0)
+    return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+  return ok();
 }
 
 }  // extern "C"

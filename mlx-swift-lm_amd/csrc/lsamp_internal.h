@@ -120,15 +120,10 @@ struct Workspace {
   uint32_t* arrive_stats;   // [max_rows]
   uint32_t* arrive_select;  // [max_rows]
   uint32_t* status;         // [1] sticky error bits (kStatus*)
-  // MTP verification scratch
-  lsamp_row_stats* vstats;    // [max_rows]
-  int32_t* vtokens;           // [max_rows]
-  uint32_t* vflags;           // [max_rows]
-  int32_t* vprobe;            // [max_rows]
-  float* vuniform;            // [max_rows]
-  lsamp_row_params* vparams;  // [max_rows]
-  uint64_t* vres_chunk;       // [max_rows][max_chunks] residual chunk sums
-  uint32_t* arrive_resid;     // [max_rows]
+  // MTP verification: the sampled rows' outputs
+  lsamp_row_stats* vstats;  // [max_rows]
+  int32_t* vtokens;         // [max_rows]
+  uint32_t* vflags;         // [max_rows]
 };
 
 // Sticky device status bits.
@@ -150,6 +145,12 @@ struct SamplePlan {
   const void* logits;
   const void* logits2;     // rows >= rows_split read logits2 (MTP draft rows)
   int32_t rows_split;
+  // MTP verification layout (vwin = 0: a plain sampling step).  Rows below
+  // rows_split are target positions (s, j), row = s * vwin + j; the others
+  // are draft positions (s, j), row - rows_split = s * (vwin - 1) + j.  Each
+  // row uses params[s], the uniform [s, j] of a [S, vwin] array, and probes
+  // the draft token [s, j] of a [S, vwin - 1] array (none at j = vwin - 1).
+  int32_t vwin;
   const lsamp_row_params* params;
   const int32_t* row_ptr;
   const lsamp_penalty_entry* entries;
@@ -167,11 +168,33 @@ struct SamplePlan {
   lsamp_row_stats* stats;
 };
 
+// MTP verification outcome computation (after the sampling launch).
+struct VerifyPlan {
+  int32_t mode;        // lsamp_verify_mode
+  int32_t sequences;   // S
+  int32_t window;      // W
+  int32_t vocab;
+  int32_t dtype;
+  int32_t semantics;   // LSAMP_SEM_CBV2
+  float typical_delta;
+  const void* target;  // [S, W, V]
+  const void* draft;   // [S, W-1, V]
+  const int32_t* draft_tokens;
+  const lsamp_row_params* params;
+  const float* uniforms;
+  int32_t* accepted;
+  int32_t* tokens;
+  uint8_t* accept_mask;
+};
+
 // Kernel launchers (lsamp_kernels.hip).  Return a hipError_t as int.
 // `events` (3 hipEvent_t or NULL) bracket the step: before, between the two
 // kernels (split mode; same as before in fused mode), after.
 int launch_sample(const Workspace& ws, const SamplePlan& plan, void* stream, void* const* events);
 // Work-groups of the fused kernel that fit on one CU (occupancy query).
 int fused_blocks_per_cu(int dtype);
+// Acceptance, residual / bonus draws and outputs of an MTP verification whose
+// rows were sampled by launch_sample into ws.v* (one work-group per sequence).
+int launch_verify_finish(const Workspace& ws, const VerifyPlan& plan, void* stream);
 
 }  // namespace lsamp

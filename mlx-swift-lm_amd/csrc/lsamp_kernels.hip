@@ -37,7 +37,6 @@ namespace {
 using namespace dev;
 
 constexpr int kSliceWords = kMaxSliceLen / 32;       // penalty bitmap words
-constexpr int kFinalPerThread = kCandCap / kThreads;  // sorted candidates per thread
 constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
 
 enum TaskMode { kFused = 0, kStatsOnly = 1, kSelectOnly = 2 };
@@ -151,6 +150,24 @@ __device__ __forceinline__ uint32_t mask_allow_bits(const uint32_t* mrow, int32_
 __device__ __forceinline__ bool mask_allows(const uint32_t* mrow, int32_t mask_words,
                                             int32_t mask_bits, int32_t tail, int32_t i) {
   return mask_allow_bits(mrow, mask_words, mask_bits, tail, i, 1) != 0u;
+}
+
+// Per-row parameter, uniform and probe slots (plain step: the row itself).
+__device__ __forceinline__ int params_index(const SamplePlan& P, int row) {
+  if (P.vwin == 0) return row;
+  return row < P.rows_split ? row / P.vwin : (row - P.rows_split) / (P.vwin - 1);
+}
+__device__ __forceinline__ int uniform_index(const SamplePlan& P, int row) {
+  if (P.vwin == 0 || row < P.rows_split) return row;
+  const int d = row - P.rows_split, D = P.vwin - 1;
+  return (d / D) * P.vwin + d % D;
+}
+__device__ __forceinline__ int probe_index(const SamplePlan& P, int row) {
+  if (P.vwin == 0) return row;
+  const int D = P.vwin - 1;
+  if (row >= P.rows_split) return row - P.rows_split;
+  const int j = row % P.vwin;
+  return j < D ? (row / P.vwin) * D + j : -1;
 }
 
 __device__ __forceinline__ const char* row_base(const SamplePlan& P, int row) {
@@ -647,10 +664,11 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
     if (l == 0) {
       tc = (int32_t)ld_coherent(&ws.cand_count[row]);
       if (P.uniforms)
-        u = P.uniforms[row];
+        u = P.uniforms[uniform_index(P, row)];
       else if (P.philox_keys)
         u = philox_uniform(P.philox_keys[row], 0u);
-      pr = P.probe_tokens ? P.probe_tokens[row] : -1;
+      const int pi = probe_index(P, row);
+      pr = (P.probe_tokens && pi >= 0) ? P.probe_tokens[pi] : -1;
     }
     total_cand = read_lane(tc, 0);
     u_draw = read_lane(u, 0);
@@ -1048,7 +1066,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   constexpr int ES = Vec<DT>::ESIZE;
   const int tid = fresh_tid();
   const int G = P.slices;
-  const lsamp_row_params prm = P.params[row];
+  const lsamp_row_params prm = P.params[params_index(P, row)];
   const RowCtx c = make_ctx(P.semantics, prm);
   const int64_t V = P.vocab;
   const int64_t base = (int64_t)slice * P.slice_len;
@@ -1495,7 +1513,185 @@ int launch_dt(const Workspace& ws, const SamplePlan& P, hipStream_t st, void* co
   return (int)hipGetLastError();
 }
 
+// ============================================================ MTP verify
+// Is (y, id) among the n kept candidates of a row (sorted by cand_key,
+// descending)?  Binary search in global memory; called for cut-bin tokens only.
+__device__ __forceinline__ bool in_kept_list(const Candidate* rc, int n, uint64_t key) {
+  int lo = 0, hi = n - 1;
+  while (lo <= hi) {
+    const int mid = (lo + hi) >> 1;
+    const uint64_t k = cand_key(rc[mid].y, rc[mid].id);
+    if (k == key) return true;
+    if (k > key) lo = mid + 1; else hi = mid - 1;
+  }
+  return false;
+}
+
+// Kept weight of token i in a sampled row, from the row's decision (RowInfo),
+// its kept candidates and its logit.
+template <int DT>
+__device__ __forceinline__ uint64_t kept_weight_of(const RowCtx& c, const RowInfo& info,
+                                                   const ClassRule& rule, const Candidate* rc,
+                                                   const char* rowp, int32_t i) {
+  float x = load_scalar<DT>(rowp, i);
+  if (x != x) x = kNegInf;
+  const int cls = classify(rule, x);
+  if (cls == kDrop) return 0ull;
+  const float y = to_filter(c, x);
+  if (cls == kCand && !in_kept_list(rc, info.kept_cands, cand_key(y, i))) return 0ull;
+  const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
+  return weight(y, y_max, c.scale);
+}
+
+// One work-group per sequence.  Rows were sampled into ws.v* by launch_sample:
+// target (s, j) at row s*W + j, draft (s, j) at row S*W + s*(W-1) + j; each
+// row's draw used uniform [s, j] and probed draft token [s, j].
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, VerifyPlan Q) {
+  __shared__ int32_t s_rej;
+  __shared__ uint64_t s_red[kWaves];
+  __shared__ int32_t s_tok;
+  const int s = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int W = Q.window, D = W - 1, S = Q.sequences;
+  const int32_t V = Q.vocab;
+  int32_t* tok = Q.tokens + (size_t)s * W;
+  if (tid == 0) {
+    const lsamp_row_params prm = Q.params[s];
+    const bool greedy = make_ctx(Q.semantics, prm).kind == LSAMP_KIND_ARGMAX;
+    const int32_t* drafts = Q.draft_tokens + (size_t)s * D;
+    const float* u = Q.uniforms + (size_t)s * W;
+    uint8_t* am = Q.accept_mask ? Q.accept_mask + (size_t)s * D : nullptr;
+    bool failed = false;  // a row whose keep set could not be resolved
+    for (int j = 0; j < W; ++j) {
+      tok[j] = -1;
+      if (ws.vflags[s * W + j] & LSAMP_ROW_OVERFLOW) failed = true;
+      if (Q.mode == LSAMP_VERIFY_RESIDUAL && j < D &&
+          (ws.vflags[S * W + s * D + j] & LSAMP_ROW_OVERFLOW))
+        failed = true;
+    }
+    if (am)
+      for (int j = 0; j < D; ++j) am[j] = 0;
+    int rej = -1;
+    if (failed) {
+      Q.accepted[s] = 0;
+    } else if (Q.mode == LSAMP_VERIFY_RESIDUAL) {
+      int j = 0;
+      for (; j < D; ++j) {
+        const lsamp_row_stats& st = ws.vstats[s * W + j];
+        const lsamp_row_stats& sd = ws.vstats[S * W + s * D + j];
+        const double pt = st.kept_weight ? (double)st.probe_weight / (double)st.kept_weight : 0.0;
+        const double pd = sd.kept_weight ? (double)sd.probe_weight / (double)sd.kept_weight : 0.0;
+        const bool accept = pd > 0.0 ? ((double)u[j] < pt / pd) : (pt > 0.0);
+        if (!accept) break;
+        tok[j] = drafts[j];
+        if (am) am[j] = 1;
+      }
+      Q.accepted[s] = j;
+      if (j == D)
+        tok[D] = ws.vtokens[s * W + D];  // the bonus: the target row's own draw
+      else
+        rej = j;
+    } else {
+      int prefix = 0;
+      bool still = true;
+      for (int j = 0; j < W; ++j) {
+        tok[j] = ws.vtokens[s * W + j];
+        if (j >= D) continue;
+        bool accept;
+        if (Q.mode == LSAMP_VERIFY_EXACT || greedy) {
+          accept = tok[j] == drafts[j];
+        } else {
+          // p(draft) > min(1, delta * e^-H) on the filtered, tempered row
+          const lsamp_row_stats& st = ws.vstats[s * W + j];
+          const double p = st.kept_weight ? (double)st.probe_weight / (double)st.kept_weight : 0.0;
+          const double fl = fmin(1.0, (double)Q.typical_delta * exp(-(double)st.kept_entropy));
+          accept = p > fl;
+        }
+        if (am) am[j] = accept ? 1 : 0;
+        if (still && accept)
+          ++prefix;
+        else
+          still = false;
+      }
+      Q.accepted[s] = prefix;
+    }
+    s_rej = rej;
+  }
+  __syncthreads();
+  const int j = s_rej;
+  if (j < 0) return;
+
+  // residual draw at the first rejected position: normalize(max(0, p_t - p_d))
+  // with both distributions quantized to 2^-52, by inverse CDF in id order
+  const lsamp_row_params prm = Q.params[s];
+  const RowCtx c = make_ctx(Q.semantics, prm);
+  const int rt = s * W + j, rd = S * W + s * D + j;
+  const RowInfo it = ws.rows[rt], id = ws.rows[rd];
+  const ClassRule qt = make_rule(it, c), qd = make_rule(id, c);
+  const Candidate* ct = ws.cands + (size_t)rt * kCandCap;
+  const Candidate* cd = ws.cands + (size_t)rd * kCandCap;
+  const uint64_t Wt = ws.vstats[rt].kept_weight, Wd = ws.vstats[rd].kept_weight;
+  const size_t es = DT == LSAMP_DTYPE_F32 ? 4 : 2;
+  const char* trow = reinterpret_cast<const char*>(Q.target) + (size_t)rt * V * es;
+  const char* drow = reinterpret_cast<const char*>(Q.draft) + (size_t)(s * D + j) * V * es;
+  auto res_of = [&](int32_t i, bool use_residual) -> uint64_t {
+    const uint64_t wt = kept_weight_of<DT>(c, it, qt, ct, trow, i);
+    if (!use_residual) return wt;
+    if (wt == 0ull) return 0ull;
+    const uint64_t wd = kept_weight_of<DT>(c, id, qd, cd, drow, i);
+    const uint64_t a = (uint64_t)((double)wt / (double)Wt * 4503599627370496.0);
+    const uint64_t b = Wd ? (uint64_t)((double)wd / (double)Wd * 4503599627370496.0) : 0ull;
+    return a > b ? a - b : 0ull;
+  };
+  const int32_t per = (V + kThreads - 1) / kThreads;
+  const int32_t i0 = tid * per, i1 = i0 + per < V ? i0 + per : V;
+  const float ur = Q.uniforms[(size_t)s * W + D];
+  int tokout = -1;
+  for (int pass = 0; pass < 2 && tokout < 0; ++pass) {
+    // pass 0: the residual; pass 1 (only when it is empty): the target itself
+    const bool use_residual = pass == 0;
+    uint64_t mine = 0ull;
+    for (int32_t i = i0; i < i1; ++i) mine += res_of(i, use_residual);
+    uint64_t tot = 0ull;
+    const uint64_t ex = block_excl_scan(mine, s_red, &tot);
+    if (tot == 0ull) continue;
+    const uint64_t target = scaled_target(uniform_u32(ur), tot);
+    if (tid == 0) s_tok = -1;
+    __syncthreads();
+    if (ex <= target && target < ex + mine) {
+      uint64_t cum = ex;
+      for (int32_t i = i0; i < i1; ++i) {
+        const uint64_t w = res_of(i, use_residual);
+        cum += w;
+        if (w && cum > target) {
+          s_tok = i;
+          break;
+        }
+      }
+    }
+    __syncthreads();
+    tokout = s_tok;
+  }
+  if (tid == 0) tok[j] = tokout;
+}
+
+template <int DT>
+int launch_verify_dt(const Workspace& ws, const VerifyPlan& Q, hipStream_t st) {
+  hipLaunchKernelGGL(k_verify_finish<DT>, dim3((unsigned)Q.sequences), dim3(kThreads), 0, st, ws, Q);
+  return (int)hipGetLastError();
+}
+
 }  // namespace
+
+int launch_verify_finish(const Workspace& ws, const VerifyPlan& Q, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (Q.dtype) {
+    case LSAMP_DTYPE_F32: return launch_verify_dt<LSAMP_DTYPE_F32>(ws, Q, st);
+    case LSAMP_DTYPE_BF16: return launch_verify_dt<LSAMP_DTYPE_BF16>(ws, Q, st);
+    default: return launch_verify_dt<LSAMP_DTYPE_F16>(ws, Q, st);
+  }
+}
 
 int launch_sample(const Workspace& ws, const SamplePlan& P, void* stream, void* const* events) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

@@ -133,6 +133,23 @@ class Context:
         prep.launch()
         return prep.outputs()
 
+    # ----------------------------------------------------------------- verify
+    def prepare_verify(self, target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens,
+                       params, uniforms, *, mode: int = _ffi.VERIFY_RESIDUAL,
+                       typical_delta: float = 0.0) -> "PreparedVerify":
+        return PreparedVerify(self, target, draft, draft_tokens, params, uniforms, mode,
+                              typical_delta)
+
+    def verify(self, target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens, params,
+               uniforms, **kw) -> dict:
+        """MTP verification (lsamp_verify): target [S, W, V], draft [S, W-1, V]
+        (RESIDUAL mode), draft_tokens [S, W-1], CBv2-resolved params [S],
+        uniforms [S, W].  Returns accepted [S], tokens [S, W], accept_mask
+        [S, W-1] as device tensors."""
+        prep = self.prepare_verify(target, draft, draft_tokens, params, uniforms, **kw)
+        prep.launch()
+        return prep.outputs()
+
 
 class PreparedSample:
     """A fully bound lsamp_sample call: every input and output buffer is a
@@ -238,6 +255,62 @@ class PreparedSample:
 
     def stats_numpy(self) -> np.ndarray:
         return self.stats.cpu().numpy().view(STATS_DTYPE)
+
+
+class PreparedVerify:
+    """A fully bound lsamp_verify call (device buffers kept alive here)."""
+
+    def __init__(self, ctx: Context, target, draft, draft_tokens, params, uniforms, mode,
+                 typical_delta):
+        if target.dim() != 3 or not target.is_contiguous():
+            raise ValueError("target must be a contiguous [S, W, V] tensor")
+        S, W, V = target.shape
+        dev = target.device
+        self.ctx = ctx
+        self.keep_alive = [target]
+        a = _ffi.VerifyArgs()
+        a.mode = mode
+        a.sequences, a.window, a.vocab = S, W, V
+        a.dtype = LSAMP_DTYPE[target.dtype]
+        a.target_logits = target.data_ptr()
+        if draft is not None:
+            if tuple(draft.shape) != (S, W - 1, V) or not draft.is_contiguous():
+                raise ValueError("draft must be a contiguous [S, W-1, V] tensor")
+            if draft.dtype != target.dtype:
+                raise ValueError("draft and target must share a dtype")
+            self.keep_alive.append(draft)
+            a.draft_logits = draft.data_ptr()
+
+        def dev_tensor(x, np_dtype):
+            if isinstance(x, torch.Tensor):
+                return x.to(dev).contiguous()
+            return torch.from_numpy(np.ascontiguousarray(x, np_dtype)).to(dev)
+
+        dt = dev_tensor(draft_tokens, np.int32)
+        u = dev_tensor(uniforms, np.float32)
+        pr = params if isinstance(params, torch.Tensor) else to_device_bytes(params_array(params), dev)
+        self.keep_alive += [dt, u, pr]
+        a.draft_tokens = dt.data_ptr()
+        a.uniforms = u.data_ptr()
+        a.params = pr.data_ptr()
+        a.typical_delta = typical_delta
+        self.accepted = torch.empty(S, dtype=torch.int32, device=dev)
+        self.tokens = torch.empty((S, W), dtype=torch.int32, device=dev)
+        self.accept_mask = torch.empty((S, W - 1), dtype=torch.uint8, device=dev)
+        a.accepted = self.accepted.data_ptr()
+        a.tokens = self.tokens.data_ptr()
+        a.accept_mask = self.accept_mask.data_ptr()
+        self.args = a
+        self._byref = ctypes.byref(a)
+
+    def launch(self, stream: Optional[int] = None) -> None:
+        s = stream if stream is not None else current_stream_handle(self.tokens.device)
+        st = self.ctx.lib.lsamp_verify(self.ctx.handle, self._byref, ctypes.c_void_p(s))
+        if st != 0:
+            raise _ffi.LsampError(st, "lsamp_verify")
+
+    def outputs(self) -> dict:
+        return {"accepted": self.accepted, "tokens": self.tokens, "accept_mask": self.accept_mask}
 
 
 def stats_to_numpy(t: torch.Tensor) -> np.ndarray:
