@@ -12,9 +12,11 @@ per row.  A "step" is one lsamp_sample call over that batch.
   the 256 MB Infinity Cache holds), so each step reads its logits from HBM.
 * kernel times: an eager pass with the library's per-kernel timing hook (HIP
   events on the launch stream, queue kept full by a leading GPU sleep).
-* roofline: algorithmic bytes of one step / average duration of the step's
-  kernel (fused mode: the one kernel; split mode: both kernels, since the
-  second re-reads its slice), against 8 TB/s.
+* roofline: algorithmic bytes of one step / average launch duration of the
+  step's kernel (fused mode: the one kernel, timed by HIP events around the
+  graph replays on its stream; split mode: both kernels from the eager hook),
+  against 8 TB/s; `traffic` is the HBM bytes per launch measured with
+  rocprofv3 FETCH_SIZE / WRITE_SIZE and calibrated on a copy of known size.
 * cpu_baseline: the oracle (the reference op sequence restated in C: full
   sorts, dense penalty tensors) timed on the host's cores on whole steps.
 
@@ -46,6 +48,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(REPO, "profiles", "traffic_c2.json"),
                     help="measured HBM traffic per launch (rocprofv3 --pmc summary)")
+    ap.add_argument("--probe", action="store_true",
+                    help="counter-collection run: one copy kernel of --probe-copy-mib MiB "
+                         "(the calibration), then --probe-steps eager steps; no timing")
+    ap.add_argument("--probe-copy-mib", type=int, default=256)
+    ap.add_argument("--probe-steps", type=int, default=32)
     return ap.parse_args()
 
 
@@ -118,6 +125,25 @@ def main():
             p.launch()
     torch.cuda.synchronize()
 
+    if args.probe:
+        # a plain device-to-device copy of known size calibrates the traffic
+        # counters; then eager steps, each reading a distinct input copy
+        n = args.probe_copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            for i in range(args.probe_steps):
+                preps[i % R].launch()
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": True, "copy_bytes": n, "steps": args.probe_steps,
+                          "launch": ctx.last_launch(),
+                          "algorithmic_bytes": W.algorithmic_bytes(cfg)}))
+        ctx.close()
+        return 0
+
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         for p in preps:
@@ -165,7 +191,13 @@ def main():
     tok0 = preps[0].tokens.cpu().numpy()
 
     alg_bytes = W.algorithmic_bytes(cfg)
-    achieved = alg_bytes / (dom_us * 1e-6) / 1e9
+    # The timed region is back-to-back launches of the step on one stream
+    # (HIP events on that stream bracket it); in fused mode a step is exactly
+    # one launch of the dominant kernel, so its average launch duration is the
+    # events' time per step.  (The eager hook's per-launch figure above also
+    # counts each launch's own event overhead.)
+    launch_us = 1e3 * ev_ms / steps if launch["fused"] else dom_us
+    achieved = alg_bytes / (launch_us * 1e-6) / 1e9
     traffic = None
     if args.traffic and os.path.exists(args.traffic):
         with open(args.traffic) as f:
@@ -192,7 +224,7 @@ def main():
         "step_effective_GBps": alg_bytes / (us_step * 1e-6) / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "algorithmic_bytes": alg_bytes, "kernel": dom_name},
+                     "algorithmic_bytes": alg_bytes, "kernel": dom_name, "launch_us": launch_us},
         "tokens_copy0_head": tok0[:4].tolist(),
     }
     if not args.no_cpu:
