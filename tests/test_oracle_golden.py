@@ -609,6 +609,29 @@ def test_typical_acceptance_uses_the_filtered_row():
         assert out["accept_mask"][0, 0] == want
 
 
+@pytest.mark.parametrize("pkw", [dict(temperature=0.8, top_p=0.9), dict(temperature=0.0),
+                                 dict(temperature=1.2, top_k=7, min_p=0.05)])
+def test_exact_verify_is_the_ordinary_draw_at_every_position(pkw):
+    # CBv2MTPTargetSamplingMatrixTests.swift:10-58: the verify window's target
+    # token at position j is the token an ordinary step would sample from that
+    # position's logits with the same uniform; accept iff it equals the draft
+    rng = np.random.default_rng(77)
+    S, Wn, V = 5, 4, 97
+    target = rng.normal(0, 2, (S, Wn, V)).astype(np.float32)
+    u = rng.random((S, Wn), dtype=np.float32)
+    params = W._params([W.resolve_cbv2(vocab=V, **pkw)] * S)
+    plain = O.sample(semantics=_ffi.SEM_CBV2, logits=target.reshape(S * Wn, V), dtype=F32,
+                     params=np.repeat(params, Wn), uniforms=u.reshape(-1))["tokens"].reshape(S, Wn)
+    drafts = plain[:, :-1].copy()
+    drafts[::2, 1] = (drafts[::2, 1] + 1) % V  # even sequences diverge at position 1
+    out = O.verify(mode=_ffi.VERIFY_EXACT, target=target, draft=None, draft_tokens=drafts,
+                   dtype=F32, params=params, uniforms=u)
+    assert np.array_equal(out["tokens"], plain)
+    assert np.array_equal(out["accept_mask"].astype(bool), drafts == plain[:, :-1])
+    want = np.argmin(np.concatenate([drafts == plain[:, :-1], np.zeros((S, 1), bool)], 1), 1)
+    assert np.array_equal(out["accepted"], want)
+
+
 # -------------------------------- speculative sampling: distribution invariant
 def test_residual_speculative_sampling_preserves_the_target_distribution():
     """Leviathan et al. 2023 / Chen et al. 2023: with drafts x ~ p_d, accept
