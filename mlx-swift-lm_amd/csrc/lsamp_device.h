@@ -406,6 +406,16 @@ __device__ __forceinline__ void st_coherent_f64(double* p, double v) {
 // Wait until every memory operation this wave issued has completed.
 __device__ __forceinline__ void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Work-group barrier for LDS traffic only: each wave waits for its own LDS
+// (and scalar) operations, not for its global loads, so loads in flight keep
+// streaming across it.  It orders nothing in global memory.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Arrival on a per-row counter; true in every thread of the last arriver.
 // `flag` is an LDS int.
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, int* flag) {

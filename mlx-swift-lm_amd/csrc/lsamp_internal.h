@@ -33,6 +33,14 @@ constexpr int kMassFracBits = 29;
 // Candidates (tokens in the cut bin) per row, and per work-group in LDS.
 constexpr int kCandCap = 4096;
 constexpr int kWgCandCap = 2048;
+// Short-list rows (argmax, or top-k <= kShortMaxK): each slice lists the
+// tokens at or above a threshold taken from its threads' maxima (at most
+// kShortCap in LDS) and publishes its own top-k plus ties (at most kShortPub,
+// which the row's candidate area holds for every slice).
+constexpr int kShortMaxK = 256;
+constexpr int kShortCap = 1024;
+constexpr int kShortPub = kCandCap / kMaxSlices;  // 512
+constexpr int kTauBins = 1024;                    // thread-maximum histogram
 // Kept tokens listed per slice (fast draw path); beyond this the draw scans.
 constexpr int kKeptCap = 256;
 // Penalty entries handled per slice (LDS).
@@ -43,6 +51,7 @@ constexpr float kWeightScale = 1099511627776.0f;
 // Cut position of a row (index into the row histogram, 0 = top bin).
 constexpr int32_t kCutTail = kBins;      // cut inside the tail bin
 constexpr int32_t kCutNone = kBins + 1;  // no filter cuts: every token kept
+constexpr int32_t kCutList = kBins + 2;  // short-list row: kept iff in the kept list
 
 // Row modes decided by the stats merge.
 constexpr int32_t kModeNormal = 0;
@@ -52,6 +61,9 @@ constexpr int32_t kModePosInf = 2;  // +inf logits present: keep exactly those
 // Slice flags.
 constexpr uint32_t kSlicePosInf = 0x100u;
 constexpr uint32_t kSliceEntryOverflow = 0x200u;
+constexpr uint32_t kSliceShortOverflow = 0x400u;  // short list did not fit
+// Slice flags that send a short-list row down the histogram path.
+constexpr uint32_t kSliceNoShort = kSlicePosInf | kSliceEntryOverflow | kSliceShortOverflow;
 
 // Per-slice summary written by the stats phase.
 struct SliceSummary {
@@ -60,7 +72,10 @@ struct SliceSummary {
   uint32_t flags;    // LSAMP_ROW_NONFINITE | kSlice*
   int32_t n_finite;  // histogram token count; without a histogram, 1 when the
                      // slice holds a finite (or +inf) transformed logit
-  double z;          // histogram mass relative to the floor of bin top_bin
+  double z;          // histogram mass relative to the top edge of bin top_bin
+  double zs;         // short-list rows: sum exp((x - x_max) / T_f) over the slice
+  int32_t npub;      // short-list rows: published keys (top-k plus ties)
+  int32_t pad;
   uint64_t hist[kHist];
 };
 
@@ -78,7 +93,7 @@ struct RowInfo {
   double z;             // sum exp(q - q_top) over every finite token
   double p_limit;       // top-p comparison bound (top_p * z), < 0 if off
   int32_t kept_cands;   // select finalize: kept candidates, listed first in cands[row]
-  int32_t pad;
+  int32_t done;         // split mode: the stats kernel already drew this row's token
 };
 
 // Per-slice partial results of the select phase.

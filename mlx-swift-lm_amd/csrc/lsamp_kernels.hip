@@ -50,6 +50,14 @@ __device__ __forceinline__ int fresh_tid() {
   return t;
 }
 
+// e^a for the rescale factors of the merges (a <= ~0.1): the hardware base-2
+// exponential, about 1e-7 relative.  The fused kernel evaluates no double-
+// precision exp / log (their constants would stay in registers for the
+// whole kernel).
+__device__ __forceinline__ double fexp(double a) {
+  return (double)__builtin_amdgcn_exp2f((float)(a * 1.4426950408889634));
+}
+
 // ------------------------------------------------------------ row context
 struct RowCtx {
   int32_t sem;
@@ -208,6 +216,9 @@ __device__ __forceinline__ ClassRule make_rule(const RowInfo& info, const RowCtx
   r.pinf_cls = c.kind == LSAMP_KIND_ARGMAX ? kCand : kKept;
   if (info.mode != kModeNormal) {
     r.kc = r.kd = -1;
+  } else if (info.cut == kCutList) {
+    r.kc = 0;  // every finite token is a candidate; the kept list decides
+    r.kd = 0x7fffffff;
   } else if (info.cut == kCutNone) {
     r.kc = r.kd = 0x7fffffff;
   } else if (info.cut == kCutTail) {
@@ -242,51 +253,100 @@ __device__ __forceinline__ int classify(const ClassRule& r, float x) {
 // Penalty bitmap of the slice + the slice's entries, patched.  Shared by both
 // kernels (they must classify identically).
 struct SliceEntries {
-  uint32_t* pen;   // [kSliceWords]
-  int32_t* tok;    // [kSliceEntryCap]
-  float* x;        // [kSliceEntryCap] transformed, -inf when masked / NaN
-  int32_t* count;  // LDS counter
+  uint32_t* pen;    // [kSliceWords]
+  uint32_t* qflag;  // [kThreads]: bit g set when quad g of that thread holds an entry
+  int32_t* tok;     // [kSliceEntryCap]
+  float* x;         // [kSliceEntryCap] transformed, -inf when masked / NaN
+  int32_t* count;   // LDS counter
 };
+
+// The row's first kEntPrefetch * kThreads penalty entries, one per thread and
+// pass, fetched before the slice's logits so that their loads return first
+// and the entry table is built while the slice is still streaming in.
+constexpr int kEntPrefetch = 2;
+struct EntryPrefetch {
+  int32_t e0, e1;
+  lsamp_penalty_entry ent[kEntPrefetch];
+};
+
+__device__ __forceinline__ void prefetch_entries(const SamplePlan& P, int row, int tid,
+                                                 EntryPrefetch& ep) {
+  ep.e0 = 0;
+  ep.e1 = 0;
+  if (P.row_ptr && P.entries) {
+    ep.e0 = P.row_ptr[row];
+    ep.e1 = P.row_ptr[row + 1];
+  }
+#pragma unroll
+  for (int k = 0; k < kEntPrefetch; ++k) {
+    const int32_t e = ep.e0 + tid + k * kThreads;
+    if (e < ep.e1) {
+      ep.ent[k] = P.entries[e];
+    } else {
+      ep.ent[k].token = -1;
+    }
+  }
+}
 
 template <int DT>
 __device__ __forceinline__ int build_slice_entries(const SamplePlan& P, const RowCtx& c,
                                                    const lsamp_row_params& prm, int row,
                                                    const char* rowp, int64_t base, int64_t end,
-                                                   SliceEntries& se, bool* overflow) {
-  const int tid = threadIdx.x;
-  for (int i = tid; i < kSliceWords; i += kThreads) se.pen[i] = 0u;
-  if (tid == 0) *se.count = 0;
-  __syncthreads();
-  int32_t e0 = 0, e1 = 0;
-  if (P.row_ptr && P.entries) {
-    e0 = P.row_ptr[row];
-    e1 = P.row_ptr[row + 1];
-  }
-  for (int32_t e = e0 + tid; e < e1; e += kThreads) {
-    const int32_t t = P.entries[e].token;
-    if (t >= base && t < end) {
-      const int32_t li = (int32_t)(t - base);
-      atomicOr(&se.pen[li >> 5], 1u << (li & 31));
-      const int idx = atomicAdd(se.count, 1);
-      if (idx < kSliceEntryCap) se.tok[idx] = e;
-    }
-  }
-  __syncthreads();
-  const int n_all = *se.count;
-  const int n = n_all < kSliceEntryCap ? n_all : kSliceEntryCap;
-  *overflow = n_all > kSliceEntryCap;
+                                                   SliceEntries& se, bool* overflow,
+                                                   const EntryPrefetch& ep, int tid) {
+  constexpr int N = Vec<DT>::N;
   const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
-  for (int j = tid; j < n; j += kThreads) {
-    const lsamp_penalty_entry ent = P.entries[se.tok[j]];
-    float x = load_scalar<DT>(rowp, ent.token);
+  for (int i = tid; i < kSliceWords; i += kThreads) se.pen[i] = 0u;
+  se.qflag[tid] = 0u;
+  if (tid == 0) *se.count = 0;
+  lds_barrier();
+  auto mark = [&](int32_t t) {
+    const int32_t li = t - (int32_t)base;
+    atomicOr(&se.pen[li >> 5], 1u << (li & 31));
+    const int32_t q = li / N;
+    atomicOr(&se.qflag[q % kThreads], 1u << (q / kThreads));
+    return atomicAdd(se.count, 1);
+  };
+  auto patched = [&](float x, const lsamp_penalty_entry& ent) {
     x = patch_value(c, prm, x, ent, DT);
     if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, ent.token)) x = kNegInf;
-    if (x != x) x = kNegInf;
-    se.x[j] = x;
-    se.tok[j] = ent.token;
+    return x != x ? kNegInf : x;
+  };
+  // the prefetched entries: their logits are gathered now and patched below
+  int slot[kEntPrefetch];
+  float xr[kEntPrefetch];
+#pragma unroll
+  for (int k = 0; k < kEntPrefetch; ++k) {
+    const int32_t t = ep.ent[k].token;
+    slot[k] = -1;
+    xr[k] = 0.0f;
+    if (t >= base && t < end) {
+      slot[k] = mark(t);
+      xr[k] = load_scalar<DT>(rowp, t);
+    }
   }
-  __syncthreads();
-  return n;
+  // the rest of a long history
+  for (int32_t e = ep.e0 + tid + kEntPrefetch * kThreads; e < ep.e1; e += kThreads) {
+    const lsamp_penalty_entry ent = P.entries[e];
+    if (ent.token >= base && ent.token < end) {
+      const int idx = mark(ent.token);
+      if (idx < kSliceEntryCap) {
+        se.x[idx] = patched(load_scalar<DT>(rowp, ent.token), ent);
+        se.tok[idx] = ent.token;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kEntPrefetch; ++k) {
+    if (slot[k] >= 0 && slot[k] < kSliceEntryCap) {
+      se.x[slot[k]] = patched(xr[k], ep.ent[k]);
+      se.tok[slot[k]] = ep.ent[k].token;
+    }
+  }
+  lds_barrier();
+  const int n_all = *se.count;
+  *overflow = n_all > kSliceEntryCap;
+  return n_all < kSliceEntryCap ? n_all : kSliceEntryCap;
 }
 
 // ----------------------------------------------------------------- LDS
@@ -314,9 +374,18 @@ union PhaseLds {
   SelectLds s;
   FinalLds f;
 };
+// Short-list slice phase: thread-maximum histogram and the slice's candidates.
+struct ShortLds {
+  uint32_t tcnt[kTauBins];
+  uint64_t ckey[kShortCap];  // raw candidates: value bits << 32 | token id
+};
 struct TaskLds {
   PhaseLds u;
+  ShortLds sh;
+  uint64_t ssrc[kCandCap];  // short-list finalize: the slices' published keys
+  int32_t soff[kMaxSlices + 1];
   uint32_t pen[kSliceWords];
+  uint32_t qflag[kThreads];
   int32_t etok[kSliceEntryCap];
   float ex[kSliceEntryCap];
   RowInfo info;
@@ -326,6 +395,7 @@ struct TaskLds {
   uint32_t hfl[kMaxSlices];
   int32_t hn[kMaxSlices];
   float redf[kWaves];
+  float redf2[kWaves];
   int32_t redi[kWaves];
   double redd[kWaves];
   uint64_t redu[kWaves];
@@ -370,6 +440,29 @@ __device__ __forceinline__ float token_value(const SamplePlan& P, const RowCtx& 
   }
   if (x != x) x = kNegInf;
   return x;
+}
+
+// Top-p bound on the mass ranked before a token, z the row's total mass (both
+// relative to the same e^q): CBv2 keeps exclusive mass <= top_p * z, a
+// non-positive top_p keeping the top token (LogitsPipelineV2.swift:199-206,
+// 440-445); mlx-lm keeps mass-before < top_p * z for 0 < top_p < 1
+// (Evaluate.swift:462-471).  Negative: top-p is off.
+__device__ __forceinline__ double top_p_limit(const SamplePlan& P, const RowCtx& c,
+                                              const lsamp_row_params& prm, double z) {
+  if (c.kind != LSAMP_KIND_FILTERED) return -1.0;
+  if (P.semantics == LSAMP_SEM_CBV2)
+    return prm.top_p < 1.0f ? (double)(prm.top_p > 0.0f ? prm.top_p : 0.0f) * z : -1.0;
+  return (prm.top_p > 0.0f && prm.top_p < 1.0f) ? (double)prm.top_p * z : -1.0;
+}
+
+// Rows drawn through the short list: argmax rows (k = 1) and filtered rows
+// whose top-k is active and at most kShortMaxK.  0: the histogram path.
+__device__ __forceinline__ int short_k(const RowCtx& c, const lsamp_row_params& prm, int64_t V) {
+  if (c.kind == LSAMP_KIND_ARGMAX) return 1;
+  if (c.kind == LSAMP_KIND_FILTERED && prm.top_k > 0 && (int64_t)prm.top_k < V &&
+      prm.top_k <= kShortMaxK)
+    return prm.top_k;
+  return 0;
 }
 
 // ============================================================ merge (stats)
@@ -439,7 +532,7 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
   info.z = 0.0;
   info.p_limit = -1.0;
   info.kept_cands = 0;
-  info.pad = 0;
+  info.done = 0;
   const float s_top = bin_pos(row_max, c.c32);
   // masses are relative to e^q_top, q_top the row's top in filter units
   info.q_top = (float)((double)s_top / (32.0 * c.tf));
@@ -455,23 +548,14 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
     const double inv_frac = 1.0 / (double)(1ull << kMassFracBits);
     // total mass relative to the row top: each slice's total is relative to
     // its own top bin
-    const double z = wave_sum((l < G && hn > 0) ? hz * exp((double)(htop + 1) * bin_t - q_ref)
+    const double z = wave_sum((l < G && hn > 0) ? hz * fexp((double)(htop + 1) * bin_t - q_ref)
                                                 : 0.0);
     info.z = z;
     const int32_t k_lim = (prm.top_k > 0 && (int64_t)prm.top_k < V) ? prm.top_k : 0;
-    bool p_on;
-    double P_lim;
-    bool strict;  // CBv2 keeps exclusive mass <= P; mlx-lm keeps mass-before < P
-    if (P.semantics == LSAMP_SEM_CBV2) {
-      p_on = prm.top_p < 1.0f;
-      P_lim = (double)(prm.top_p > 0.0f ? prm.top_p : 0.0f) * z;
-      strict = false;
-    } else {
-      p_on = prm.top_p > 0.0f && prm.top_p < 1.0f;
-      P_lim = (double)prm.top_p * z;
-      strict = true;
-    }
-    if (c.kind != LSAMP_KIND_FILTERED) p_on = false;
+    const double P_lim = top_p_limit(P, c, prm, z);
+    const bool p_on = P_lim >= 0.0;
+    // CBv2 keeps exclusive mass <= P; mlx-lm keeps mass-before < P
+    const bool strict = P.semantics != LSAMP_SEM_CBV2;
     const bool k_on = c.kind == LSAMP_KIND_FILTERED && k_lim > 0;
     const float mp = prm.min_p > 1.0f ? 1.0f : prm.min_p;
     const bool m_on = c.kind == LSAMP_KIND_FILTERED && mp > 0.0f;
@@ -482,7 +566,7 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
       if (j_t < 0) j_t = 0;
       if (j_t > kBins) j_t = kBins;
     }
-    info.p_limit = p_on ? P_lim : -1.0;
+    info.p_limit = P_lim;
 
     // batch 0: align the top 256 bins of every slice in LDS
 #pragma unroll
@@ -547,7 +631,7 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
         const int j = 64 * kBlk * b + 64 * k + l;
         const int32_t cj = (int32_t)cnt[k];
         const double mj = cj ? (double)msum[k] * inv_frac *
-                                   exp((double)(row_top - j + 1) * bin_t - q_ref)
+                                   fexp((double)(row_top - j + 1) * bin_t - q_ref)
                              : 0.0;
         const int32_t ic = wave_incl_scan(cj);
         const double im = wave_incl_scan(mj);
@@ -617,125 +701,39 @@ __device__ __forceinline__ uint64_t cand_key(float y, int32_t id) {
   return ((uint64_t)ordered_key(y == 0.0f ? 0.0f : y) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
 }
 
+// What the finalize tail needs besides the sorted candidates in F.keys.
+struct TailIn {
+  int nc;           // candidates in F.keys, sorted by cand_key descending
+  bool overflow;    // the row's keep set could not be resolved
+  double ent_all;   // kept tokens outside the candidates: entropy numerator,
+  float min_all;    //   smallest kept value,
+  int32_t kept_all; //   count
+  float u_draw;
+  int32_t probe;
+  int32_t n_list;   // lane s < G: kept tokens slice s listed (> kKeptCap: incomplete)
+  bool reset;       // clear the row's select counters (histogram path)
+  bool fused;
+  int32_t done;     // RowInfo.done of the written row decision
+};
+
+// Keep rule over the sorted candidates, the draw, the probe and the outputs
+// (wave 0 of the finalizing work-group).
 template <int DT>
-__device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
-                             const lsamp_row_params& prm, const RowInfo& info, TaskLds& L,
-                             const char* rowp, const uint32_t* mrow, bool fused) {
-  const int tid = fresh_tid();
-  const int l = tid & 63;
-  const bool wave0 = tid < 64;
-  const int G = P.slices;
+__device__ __forceinline__ void finalize_tail(const Workspace& ws, const SamplePlan& P, int row,
+                                              const RowCtx& c, const lsamp_row_params& prm,
+                                              const RowInfo& info, TaskLds& L, const char* rowp,
+                                              const uint32_t* mrow, const TailIn& t,
+                                              uint64_t (&rch)[kChunksPerLane]) {
+  const int l = fresh_tid() & 63;
   const int64_t V = P.vocab;
-  const int nch_row = P.nchunks;
   const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
   const bool active = info.mode != kModeEmpty;
-  uint64_t* rowchunks = ws.chunk_w + (size_t)row * (size_t)ws.max_chunks;
   Candidate* rc = ws.cands + (size_t)row * kCandCap;
   FinalLds& F = L.u.f;
-
-  // ---- wave 0 issues every independent load at once
-  SelectPartial part{};
-  uint64_t rch[kChunksPerLane];
-  uint64_t key0 = 0ull;
-  float u_draw = 0.0f;
-  int32_t probe = -1, total_cand = 0;
-  if (wave0) {
-    if (l < G) {
-      const SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + l;
-      part.ent = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&sp->ent)));
-      part.min_kept = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&sp->min_kept)));
-      part.n_kept = ld_coherent(&sp->n_kept);
-      part.n_cand = ld_coherent(&sp->n_cand);
-      part.n_list = ld_coherent(&sp->n_list);
-      part.overflow = ld_coherent(&sp->overflow);
-    }
-#pragma unroll
-    for (int i = 0; i < kChunksPerLane; ++i) {
-      const int ci = kChunksPerLane * l + i;
-      rch[i] = ci < nch_row ? ld_coherent(&rowchunks[ci]) : 0ull;
-    }
-    // candidate l, read before the count is known (slots past it are ignored)
-    const float cy = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[l].y)));
-    const int32_t cid = ld_coherent(&rc[l].id);
-    key0 = cand_key(cy, cid);
-    int32_t tc = 0;
-    float u = 0.0f;
-    int32_t pr = -1;
-    if (l == 0) {
-      tc = (int32_t)ld_coherent(&ws.cand_count[row]);
-      if (P.uniforms)
-        u = P.uniforms[uniform_index(P, row)];
-      else if (P.philox_keys)
-        u = philox_uniform(P.philox_keys[row], 0u);
-      const int pi = probe_index(P, row);
-      pr = (P.probe_tokens && pi >= 0) ? P.probe_tokens[pi] : -1;
-    }
-    total_cand = read_lane(tc, 0);
-    u_draw = read_lane(u, 0);
-    probe = read_lane(pr, 0);
-  }
-  // ---- row-wide partials (wave 0), shared through LDS with the other waves
-  double ent_all = 0.0;
-  float min_all = kPosInf;
-  int32_t kept_all = 0;
-  bool overflow = false;
-  int nc = 0;
-  if (wave0) {
-    const bool in = l < G;
-    ent_all = wave_sum(in ? part.ent : 0.0);
-    min_all = wave_min(in ? part.min_kept : kPosInf);
-    kept_all = wave_sum(in ? part.n_kept : 0);
-    const int32_t ov = wave_max(in && (part.n_cand > kWgCandCap || part.overflow) ? 1 : 0);
-    overflow = (info.flags & LSAMP_ROW_OVERFLOW) != 0 || ov != 0 || total_cand > kCandCap;
-    nc = (overflow || !active) ? 0 : total_cand;
-    if (l == 0) L.misc[1] = nc;
-  }
-  __syncthreads();
-  nc = L.misc[1];
-
-  // ---- sort candidates: value descending, id ascending (-0 == +0)
-  if (nc > 64) {
-    int n2 = 1;
-    while (n2 < nc) n2 <<= 1;
-    for (int i = tid; i < n2; i += kThreads) {
-      uint64_t key = 0ull;
-      if (i < nc) {
-        const float y = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[i].y)));
-        key = cand_key(y, ld_coherent(&rc[i].id));
-      }
-      F.keys[i] = key;
-    }
-    __syncthreads();
-    for (int kk = 2; kk <= n2; kk <<= 1) {
-      for (int jj = kk >> 1; jj > 0; jj >>= 1) {
-        for (int i = tid; i < n2; i += kThreads) {
-          const int ixj = i ^ jj;
-          if (ixj > i) {
-            const uint64_t a = F.keys[i], b = F.keys[ixj];
-            const bool desc = (i & kk) == 0;
-            if (desc ? (a < b) : (a > b)) {
-              F.keys[i] = b;
-              F.keys[ixj] = a;
-            }
-          }
-        }
-        __syncthreads();
-      }
-    }
-  }
-  if (!wave0) return;
-  if (nc > 0 && nc <= 64) {
-    // rank sort of the wave's own keys (keys are distinct: ids are)
-    const uint64_t key = l < nc ? key0 : 0ull;
-    F.dw[l] = key;
-    __builtin_amdgcn_wave_barrier();
-    int rank = 0;
-    for (int i = 0; i < nc; ++i) rank += F.dw[i] > key ? 1 : 0;
-    __builtin_amdgcn_wave_barrier();
-    if (l < nc) F.keys[rank] = key;
-    __builtin_amdgcn_wave_barrier();
-  }
-
+  const int nc = t.nc;
+  const bool overflow = t.overflow;
+  const float u_draw = t.u_draw;
+  const int32_t probe = t.probe;
   // ---- keep rule over the sorted candidates, 64 at a time
   const double P_lim = info.p_limit;
   const bool p_on = P_lim >= 0.0;
@@ -859,7 +857,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
     const int32_t ce = cb + kChunk < V ? cb + kChunk : (int32_t)V;
     const int cps = P.slice_len / kChunk;
     const int sc = cstar / cps;
-    const int32_t n_list = __shfl(part.n_list, sc, 64);
+    const int32_t n_list = __shfl(t.n_list, sc, 64);
 #pragma unroll
     for (int i = 0; i < kSlotsPerLane; ++i) F.dw[draw_slot(kSlotsPerLane * l + i)] = 0ull;
     __builtin_amdgcn_wave_barrier();
@@ -977,25 +975,496 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
       lsamp_row_stats st;
       st.max_value = y_max;
       st.log_normalizer =
-          info.z > 0.0 ? (float)(log(info.z) + ((double)info.q_top - (double)y_max)) : 0.0f;
-      st.kept = kept_all + kept_c;
+          info.z > 0.0 ? __builtin_logf((float)info.z) + (info.q_top - y_max) : 0.0f;
+      st.kept = t.kept_all + kept_c;
       st.token = tok;
       st.kept_weight = W;
       st.probe_weight = probe_w;
-      st.cut_value = __builtin_fminf(min_all, cmin);
+      st.cut_value = __builtin_fminf(t.min_all, cmin);
       const double zk = (double)W * (1.0 / 1099511627776.0);
       st.kept_mass = (float)zk;
-      st.kept_entropy = zk > 0.0 ? (float)(log(zk) - (ent_all + cent) / zk) : 0.0f;
+      st.kept_entropy = zk > 0.0 ? __builtin_logf((float)zk) - (float)((t.ent_all + cent) / zk) : 0.0f;
       st.probe_prob = W ? (float)((double)probe_w / (double)W) : 0.0f;
       P.stats[row] = st;
     }
     RowInfo out = info;
     out.kept_cands = overflow ? 0 : kept_c;
+    out.done = t.done;
     ws.rows[row] = out;
-    ws.cand_count[row] = 0u;
-    ws.arrive_select[row] = 0u;
-    if (fused) ws.arrive_stats[row] = 0u;
+    if (t.reset) {
+      ws.cand_count[row] = 0u;
+      ws.arrive_select[row] = 0u;
+      if (t.fused) ws.arrive_stats[row] = 0u;
+    }
   }
+}
+
+
+template <int DT>
+__device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
+                             const lsamp_row_params& prm, const RowInfo& info, TaskLds& L,
+                             const char* rowp, const uint32_t* mrow, bool fused) {
+  const int tid = fresh_tid();
+  const int l = tid & 63;
+  const bool wave0 = tid < 64;
+  const int G = P.slices;
+  const int64_t V = P.vocab;
+  const int nch_row = P.nchunks;
+  const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
+  const bool active = info.mode != kModeEmpty;
+  uint64_t* rowchunks = ws.chunk_w + (size_t)row * (size_t)ws.max_chunks;
+  Candidate* rc = ws.cands + (size_t)row * kCandCap;
+  FinalLds& F = L.u.f;
+
+  // ---- wave 0 issues every independent load at once
+  SelectPartial part{};
+  uint64_t rch[kChunksPerLane];
+  uint64_t key0 = 0ull;
+  float u_draw = 0.0f;
+  int32_t probe = -1, total_cand = 0;
+  if (wave0) {
+    if (l < G) {
+      const SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + l;
+      part.ent = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&sp->ent)));
+      part.min_kept = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&sp->min_kept)));
+      part.n_kept = ld_coherent(&sp->n_kept);
+      part.n_cand = ld_coherent(&sp->n_cand);
+      part.n_list = ld_coherent(&sp->n_list);
+      part.overflow = ld_coherent(&sp->overflow);
+    }
+#pragma unroll
+    for (int i = 0; i < kChunksPerLane; ++i) {
+      const int ci = kChunksPerLane * l + i;
+      rch[i] = ci < nch_row ? ld_coherent(&rowchunks[ci]) : 0ull;
+    }
+    // candidate l, read before the count is known (slots past it are ignored)
+    const float cy = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[l].y)));
+    const int32_t cid = ld_coherent(&rc[l].id);
+    key0 = cand_key(cy, cid);
+    int32_t tc = 0;
+    float u = 0.0f;
+    int32_t pr = -1;
+    if (l == 0) {
+      tc = (int32_t)ld_coherent(&ws.cand_count[row]);
+      if (P.uniforms)
+        u = P.uniforms[uniform_index(P, row)];
+      else if (P.philox_keys)
+        u = philox_uniform(P.philox_keys[row], 0u);
+      const int pi = probe_index(P, row);
+      pr = (P.probe_tokens && pi >= 0) ? P.probe_tokens[pi] : -1;
+    }
+    total_cand = read_lane(tc, 0);
+    u_draw = read_lane(u, 0);
+    probe = read_lane(pr, 0);
+  }
+  // ---- row-wide partials (wave 0), shared through LDS with the other waves
+  double ent_all = 0.0;
+  float min_all = kPosInf;
+  int32_t kept_all = 0;
+  bool overflow = false;
+  int nc = 0;
+  if (wave0) {
+    const bool in = l < G;
+    ent_all = wave_sum(in ? part.ent : 0.0);
+    min_all = wave_min(in ? part.min_kept : kPosInf);
+    kept_all = wave_sum(in ? part.n_kept : 0);
+    const int32_t ov = wave_max(in && (part.n_cand > kWgCandCap || part.overflow) ? 1 : 0);
+    overflow = (info.flags & LSAMP_ROW_OVERFLOW) != 0 || ov != 0 || total_cand > kCandCap;
+    nc = (overflow || !active) ? 0 : total_cand;
+    if (l == 0) L.misc[1] = nc;
+  }
+  __syncthreads();
+  nc = L.misc[1];
+
+  // ---- sort candidates: value descending, id ascending (-0 == +0)
+  if (nc > 64) {
+    int n2 = 1;
+    while (n2 < nc) n2 <<= 1;
+    for (int i = tid; i < n2; i += kThreads) {
+      uint64_t key = 0ull;
+      if (i < nc) {
+        const float y = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[i].y)));
+        key = cand_key(y, ld_coherent(&rc[i].id));
+      }
+      F.keys[i] = key;
+    }
+    __syncthreads();
+    for (int kk = 2; kk <= n2; kk <<= 1) {
+      for (int jj = kk >> 1; jj > 0; jj >>= 1) {
+        for (int i = tid; i < n2; i += kThreads) {
+          const int ixj = i ^ jj;
+          if (ixj > i) {
+            const uint64_t a = F.keys[i], b = F.keys[ixj];
+            const bool desc = (i & kk) == 0;
+            if (desc ? (a < b) : (a > b)) {
+              F.keys[i] = b;
+              F.keys[ixj] = a;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+  }
+  if (!wave0) return;
+  if (nc > 0 && nc <= 64) {
+    // rank sort of the wave's own keys (keys are distinct: ids are)
+    const uint64_t key = l < nc ? key0 : 0ull;
+    F.dw[l] = key;
+    __builtin_amdgcn_wave_barrier();
+    int rank = 0;
+    for (int i = 0; i < nc; ++i) rank += F.dw[i] > key ? 1 : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (l < nc) F.keys[rank] = key;
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  TailIn t;
+  t.nc = nc;
+  t.overflow = overflow;
+  t.ent_all = ent_all;
+  t.min_all = min_all;
+  t.kept_all = kept_all;
+  t.u_draw = u_draw;
+  t.probe = probe;
+  t.n_list = part.n_list;
+  t.reset = true;
+  t.fused = fused;
+  t.done = 0;
+  finalize_tail<DT>(ws, P, row, c, prm, info, L, rowp, mrow, t, rch);
+}
+
+// A short-list row's slice leaves through a second counter; the last one out
+// clears both counters for the next step (fused mode).
+__device__ __forceinline__ void short_depart(const Workspace& ws, int row, int G) {
+  const uint32_t out = __hip_atomic_fetch_add(&ws.arrive_select[row], 1u, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+  if (out + 1u == (uint32_t)G) {
+    st_coherent(&ws.arrive_stats[row], 0u);
+    st_coherent(&ws.arrive_select[row], 0u);
+  }
+}
+
+// Single-wave tail of a short-list row with at most 64 candidates (lane r
+// holds F.keys[r]): the keep rule of finalize_tail with nothing kept above
+// the candidates, the same integer inverse-CDF draw in token-id order, the
+// probe and the outputs.
+template <int DT>
+__device__ __forceinline__ void short_tail(const Workspace& ws, const SamplePlan& P, int row,
+                                           const RowCtx& c, const lsamp_row_params& prm,
+                                           const RowInfo& info, TaskLds& L, int nc, float u_draw,
+                                           int32_t probe) {
+  const int l = fresh_tid() & 63;
+  const int64_t V = P.vocab;
+  FinalLds& F = L.u.f;
+  const float y_max = to_filter(c, info.x_max);
+  const bool in = l < nc;
+  const uint64_t key = in ? F.keys[l] : 0ull;
+  const float y = key_y(key);
+  const int32_t id = key_id(key);
+  const double P_lim = info.p_limit;
+  const bool p_on = P_lim >= 0.0;
+  const int32_t k_lim = (c.kind == LSAMP_KIND_FILTERED && prm.top_k > 0 && (int64_t)prm.top_k < V)
+                            ? prm.top_k
+                            : (c.kind == LSAMP_KIND_ARGMAX ? 1 : 0);
+  const float mp = prm.min_p > 1.0f ? 1.0f : prm.min_p;
+  const bool m_on = c.kind == LSAMP_KIND_FILTERED && mp > 0.0f;
+  const float ln_mp = m_on ? __builtin_logf(mp) : 0.0f;
+  const bool mlx = P.semantics == LSAMP_SEM_MLXLM;
+  const double e = in ? (double)__builtin_expf(y - info.q_top) : 0.0;
+  const double e_excl = wave_incl_scan(e) - e;
+  bool keep_p = true, keep_m = true;
+  if (mlx) {
+    if (in) {
+      // tie group [g0, g1) of equal values; the reference's ascending stable
+      // argsort ranks higher ids of a tie first (Evaluate.swift:463-469)
+      const uint32_t kr = (uint32_t)(key >> 32);
+      int g0 = l, g1 = l + 1;
+      while (g0 > 0 && (uint32_t)(F.keys[g0 - 1] >> 32) == kr) --g0;
+      while (g1 < nc && (uint32_t)(F.keys[g1] >> 32) == kr) ++g1;
+      const double sp = e_excl - (double)(l - g0) * e + (double)(g1 - 1 - l) * e;
+      if (p_on) keep_p = sp < P_lim;
+      if (m_on) keep_m = (y - y_max) >= ln_mp;
+    }
+  } else {
+    if (p_on) keep_p = e_excl <= P_lim;
+    if (m_on) keep_m = __builtin_expf(y - y_max) >= mp;
+    if (k_lim > 0 && l >= k_lim) keep_p = false;
+  }
+  const int32_t surv = (in && keep_p && keep_m) ? 1 : 0;
+  const int32_t is = wave_incl_scan(surv);
+  bool keep = surv != 0;
+  if (keep && mlx && k_lim > 0) keep = (is - 1) < k_lim;
+  const int32_t ik = wave_incl_scan(keep ? 1 : 0);
+  const int32_t kept_c = read_lane(ik, 63);
+  const uint64_t w = keep ? weight(y, y_max, c.scale) : 0ull;
+  const uint64_t W = wave_sum(w);
+  // the kept tokens in id order (each kept lane counts the kept ids below
+  // its own), then a running sum: the token is the one whose run crosses the
+  // target
+  int32_t* sid = reinterpret_cast<int32_t*>(F.cx);
+  int32_t* sid2 = sid + 64;
+  if (keep) sid[ik - 1] = id;  // kept ids, compacted
+  if (l >= kept_c) sid[l] = 0x7fffffff;
+  __builtin_amdgcn_wave_barrier();
+  int pos = 0;
+  for (int j0 = 0; j0 < kept_c; j0 += 16) {
+    int32_t ij[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) ij[q] = sid[j0 + q];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) pos += ij[q] < id ? 1 : 0;
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (keep) {
+    F.dw[pos] = w;
+    sid2[pos] = id;
+  }
+  __builtin_amdgcn_wave_barrier();
+  const uint64_t wo = l < kept_c ? F.dw[l] : 0ull;
+  const int32_t io = l < kept_c ? sid2[l] : -1;
+  const uint64_t cum = wave_incl_scan(wo);
+  const uint64_t target = W ? scaled_target(uniform_u32(u_draw), W) : 0ull;
+  const uint64_t hm = __ballot(wo != 0ull && cum > target && cum - wo <= target);
+  const int32_t token = hm ? read_lane(io, __builtin_ctzll(hm)) : -1;
+  const uint64_t hp = __ballot(keep && probe >= 0 && id == probe);
+  const uint64_t probe_w = hp ? read_lane(w, __builtin_ctzll(hp)) : 0ull;
+  const double cent =
+      wave_sum(keep ? (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale) : 0.0);
+  const float cmin = wave_min(keep ? y : kPosInf);
+  // kept candidates persist, in key order, for the MTP residual pass
+  Candidate* rc = ws.cands + (size_t)row * kCandCap;
+  if (keep) {
+    rc[ik - 1].y = y;
+    rc[ik - 1].id = id;
+  }
+  if (in && P.keep) P.keep[(size_t)row * (size_t)V + id] = keep ? 1 : 0;
+  if (l == 0) {
+    uint32_t flags = info.flags;
+    if (token < 0 || W == 0ull) flags |= LSAMP_ROW_EMPTY;
+    P.tokens[row] = token;
+    if (P.row_flags) P.row_flags[row] = flags;
+    if (P.stats) {
+      lsamp_row_stats st;
+      st.max_value = y_max;
+      st.log_normalizer = info.z > 0.0 ? __builtin_logf((float)info.z) : 0.0f;
+      st.kept = kept_c;
+      st.token = token;
+      st.kept_weight = W;
+      st.probe_weight = probe_w;
+      st.cut_value = cmin;
+      const double zk = (double)W * (1.0 / 1099511627776.0);
+      st.kept_mass = (float)zk;
+      st.kept_entropy = zk > 0.0 ? __builtin_logf((float)zk) - (float)(cent / zk) : 0.0f;
+      st.probe_prob = W ? (float)((double)probe_w / (double)W) : 0.0f;
+      P.stats[row] = st;
+    }
+    RowInfo out = info;
+    out.kept_cands = kept_c;
+    out.done = 1;
+    ws.rows[row] = out;
+  }
+}
+
+// Short-list finalize (the last work-group of a short-list row to publish).
+// Every slice published the tokens at or above its own k-th largest filter-
+// space value, sorted by cand_key descending; every token of the row's top-k
+// (and every token tied with the k-th) is among them.  The lists are merged
+// by rank into F.keys, cut after the row's top-k plus ties, and drawn from.
+// The row's total mass comes from the slices' sums.  Returns false, having
+// changed nothing, when a slice asks for the histogram path instead.
+template <int DT>
+__device__ __forceinline__ bool short_gather(const Workspace& ws, const SamplePlan& P, int row,
+                                             const RowCtx& c, const lsamp_row_params& prm,
+                                             TaskLds& L) {
+  const int tid = fresh_tid();
+  const int l = tid & 63;
+  const bool wave0 = tid < 64;
+  const int G = P.slices;
+  const SliceSummary* summ = ws.summaries + (size_t)row * kMaxSlices;
+  const uint64_t* pub = reinterpret_cast<const uint64_t*>(ws.cands + (size_t)row * kCandCap);
+  // one round trip: thread t fetches key t % 64 of slice t / 64 (lists are
+  // short), wave 0 also the slices' headers, the row's uniform and probe
+  const int ks = tid >> 6, kj = tid & 63;
+  const uint64_t kspec = ks < G ? ld_coherent(pub + (size_t)ks * kShortPub + kj) : 0ull;
+  if (wave0) {
+    float hx = kNegInf;
+    int32_t hn = 0, hp = 0;
+    uint32_t hf = 0u;
+    double hz = 0.0;
+    if (l < G) {
+      hx = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&summ[l].x_max)));
+      hn = ld_coherent(&summ[l].n_finite);
+      hp = ld_coherent(&summ[l].npub);
+      hf = ld_coherent(&summ[l].flags);
+      hz = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&summ[l].zs)));
+    }
+    float u = 0.0f;
+    int32_t pr = -1;
+    if (l == 0) {
+      if (P.uniforms)
+        u = P.uniforms[uniform_index(P, row)];
+      else if (P.philox_keys)
+        u = philox_uniform(P.philox_keys[row], 0u);
+      const int pi = probe_index(P, row);
+      pr = (P.probe_tokens && pi >= 0) ? P.probe_tokens[pi] : -1;
+    }
+    const bool fallback = __ballot(l < G && (hf & kSliceNoShort) != 0u) != 0ull;
+    const bool live = l < G && hn > 0;
+    const bool any = __ballot(live) != 0ull;
+    const float row_max = wave_max(live ? hx : kNegInf);
+    const bool nonfinite = __ballot(l < G && (hf & LSAMP_ROW_NONFINITE) != 0u) != 0ull;
+    const int32_t hpv = live ? hp : 0;
+    const int32_t ip = wave_incl_scan(hpv);
+    const int32_t npmax = wave_max(hpv);
+    if (l < G) L.soff[l] = ip - hpv;
+    if (l == G - 1) L.soff[G] = ip;
+    const float y_max = any ? to_filter(c, row_max) : 0.0f;
+    // slice s summed exp((x - x_s) / T_f); rescaled to e^y_max
+    double z = 0.0;
+    if (any && c.kind != LSAMP_KIND_ARGMAX)
+      z = wave_sum(live ? hz * (double)__builtin_expf((hx - row_max) / (float)c.tf) : 0.0);
+    RowInfo info;
+    info.x_max = row_max;
+    info.q_top = y_max;
+    info.top_bin = any ? bin_of(row_max, c.c32) : 0;
+    info.cut = kCutList;
+    info.mode = any ? kModeNormal : kModeEmpty;
+    info.flags = nonfinite ? LSAMP_ROW_NONFINITE : 0u;
+    info.count_above = 0;
+    info.n_finite = any ? 1 : 0;
+    info.mass_above = 0.0;
+    info.z = z;
+    info.p_limit = top_p_limit(P, c, prm, z);
+    info.kept_cands = 0;
+    info.done = 1;
+    if (l == 0) {
+      L.info = info;
+      L.misc[5] = fallback ? 1 : 0;
+      L.misc[7] = npmax;
+      L.misc64[0] = __float_as_uint(u);
+      L.misc[4] = pr;
+    }
+  }
+  __syncthreads();
+  if (L.misc[5]) return false;
+  if (ks < G && kj < L.soff[ks + 1] - L.soff[ks]) L.ssrc[L.soff[ks] + kj] = kspec;
+  return true;
+}
+
+// The rest of a short-list row's finalize, once short_gather has accepted it:
+// the keys past the 64th of a slice, the merge by rank, the cut after the
+// row's top-k plus ties, and the tail.
+template <int DT>
+__device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePlan& P, int row,
+                                             const RowCtx& c, const lsamp_row_params& prm,
+                                             TaskLds& L, const char* rowp, const uint32_t* mrow,
+                                             int K) {
+  const int tid = fresh_tid();
+  const bool wave0 = tid < 64;
+  const int G = P.slices;
+  const int64_t V = P.vocab;
+  FinalLds& F = L.u.f;
+  const uint64_t* pub = reinterpret_cast<const uint64_t*>(ws.cands + (size_t)row * kCandCap);
+  if (P.fused && tid == 64) short_depart(ws, row, G);  // overlaps the rest
+  const int n_tot = L.soff[G];
+  const int npmax = L.misc[7];
+  if (npmax > 64) {
+    // keys past the 64th of a slice: a second round trip
+    for (int s2 = 0; s2 < G; ++s2) {
+      const int np = L.soff[s2 + 1] - L.soff[s2];
+      for (int j = 64 + tid; j < np; j += kThreads)
+        L.ssrc[L.soff[s2] + j] = ld_coherent(pub + (size_t)s2 * kShortPub + j);
+    }
+  }
+  if (P.keep) {
+    // the tail writes the bytes of the listed tokens; every other token of
+    // the row is dropped
+    uint8_t* kr = P.keep + (size_t)row * (size_t)V;
+    for (int64_t i = tid; i < V; i += kThreads) kr[i] = 0;
+  }
+  __syncthreads();
+  // rank of each key in the union (keys are distinct: token ids are): the
+  // keys above it.  The comparisons of a key are split over `parts` threads
+  // (the whole work-group works), each reading its share of the keys 16 at a
+  // time, and the partial counts meet in LDS.
+  int32_t* racc = reinterpret_cast<int32_t*>(F.dw);  // [n_tot] partial ranks (n_tot <= kCandCap)
+  int32_t* rk = racc;
+  const int parts = n_tot > 0 && n_tot <= kThreads / 2 ? kThreads / n_tot : 1;
+  if (parts > 1) {
+    for (int i = tid; i < n_tot; i += kThreads) racc[i] = 0;
+    if (tid == 0) L.misc[6] = n_tot;
+    __syncthreads();
+    const int i = tid % n_tot, part = tid / n_tot;
+    if (part < parts) {
+      const uint64_t key = L.ssrc[i];
+      const int j0 = (n_tot * part) / parts, j1 = (n_tot * (part + 1)) / parts;
+      int r = 0;
+      int j = j0;
+      for (; j + 16 <= j1; j += 16) {
+        uint64_t kk[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) kk[q] = L.ssrc[j + q];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) r += kk[q] > key ? 1 : 0;
+      }
+      for (; j < j1; ++j) r += L.ssrc[j] > key ? 1 : 0;
+      atomicAdd(&racc[i], r);
+    }
+    __syncthreads();
+    for (int i2 = tid; i2 < n_tot; i2 += kThreads) F.keys[rk[i2]] = L.ssrc[i2];
+  } else {
+    if (tid == 0) L.misc[6] = n_tot;
+    for (int i = tid; i < n_tot; i += kThreads) {
+      const uint64_t key = L.ssrc[i];
+      int r = 0;
+      int j = 0;
+      for (; j + 16 <= n_tot; j += 16) {
+        uint64_t kk[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) kk[q] = L.ssrc[j + q];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) r += kk[q] > key ? 1 : 0;
+      }
+      for (; j < n_tot; ++j) r += L.ssrc[j] > key ? 1 : 0;
+      F.keys[r] = key;
+    }
+  }
+  __syncthreads();
+  // the row's top-k and every token tied with the k-th: the first position
+  // past K - 1 whose value is below the k-th's
+  if (n_tot > K) {
+    const uint32_t kv = (uint32_t)(F.keys[K - 1] >> 32);
+    for (int i = K + tid; i < n_tot; i += kThreads)
+      if ((uint32_t)(F.keys[i] >> 32) < kv && (uint32_t)(F.keys[i - 1] >> 32) >= kv) L.misc[6] = i;
+  }
+  __syncthreads();
+  if (!wave0) return;
+  int nc = L.misc[6];
+  const RowInfo info = L.info;
+  if (info.mode != kModeNormal) nc = 0;
+  const float u_draw = __uint_as_float((uint32_t)L.misc64[0]);
+  const int32_t probe = L.misc[4];
+  if (nc <= 64) {
+    short_tail<DT>(ws, P, row, c, prm, info, L, nc, u_draw, probe);
+    return;
+  }
+  TailIn t;
+  t.nc = nc;
+  t.overflow = false;
+  t.ent_all = 0.0;
+  t.min_all = kPosInf;
+  t.kept_all = 0;
+  t.u_draw = u_draw;
+  t.probe = probe;
+  t.n_list = 0;
+  t.reset = false;
+  t.fused = P.fused != 0;
+  t.done = 1;
+  uint64_t rch[kChunksPerLane];
+#pragma unroll
+  for (int i = 0; i < kChunksPerLane; ++i) rch[i] = 0ull;
+  finalize_tail<DT>(ws, P, row, c, prm, info, L, rowp, mrow, t, rch);
 }
 
 // ================================================================ one task
@@ -1042,6 +1511,20 @@ __device__ __forceinline__ void for_quads(Slab<DT>& S, int nq, F&& f) {
   }
 }
 
+// for_quads with every quad at a static register position: fully unrolled
+// (larger code, but no register-relative moves, which cost about a third of
+// a pass); used by the passes over every token.
+template <int DT, typename F>
+__device__ __forceinline__ void for_quads_static(Slab<DT>& S, int nq, F&& f) {
+#pragma unroll
+  for (int g = 0; g < Slab<DT>::Q; ++g) {
+    if (g < nq) {
+      uint4 v = quad_get(S.bank[g / kQuadsPerBank], g % kQuadsPerBank);
+      if (f(g, v)) quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, v);
+    }
+  }
+}
+
 // Accumulates a probe of the quad's exponent fields: bit 15 / 31 (16-bit
 // types) or bit 31 (fp32) of the result is set when some element is inf/NaN.
 template <int DT>
@@ -1057,9 +1540,24 @@ __device__ __forceinline__ bool nonfinite_seen(uint32_t acc) {
   return (acc & (DT == LSAMP_DTYPE_F32 ? 0x80000000u : 0x80008000u)) != 0u;
 }
 
+// Does any slice of a short-list row need the histogram path (+inf logits,
+// an entry-table or short-list overflow)?  Called by the whole work-group.
+__device__ __forceinline__ bool short_fallback(const Workspace& ws, int row, int G, TaskLds& L) {
+  const int tid = fresh_tid();
+  if (tid < 64) {
+    const uint32_t f = tid < G ? ld_coherent(&ws.summaries[(size_t)row * kMaxSlices + tid].flags) : 0u;
+    const bool fb = __ballot((f & kSliceNoShort) != 0u) != 0ull;
+    if (tid == 0) L.misc[5] = fb ? 1 : 0;
+  }
+  __syncthreads();
+  return L.misc[5] != 0;
+}
+
 template <int DT, int MODE>
 __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& P, int row, int slice,
                                          TaskLds& L) {
+  // split mode: rows the stats kernel already drew (short lists) are done
+  if (MODE == kSelectOnly && ws.rows[row].done) return;
   constexpr int N = Vec<DT>::N;
   constexpr int Q = Slab<DT>::Q;
   constexpr uint32_t FULL = (1u << N) - 1u;
@@ -1079,6 +1577,8 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   const int nq = (P.slice_len + kThreads * N - 1) / (kThreads * N);  // quads per thread
 
   // ---------------------------------------------------- A: loads + entries
+  EntryPrefetch ep;
+  prefetch_entries(P, row, tid, ep);
   // Aligned whole quads are read as 16-byte vectors, all in flight at once;
   // lanes past the slice end read as zero until the exclusion pass.
   // (uniform base address per quad + the lane's 32-bit byte offset)
@@ -1111,32 +1611,50 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       return true;
     });
   }
-  if (MODE != kSelectOnly)
+  if (MODE != kSelectOnly) {
     for (int i = tid; i < kHist; i += kThreads) L.u.hist[i] = 0ull;
-  if (tid == 0) L.flags = 0u;
-  SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
+    for (int i = tid; i < kTauBins; i += kThreads) L.sh.tcnt[i] = 0u;
+  }
+  if (tid == 0) {
+    L.flags = 0u;
+    L.ncand = 0;
+  }
+  SliceEntries se{L.pen, L.qflag, L.etok, L.ex, &L.ecount};
   bool ent_overflow = false;
-  const int n_ent = build_slice_entries<DT>(P, c, prm, row, rowp, base, end, se, &ent_overflow);
+  const int n_ent = build_slice_entries<DT>(P, c, prm, row, rowp, base, end, se, &ent_overflow, ep, tid);
 
   // Masked tokens, tokens of the entry table (their patched values live in
   // L.ex) and lanes past the slice end become -inf in the register copy, and
   // so do NaNs.  From here on "excluded" is simply "not > -inf".  The same
-  // pass takes the thread's maximum.
+  // pass takes the thread's maximum and, for short-list rows, the thread's
+  // sum of exp((x - m) / T_f): each term is exp2(x * lgz + nbz) with nbz an
+  // integer anchored at a quad maximum (re-anchored by an exact power of two
+  // only if the running maximum climbs 64 binary orders above it), so the
+  // largest terms are computed at full precision.
+  const int K = MODE != kSelectOnly ? short_k(c, prm, V) : 0;
+  const bool zon = K > 0 && c.kind != LSAMP_KIND_ARGMAX;
+  const float lgz = (float)(1.4426950408889634 / c.tf);  // log2(e) / T_f
+  // penalty-bitmap word of quad g, read only for quads holding an entry;
+  // fetched one quad ahead so the LDS read overlaps the current quad
+  const uint32_t qf = L.qflag[tid];
+  auto pen_word = [&](int g) -> uint32_t {
+    return ((qf >> g) & 1u) ? L.pen[((tid + g * kThreads) * N) >> 5] : 0u;
+  };
+  const uint32_t pen_shift = (uint32_t)((tid * N) & 31);
+  uint32_t pw = nq > 0 ? pen_word(0) : 0u;
   uint32_t nf_acc = 0u;
   float xmax = kNegInf;
-  for_quads(S, nq, [&](int g, uint4& v) -> bool {
+  float zt = 0.0f, nbz = 0.0f;
+  bool zref = false;
+  for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
     const int32_t i0 = base32 + (tid + g * kThreads) * N;
+    const uint32_t pcur = pw;
+    pw = g + 1 < nq ? pen_word(g + 1) : 0u;
     const uint32_t probe = nonfinite_probe<DT>(v);
     nf_acc |= probe;
-    uint32_t ex = FULL;
-    if (i0 < end32) {
-      const int32_t nvalid = end32 - i0;
-      const uint32_t valid = nvalid >= N ? FULL : ((1u << nvalid) - 1u);
-      const uint32_t allow = mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N);
-      const int32_t li0 = i0 - base32;
-      const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
-      ex = (~allow | pen | ~valid) & FULL;
-    }
+    uint32_t ex = (pcur >> pen_shift) & FULL;
+    if (i0 + N > end32) ex |= i0 >= end32 ? FULL : (FULL & ~((1u << (end32 - i0)) - 1u));
+    if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
     if (nonfinite_seen<DT>(probe)) {
 #pragma unroll
       for (int e = 0; e < N; ++e) {
@@ -1146,8 +1664,22 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     }
     if (ex != 0u) exclude_elems<DT>(v, ex);
     if (MODE != kSelectOnly) {
+      float qm = vec_elem<DT>(v, 0);
 #pragma unroll
-      for (int e = 0; e < N; ++e) xmax = __builtin_fmaxf(xmax, vec_elem<DT>(v, e));
+      for (int e = 1; e < N; ++e) qm = __builtin_fmaxf(qm, vec_elem<DT>(v, e));
+      xmax = __builtin_fmaxf(xmax, qm);
+      if (zon) {
+        const float ql = qm * lgz;
+        if (ql > -0x1p20f && ql < 0x1p20f && (!zref || __builtin_fmaf(qm, lgz, nbz) > 64.0f)) {
+          const float nn = -__builtin_ceilf(ql);
+          zt = zref ? __builtin_ldexpf(zt, (int)(nn - nbz)) : 0.0f;
+          nbz = nn;
+          zref = true;
+        }
+#pragma unroll
+        for (int e = 0; e < N; ++e)
+          zt += __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(v, e), lgz, nbz));
+      }
     }
     return ex != 0u;
   });
@@ -1155,15 +1687,244 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
 
   RowInfo info;
   if (MODE != kSelectOnly) {
-    // ------------------------------------------------ B: max, histogram
+    // ------------------------------------------------ B: max
     for (int j = tid; j < n_ent; j += kThreads) xmax = __builtin_fmaxf(xmax, L.ex[j]);
     if (nonfinite) atomicOr(&L.flags, LSAMP_ROW_NONFINITE);
-    xmax = block_max(xmax, L.redf);
+    const float tmax = xmax;  // this thread's largest (transformed) logit
+    float tlo = kPosInf;      // smallest finite thread maximum (short lists, k > 1)
+    if (K > 1) {
+      float hi = wave_max(tmax);
+      float lo = wave_min(tmax > kNegInf ? tmax : kPosInf);
+      const int wv = tid >> 6;
+      __syncthreads();
+      if ((tid & 63) == 0) {
+        L.redf[wv] = hi;
+        L.redf2[wv] = lo;
+      }
+      __syncthreads();
+      hi = L.redf[0];
+      lo = L.redf2[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; ++i) {
+        hi = __builtin_fmaxf(hi, L.redf[i]);
+        lo = __builtin_fminf(lo, L.redf2[i]);
+      }
+      __syncthreads();
+      xmax = hi;
+      tlo = lo;
+    } else {
+      xmax = block_max(xmax, L.redf);
+    }
     const bool posinf = xmax == kPosInf;
     const bool has_finite = xmax > kNegInf && !posinf;
-    const uint32_t sflags = L.flags | (ent_overflow ? kSliceEntryOverflow : 0u) |
-                            (posinf ? kSlicePosInf : 0u);
+    uint32_t sflags = L.flags | (ent_overflow ? kSliceEntryOverflow : 0u) |
+                      (posinf ? kSlicePosInf : 0u);
     const int32_t top = has_finite ? bin_of(xmax, c.c32) : 0;
+    SliceSummary* Ssum = ws.summaries + ((size_t)row * kMaxSlices + slice);
+    if (P.processed) {
+      float* out = P.processed + (size_t)row * (size_t)V;
+      for_quads(S, nq, [&](int g, uint4& v) -> bool {
+        const int32_t i0 = base32 + (tid + g * kThreads) * N;
+        if (i0 >= end32) return false;
+        const int32_t li0 = i0 - base32;
+        const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          if (i0 + e >= end32 || ((pen >> e) & 1u)) continue;
+          out[i0 + e] = to_filter(c, vec_elem<DT>(v, e));
+        }
+        return false;
+      });
+      for (int j = tid; j < n_ent; j += kThreads) out[L.etok[j]] = to_filter(c, L.ex[j]);
+    }
+
+    if (K > 0) {
+      // -------------------------------------------- B': the short list
+      // A threshold no higher than the k-th largest thread maximum leaves at
+      // least k tokens at or above it; those few are sorted, and the slice's
+      // top-k plus ties is published.
+      int32_t npub = 0;
+      double zsum = 0.0;
+      if (has_finite && !ent_overflow) {
+        float tau = xmax;  // k = 1: the maximum itself
+        if (K > 1) {
+          // thread maxima binned below the slice maximum over a range of at
+          // most 32 filter-space nats; the bin where the count reaches k
+          // bounds the k-th largest from below (half a bin of slack covers
+          // the rounding of the bin index)
+          const float D = __builtin_fminf(xmax - tlo, (float)(32.0 * c.tf));
+          const float sc = D > 0.0f ? (float)(kTauBins - 1) / D : 0.0f;
+          if (tmax > kNegInf) {
+            const float fb = (xmax - tmax) * sc;
+            const int b = fb < (float)(kTauBins - 1) ? (int)fb : kTauBins - 1;
+            atomicAdd(&L.sh.tcnt[b], 1u);
+          }
+          __syncthreads();
+          if (tid < 64) {
+            constexpr int kPer = kTauBins / 64;
+            uint32_t cb[kPer];
+            uint32_t cs = 0u;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) {
+              cb[i] = L.sh.tcnt[kPer * tid + i];
+              cs += cb[i];
+            }
+            const uint32_t ic = wave_incl_scan(cs);
+            const uint64_t hit = __ballot(ic >= (uint32_t)K);
+            int bs = kTauBins;  // fewer than k threads hold a finite logit
+            if (hit) {
+              // first bin of each lane's run where the running count reaches
+              // k; lane f's is the answer
+              uint32_t acc = ic - cs;
+              int pos = kPer - 1;
+              bool found = false;
+#pragma unroll
+              for (int i = 0; i < kPer; ++i) {
+                acc += cb[i];
+                const bool h = !found && acc >= (uint32_t)K;
+                pos = h ? i : pos;
+                found = found || h;
+              }
+              const int f = __builtin_ctzll(hit);
+              bs = kPer * f + read_lane(pos, f);
+            }
+            if (tid == 0) L.misc[6] = bs;
+          }
+          __syncthreads();
+          const int bs = L.misc[6];
+          // no bin reaches k: every finite token is a candidate
+          tau = bs >= kTauBins ? kNegInf
+                               : ((bs == kTauBins - 1 || sc == 0.0f) ? tlo
+                                                                    : xmax - ((float)bs + 1.5f) / sc);
+        }
+        // tempered rows compare fl(x / T): a margin of 2^-20 keeps every
+        // token whose filter-space value could tie with the k-th
+        const float tc = c.tempered ? tau - (__builtin_fabsf(tau) * 0x1p-20f + 1e-30f) : tau;
+        // entry-table terms exp((x - xmax) / T_f) = exp2(fma(x, lgz, nb)); nb's
+        // rounding error (exact through an fma) is common to them all
+        const float nb = -xmax * lgz;
+        const float nb_err = __builtin_fmaf(-xmax, lgz, -nb);
+        if (zon && !(xmax * lgz < 0x1p20f)) sflags |= kSliceShortOverflow;  // out of range
+        // candidates are listed raw (value bits, id); their filter-space keys
+        // are formed once the list is complete.  A quad with candidates takes
+        // its slots with one LDS atomic.
+        auto raw = [](float x, int32_t id) {
+          return ((uint64_t)__float_as_uint(x) << 32) | (uint64_t)(uint32_t)id;
+        };
+        for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
+          float qm = vec_elem<DT>(v, 0);
+#pragma unroll
+          for (int e = 1; e < N; ++e) qm = __builtin_fmaxf(qm, vec_elem<DT>(v, e));
+          if (qm >= tc) {
+            const int32_t i0 = base32 + (tid + g * kThreads) * N;
+            uint32_t hit = 0u;
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+              const float x = vec_elem<DT>(v, e);
+              hit |= (uint32_t)(x >= tc && x > kNegInf) << e;
+            }
+            int k = atomicAdd(&L.ncand, __builtin_popcount(hit));
+            for (uint32_t b = hit; b != 0u; b &= b - 1u, ++k) {
+              const int e = __builtin_ctz(b);
+              if (k < kShortCap) L.sh.ckey[k] = raw(vec_elem_dyn<DT>(v, e), i0 + e);
+            }
+          }
+          return false;
+        });
+        // the entry table's order depends on atomics: its terms are summed
+        // in fixed point (exact in any order), so the slice's sum is the
+        // same in every run and in both kernel arrangements
+        uint64_t ze = 0ull;
+        for (int j = tid; j < n_ent; j += kThreads) {
+          const float x = L.ex[j];
+          if (!(x > kNegInf)) continue;
+          if (zon) ze += (uint64_t)(__builtin_amdgcn_exp2f(__builtin_fmaf(x, lgz, nb)) * 0x1p40f);
+          if (x >= tc) {
+            const int k = atomicAdd(&L.ncand, 1);
+            if (k < kShortCap) L.sh.ckey[k] = raw(x, L.etok[j]);
+          }
+        }
+        // this thread's register terms, rescaled from 2^-nbz to e^(xmax / T_f)
+        // (xmax * lgz split into a rounded part and its exact residual)
+        const float bh = xmax * lgz;
+        const float bl = __builtin_fmaf(xmax, lgz, -bh);
+        const float zr = (zon && zref) ? zt * __builtin_amdgcn_exp2f((-nbz - bh) - bl) : 0.0f;
+        double zd = wave_sum((double)zr);
+        ze = wave_sum(ze);
+        const int wv = tid >> 6;
+        __syncthreads();
+        if ((tid & 63) == 0) {
+          L.redd[wv] = zd;
+          L.redu[wv] = ze;
+        }
+        __syncthreads();
+        zd = 0.0;
+        ze = 0ull;
+#pragma unroll
+        for (int i = 0; i < kWaves; ++i) {
+          zd += L.redd[i];
+          ze += L.redu[i];
+        }
+        zsum = zd + (double)ze * 0x1p-40 * (double)__builtin_amdgcn_exp2f(nb_err);
+        const int n = L.ncand;
+        if (n > kShortPub) {
+          sflags |= kSliceShortOverflow;
+        } else {
+          // every candidate is published (unsorted); the finalize ranks them
+          npub = n;
+          uint64_t* pub = reinterpret_cast<uint64_t*>(ws.cands + (size_t)row * kCandCap) +
+                          (size_t)slice * kShortPub;
+          for (int i = tid; i < n; i += kThreads) {
+            const uint64_t r = L.sh.ckey[i];
+            st_coherent(&pub[i], cand_key(to_filter(c, __uint_as_float((uint32_t)(r >> 32))),
+                                          (int32_t)(uint32_t)r));
+          }
+        }
+      }
+      if (tid == 0) {
+        st_coherent_f32(&Ssum->x_max, xmax);
+        st_coherent(&Ssum->top_bin, top);
+        st_coherent(&Ssum->flags, sflags);
+        st_coherent(&Ssum->n_finite, (has_finite || posinf) ? 1 : 0);
+        st_coherent_f64(&Ssum->zs, zsum);
+        st_coherent(&Ssum->npub, npub);
+      }
+      if (MODE == kFused) {
+        // first exchange of a short-list row: the last slice to publish
+        // draws the token; the others wait for it only to learn whether a
+        // slice needs the histogram path instead
+        drain_memory();
+        __syncthreads();
+        if (tid == 0) {
+          const uint32_t prev = __hip_atomic_fetch_add(&ws.arrive_stats[row], 1u, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+          const bool last = prev + 1u == (uint32_t)G;
+          if (!last) {
+            int it = 0;
+            while (ld_coherent(&ws.arrive_stats[row]) < (uint32_t)G) {
+              if (++it >= kSpinLimit) {
+                atomicOr(ws.status, kStatusSpinTimeout);
+                break;
+              }
+              __builtin_amdgcn_s_sleep(2);
+            }
+          }
+          L.last = last ? 1 : 0;
+        }
+        __syncthreads();
+        if (L.last) {
+          if (short_gather<DT>(ws, P, row, c, prm, L)) {
+            short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K);
+            return;
+          }
+        } else if (!short_fallback(ws, row, G, L)) {
+          if (tid == 0) short_depart(ws, row, G);
+          return;
+        }
+      }
+    }
+
+    // ------------------------------------------------ B: histogram
     const bool want_hist = has_finite && c.kind != LSAMP_KIND_ARGMAX;
     if (want_hist) {
       const float tail_edge = (float)(top - kBins + 1);
@@ -1197,25 +1958,8 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       }
     }
     __syncthreads();
-    if (P.processed) {
-      float* out = P.processed + (size_t)row * (size_t)V;
-      for_quads(S, nq, [&](int g, uint4& v) -> bool {
-        const int32_t i0 = base32 + (tid + g * kThreads) * N;
-        if (i0 >= end32) return false;
-        const int32_t li0 = i0 - base32;
-        const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
-#pragma unroll
-        for (int e = 0; e < N; ++e) {
-          if (i0 + e >= end32 || ((pen >> e) & 1u)) continue;
-          out[i0 + e] = to_filter(c, vec_elem<DT>(v, e));
-        }
-        return false;
-      });
-      for (int j = tid; j < n_ent; j += kThreads) out[L.etok[j]] = to_filter(c, L.ex[j]);
-    }
     // publish the slice summary; n_finite is the histogram's token count
     // (rows that build one) or whether the slice holds a finite logit
-    SliceSummary* Ssum = ws.summaries + ((size_t)row * kMaxSlices + slice);
     int32_t nfin = 0;
     double zs = 0.0;  // total mass relative to the top edge of the slice's top bin
     if (want_hist) {
@@ -1227,7 +1971,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         nfin += (int32_t)(w >> kCountShift);
         // bin i's top edge lies i bins below the slice's; the tail's mass is
         // relative to the window's lowest edge, kBins below
-        zs += (double)(w & kMassMask) * inv_frac * exp(-(double)i / (32.0 * c.tf));
+        zs += (double)(w & kMassMask) * inv_frac * fexp(-(double)i / (32.0 * c.tf));
       }
       nfin = wave_sum(nfin);
       zs = wave_sum(zs);
@@ -1256,16 +2000,18 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     }
     if (MODE == kFused) {
       // all-gather: wait until every slice of the row has published, then
-      // merge here (the merge is deterministic, so all slices agree)
+      // merge here (the merge is deterministic, so all slices agree); a
+      // short-list row that fell back counts its second arrival
+      const uint32_t target = (uint32_t)(K > 0 ? 2 * G : G);
       drain_memory();
       __syncthreads();
       if (tid == 0) {
         const uint32_t prev = __hip_atomic_fetch_add(&ws.arrive_stats[row], 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
-        if (prev + 1u < (uint32_t)G) {
+        if (prev + 1u < target) {
           // bounded: a wait that runs out sets a status bit, so the grid drains
           int it = 0;
-          while (ld_coherent(&ws.arrive_stats[row]) < (uint32_t)G) {
+          while (ld_coherent(&ws.arrive_stats[row]) < target) {
             if (++it >= kSpinLimit) {
               atomicOr(ws.status, kStatusSpinTimeout);
               break;
@@ -1279,6 +2025,11 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       info = L.info;
     } else {
       if (!arrive_last(&ws.arrive_stats[row], (uint32_t)G, &L.last)) return;
+      if (K > 0 && short_gather<DT>(ws, P, row, c, prm, L)) {
+        short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K);
+        if (tid == 0) ws.arrive_stats[row] = 0u;
+        return;
+      }
       merge_row(ws, P, row, c, prm, L);
       if (tid == 0) {
         ws.rows[row] = L.info;
