@@ -35,10 +35,10 @@ constexpr int kCandCap = 4096;
 constexpr int kWgCandCap = 2048;
 // Short-list rows (argmax, or top-k <= kShortMaxK): each slice lists the
 // tokens at or above a threshold taken from its threads' maxima (at most
-// kShortCap in LDS) and publishes its own top-k plus ties (at most kShortPub,
-// which the row's candidate area holds for every slice).
+// kStage per thread, staged in LDS) and publishes them all (at most
+// kShortPub, which the row's candidate area holds for every slice).
 constexpr int kShortMaxK = 256;
-constexpr int kShortCap = 1024;
+constexpr int kStage = 8;
 constexpr int kShortPub = kCandCap / kMaxSlices;  // 512
 constexpr int kTauBins = 1024;                    // thread-maximum histogram
 // Kept tokens listed per slice (fast draw path); beyond this the draw scans.

@@ -377,7 +377,7 @@ union PhaseLds {
 // Short-list slice phase: thread-maximum histogram and the slice's candidates.
 struct ShortLds {
   uint32_t tcnt[kTauBins];
-  uint64_t ckey[kShortCap];  // raw candidates: value bits << 32 | token id
+  uint64_t stage[kThreads * kStage];  // per thread: raw candidates, value bits << 32 | id
 };
 struct TaskLds {
   PhaseLds u;
@@ -1805,11 +1805,18 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         const float nb = -xmax * lgz;
         const float nb_err = __builtin_fmaf(-xmax, lgz, -nb);
         if (zon && !(xmax * lgz < 0x1p20f)) sflags |= kSliceShortOverflow;  // out of range
-        // candidates are listed raw (value bits, id); their filter-space keys
-        // are formed once the list is complete.  A quad with candidates takes
-        // its slots with one LDS atomic.
+        // candidates: each thread stages its own, raw (value bits, id), in a
+        // private run of kStage LDS slots (no atomics in the pass); a scan of
+        // the counts lays the slice's list out, and the filter-space keys are
+        // formed as it is published
         auto raw = [](float x, int32_t id) {
           return ((uint64_t)__float_as_uint(x) << 32) | (uint64_t)(uint32_t)id;
+        };
+        uint64_t* stg = L.sh.stage + tid * kStage;
+        int cnt = 0;
+        auto stage = [&](float x, int32_t id) {
+          if (cnt < kStage) stg[cnt] = raw(x, id);
+          ++cnt;
         };
         for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
           float qm = vec_elem<DT>(v, 0);
@@ -1817,16 +1824,10 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
           for (int e = 1; e < N; ++e) qm = __builtin_fmaxf(qm, vec_elem<DT>(v, e));
           if (qm >= tc) {
             const int32_t i0 = base32 + (tid + g * kThreads) * N;
-            uint32_t hit = 0u;
 #pragma unroll
             for (int e = 0; e < N; ++e) {
               const float x = vec_elem<DT>(v, e);
-              hit |= (uint32_t)(x >= tc && x > kNegInf) << e;
-            }
-            int k = atomicAdd(&L.ncand, __builtin_popcount(hit));
-            for (uint32_t b = hit; b != 0u; b &= b - 1u, ++k) {
-              const int e = __builtin_ctz(b);
-              if (k < kShortCap) L.sh.ckey[k] = raw(vec_elem_dyn<DT>(v, e), i0 + e);
+              if (x >= tc && x > kNegInf) stage(x, i0 + e);
             }
           }
           return false;
@@ -1839,11 +1840,11 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
           const float x = L.ex[j];
           if (!(x > kNegInf)) continue;
           if (zon) ze += (uint64_t)(__builtin_amdgcn_exp2f(__builtin_fmaf(x, lgz, nb)) * 0x1p40f);
-          if (x >= tc) {
-            const int k = atomicAdd(&L.ncand, 1);
-            if (k < kShortCap) L.sh.ckey[k] = raw(x, L.etok[j]);
-          }
+          if (x >= tc) stage(x, L.etok[j]);
         }
+        // a thread past its slots makes the slice's count exceed any list
+        const int cw = cnt > kStage ? kShortPub + 1 : cnt;
+        const int ci = wave_incl_scan(cw);
         // this thread's register terms, rescaled from 2^-nbz to e^(xmax / T_f)
         // (xmax * lgz split into a rounded part and its exact residual)
         const float bh = xmax * lgz;
@@ -1857,26 +1858,29 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
           L.redd[wv] = zd;
           L.redu[wv] = ze;
         }
+        if ((tid & 63) == 63) L.redi[wv] = ci;
         __syncthreads();
         zd = 0.0;
         ze = 0ull;
+        int n = 0, off = ci - cw;
 #pragma unroll
         for (int i = 0; i < kWaves; ++i) {
           zd += L.redd[i];
           ze += L.redu[i];
+          off += i < wv ? L.redi[i] : 0;
+          n += L.redi[i];
         }
         zsum = zd + (double)ze * 0x1p-40 * (double)__builtin_amdgcn_exp2f(nb_err);
-        const int n = L.ncand;
         if (n > kShortPub) {
           sflags |= kSliceShortOverflow;
         } else {
           // every candidate is published (unsorted); the finalize ranks them
           npub = n;
           uint64_t* pub = reinterpret_cast<uint64_t*>(ws.cands + (size_t)row * kCandCap) +
-                          (size_t)slice * kShortPub;
-          for (int i = tid; i < n; i += kThreads) {
-            const uint64_t r = L.sh.ckey[i];
-            st_coherent(&pub[i], cand_key(to_filter(c, __uint_as_float((uint32_t)(r >> 32))),
+                          (size_t)slice * kShortPub + off;
+          for (int k = 0; k < cnt; ++k) {
+            const uint64_t r = stg[k];
+            st_coherent(&pub[k], cand_key(to_filter(c, __uint_as_float((uint32_t)(r >> 32))),
                                           (int32_t)(uint32_t)r));
           }
         }
