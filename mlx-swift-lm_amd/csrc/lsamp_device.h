@@ -45,6 +45,16 @@ __device__ __forceinline__ float vec_elem(const uint4& r, int k) {
   }
 }
 
+// Largest element of a 16-byte vector that holds no NaN (NaN-propagating
+// maximum: no quieting moves are needed ahead of it).
+template <int DT>
+__device__ __forceinline__ float vec_max_nn(const uint4& r) {
+  float m = vec_elem<DT>(r, 0);
+#pragma unroll
+  for (int k = 1; k < Vec<DT>::N; ++k) m = __builtin_elementwise_maximum(m, vec_elem<DT>(r, k));
+  return m;
+}
+
 // Element e of a 16-byte vector, e not known at compile time.
 template <int DT>
 __device__ __forceinline__ float vec_elem_dyn(const uint4& r, int e) {

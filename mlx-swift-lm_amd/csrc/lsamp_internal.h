@@ -34,11 +34,12 @@ constexpr int kMassFracBits = 29;
 constexpr int kCandCap = 4096;
 constexpr int kWgCandCap = 2048;
 // Short-list rows (argmax, or top-k <= kShortMaxK): each slice lists the
-// tokens at or above a threshold taken from its threads' maxima (at most
-// kStage per thread, staged in LDS) and publishes them all (at most
-// kShortPub, which the row's candidate area holds for every slice).
+// tokens at or above a threshold taken from its threads' maxima (the quads
+// holding them staged whole in LDS, at most kQStage per thread) and
+// publishes them all (at most kShortPub, which the row's candidate area
+// holds for every slice).
 constexpr int kShortMaxK = 256;
-constexpr int kStage = 8;
+constexpr int kQStage = 3;
 constexpr int kShortPub = kCandCap / kMaxSlices;  // 512
 constexpr int kTauBins = 1024;                    // thread-maximum histogram
 // Kept tokens listed per slice (fast draw path); beyond this the draw scans.

@@ -254,7 +254,6 @@ __device__ __forceinline__ int classify(const ClassRule& r, float x) {
 // kernels (they must classify identically).
 struct SliceEntries {
   uint32_t* pen;    // [kSliceWords]
-  uint32_t* qflag;  // [kThreads]: bit g set when quad g of that thread holds an entry
   int32_t* tok;     // [kSliceEntryCap]
   float* x;         // [kSliceEntryCap] transformed, -inf when masked / NaN
   int32_t* count;   // LDS counter
@@ -297,14 +296,11 @@ __device__ __forceinline__ int build_slice_entries(const SamplePlan& P, const Ro
   constexpr int N = Vec<DT>::N;
   const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
   for (int i = tid; i < kSliceWords; i += kThreads) se.pen[i] = 0u;
-  se.qflag[tid] = 0u;
   if (tid == 0) *se.count = 0;
   lds_barrier();
   auto mark = [&](int32_t t) {
     const int32_t li = t - (int32_t)base;
     atomicOr(&se.pen[li >> 5], 1u << (li & 31));
-    const int32_t q = li / N;
-    atomicOr(&se.qflag[q % kThreads], 1u << (q / kThreads));
     return atomicAdd(se.count, 1);
   };
   auto patched = [&](float x, const lsamp_penalty_entry& ent) {
@@ -377,7 +373,7 @@ union PhaseLds {
 // Short-list slice phase: thread-maximum histogram and the slice's candidates.
 struct ShortLds {
   uint32_t tcnt[kTauBins];
-  uint64_t stage[kThreads * kStage];  // per thread: raw candidates, value bits << 32 | id
+  uint4 squad[(kQStage + 1) * kThreads];  // slot k of thread t at k * kThreads + t; k = kQStage discards
 };
 struct TaskLds {
   PhaseLds u;
@@ -385,7 +381,6 @@ struct TaskLds {
   uint64_t ssrc[kCandCap];  // short-list finalize: the slices' published keys
   int32_t soff[kMaxSlices + 1];
   uint32_t pen[kSliceWords];
-  uint32_t qflag[kThreads];
   int32_t etok[kSliceEntryCap];
   float ex[kSliceEntryCap];
   RowInfo info;
@@ -1560,6 +1555,8 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   if (MODE == kSelectOnly && ws.rows[row].done) return;
   constexpr int N = Vec<DT>::N;
   constexpr int Q = Slab<DT>::Q;
+  static_assert(Q <= 32, "staged quad numbers take 5 bits");
+  static_assert(kSliceEntryCap <= 32 * kThreads, "entry candidates take one bit each");
   constexpr uint32_t FULL = (1u << N) - 1u;
   constexpr int ES = Vec<DT>::ESIZE;
   const int tid = fresh_tid();
@@ -1619,7 +1616,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     L.flags = 0u;
     L.ncand = 0;
   }
-  SliceEntries se{L.pen, L.qflag, L.etok, L.ex, &L.ecount};
+  SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
   bool ent_overflow = false;
   const int n_ent = build_slice_entries<DT>(P, c, prm, row, rowp, base, end, se, &ent_overflow, ep, tid);
 
@@ -1634,55 +1631,58 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   const int K = MODE != kSelectOnly ? short_k(c, prm, V) : 0;
   const bool zon = K > 0 && c.kind != LSAMP_KIND_ARGMAX;
   const float lgz = (float)(1.4426950408889634 / c.tf);  // log2(e) / T_f
-  // penalty-bitmap word of quad g, read only for quads holding an entry;
-  // fetched one quad ahead so the LDS read overlaps the current quad
-  const uint32_t qf = L.qflag[tid];
-  auto pen_word = [&](int g) -> uint32_t {
-    return ((qf >> g) & 1u) ? L.pen[((tid + g * kThreads) * N) >> 5] : 0u;
-  };
+  // penalty-bitmap word of quad g (the bitmap is zeroed over the largest
+  // slice, so every quad's word is in bounds); fetched one quad ahead so the
+  // LDS read overlaps the current quad
+  const uint32_t* penw = L.pen + ((tid * N) >> 5);
+  constexpr int kQuadWords = kThreads * N / 32;  // bitmap words per quad row
   const uint32_t pen_shift = (uint32_t)((tid * N) & 31);
-  uint32_t pw = nq > 0 ? pen_word(0) : 0u;
+  // tokens of the slice from this thread's first position on: quad g holds
+  // lim - g * kThreads * N of them (lanes past the end are excluded)
+  const int32_t lim = end32 - base32 - tid * N;
+  uint32_t pw = penw[0];
   uint32_t nf_acc = 0u;
   float xmax = kNegInf;
-  float zt = 0.0f, nbz = 0.0f;
-  bool zref = false;
+  // exp-sum anchor: nbz starts above every quad, so the first finite quad
+  // anchors, and the shift of that first anchor clears what came before
+  float zt = 0.0f, nbz = __FLT_MAX__;
   for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
     const int32_t i0 = base32 + (tid + g * kThreads) * N;
     const uint32_t pcur = pw;
-    pw = g + 1 < nq ? pen_word(g + 1) : 0u;
+    if (g + 1 < Q) pw = penw[(g + 1) * kQuadWords];
     const uint32_t probe = nonfinite_probe<DT>(v);
     nf_acc |= probe;
-    uint32_t ex = (pcur >> pen_shift) & FULL;
-    if (i0 + N > end32) ex |= i0 >= end32 ? FULL : (FULL & ~((1u << (end32 - i0)) - 1u));
+    const int32_t rem = lim - g * (kThreads * N);
+    const uint32_t tail = ~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem));
+    uint32_t ex = ((pcur >> pen_shift) | tail) & FULL;
     if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
-    if (nonfinite_seen<DT>(probe)) {
+    if (ex != 0u || nonfinite_seen<DT>(probe)) {
 #pragma unroll
       for (int e = 0; e < N; ++e) {
         const float x = vec_elem<DT>(v, e);
         if (x != x) ex |= 1u << e;
       }
+      exclude_elems<DT>(v, ex);
     }
-    if (ex != 0u) exclude_elems<DT>(v, ex);
     if (MODE != kSelectOnly) {
-      float qm = vec_elem<DT>(v, 0);
-#pragma unroll
-      for (int e = 1; e < N; ++e) qm = __builtin_fmaxf(qm, vec_elem<DT>(v, e));
-      xmax = __builtin_fmaxf(xmax, qm);
+      const float qm = vec_max_nn<DT>(v);  // NaNs are excluded by now
+      xmax = __builtin_elementwise_maximum(xmax, qm);
       if (zon) {
-        const float ql = qm * lgz;
-        if (ql > -0x1p20f && ql < 0x1p20f && (!zref || __builtin_fmaf(qm, lgz, nbz) > 64.0f)) {
-          const float nn = -__builtin_ceilf(ql);
-          zt = zref ? __builtin_ldexpf(zt, (int)(nn - nbz)) : 0.0f;
+        // re-anchor when the quad's terms could pass 2^64 (an exact power-of-
+        // two rescale; the anchor is an integer, clamped to +-2^20)
+        if (__builtin_fmaf(qm, lgz, nbz) > 64.0f) {
+          const float nn = -__builtin_ceilf(__builtin_amdgcn_fmed3f(qm * lgz, -0x1p20f, 0x1p20f));
+          zt = __builtin_ldexpf(zt, (int)__builtin_fmaxf(nn - nbz, -512.0f));
           nbz = nn;
-          zref = true;
         }
 #pragma unroll
         for (int e = 0; e < N; ++e)
           zt += __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(v, e), lgz, nbz));
       }
     }
-    return ex != 0u;
+    return true;
   });
+  const bool zref = nbz < __FLT_MAX__;
   const bool nonfinite = nonfinite_seen<DT>(nf_acc);
 
   RowInfo info;
@@ -1805,30 +1805,24 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         const float nb = -xmax * lgz;
         const float nb_err = __builtin_fmaf(-xmax, lgz, -nb);
         if (zon && !(xmax * lgz < 0x1p20f)) sflags |= kSliceShortOverflow;  // out of range
-        // candidates: each thread stages its own, raw (value bits, id), in a
-        // private run of kStage LDS slots (no atomics in the pass); a scan of
-        // the counts lays the slice's list out, and the filter-space keys are
-        // formed as it is published
-        auto raw = [](float x, int32_t id) {
-          return ((uint64_t)__float_as_uint(x) << 32) | (uint64_t)(uint32_t)id;
-        };
-        uint64_t* stg = L.sh.stage + tid * kStage;
-        int cnt = 0;
-        auto stage = [&](float x, int32_t id) {
-          if (cnt < kStage) stg[cnt] = raw(x, id);
-          ++cnt;
-        };
+        // candidates are the tokens x >= tcp (tcp >= -FLT_MAX also rules out
+        // -inf).  A quad holding one is staged whole in the thread's next LDS
+        // slot (past kQStage into a discard slot) and its candidates counted,
+        // all without branching per token; entry-table candidates are marked
+        // by their table position.  A scan of the counts lays the slice's
+        // list out, and the quads are expanded as it is published.
+        const float tcp = __builtin_fmaxf(tc, -__FLT_MAX__);
+        uint4* sq = L.sh.squad + tid;
+        int qn = 0, cnt = 0;
+        uint32_t qids = 0u;  // staged quad numbers, 5 bits per slot
         for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
-          float qm = vec_elem<DT>(v, 0);
+          if (vec_max_nn<DT>(v) >= tcp) {
 #pragma unroll
-          for (int e = 1; e < N; ++e) qm = __builtin_fmaxf(qm, vec_elem<DT>(v, e));
-          if (qm >= tc) {
-            const int32_t i0 = base32 + (tid + g * kThreads) * N;
-#pragma unroll
-            for (int e = 0; e < N; ++e) {
-              const float x = vec_elem<DT>(v, e);
-              if (x >= tc && x > kNegInf) stage(x, i0 + e);
-            }
+            for (int e = 0; e < N; ++e) cnt += vec_elem<DT>(v, e) >= tcp ? 1 : 0;
+            const int slot = qn < kQStage ? qn : kQStage;
+            sq[slot * kThreads] = v;
+            qids |= (uint32_t)g << (5 * slot);
+            ++qn;
           }
           return false;
         });
@@ -1836,14 +1830,18 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         // in fixed point (exact in any order), so the slice's sum is the
         // same in every run and in both kernel arrangements
         uint64_t ze = 0ull;
-        for (int j = tid; j < n_ent; j += kThreads) {
+        uint32_t ebits = 0u;  // bit k: entry tid + k * kThreads is a candidate
+        for (int j = tid, k = 0; j < n_ent; j += kThreads, ++k) {
           const float x = L.ex[j];
           if (!(x > kNegInf)) continue;
           if (zon) ze += (uint64_t)(__builtin_amdgcn_exp2f(__builtin_fmaf(x, lgz, nb)) * 0x1p40f);
-          if (x >= tc) stage(x, L.etok[j]);
+          if (x >= tcp) {
+            ebits |= 1u << k;
+            ++cnt;
+          }
         }
         // a thread past its slots makes the slice's count exceed any list
-        const int cw = cnt > kStage ? kShortPub + 1 : cnt;
+        const int cw = qn > kQStage ? kShortPub + 1 : cnt;
         const int ci = wave_incl_scan(cw);
         // this thread's register terms, rescaled from 2^-nbz to e^(xmax / T_f)
         // (xmax * lgz split into a rounded part and its exact residual)
@@ -1878,10 +1876,19 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
           npub = n;
           uint64_t* pub = reinterpret_cast<uint64_t*>(ws.cands + (size_t)row * kCandCap) +
                           (size_t)slice * kShortPub + off;
-          for (int k = 0; k < cnt; ++k) {
-            const uint64_t r = stg[k];
-            st_coherent(&pub[k], cand_key(to_filter(c, __uint_as_float((uint32_t)(r >> 32))),
-                                          (int32_t)(uint32_t)r));
+          int w = 0;
+          for (int k = 0; k < qn; ++k) {
+            const uint4 v = sq[k * kThreads];
+            const int32_t i0 = base32 + (tid + (int)((qids >> (5 * k)) & 31u) * kThreads) * N;
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+              const float x = vec_elem<DT>(v, e);
+              if (x >= tcp) st_coherent(&pub[w++], cand_key(to_filter(c, x), i0 + e));
+            }
+          }
+          for (; ebits != 0u; ebits &= ebits - 1u) {
+            const int j = tid + __builtin_ctz(ebits) * kThreads;
+            st_coherent(&pub[w++], cand_key(to_filter(c, L.ex[j]), L.etok[j]));
           }
         }
       }
@@ -2093,9 +2100,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       const int32_t i0 = base32 + (tid + g * kThreads) * N;
       // screen the quad by its largest element; the rare quads that hold a
       // kept or candidate token are classified element by element
-      float qm = vec_elem<DT>(v, 0);
-#pragma unroll
-      for (int e = 1; e < N; ++e) qm = __builtin_fmaxf(qm, vec_elem<DT>(v, e));
+      const float qm = vec_max_nn<DT>(v);
       uint64_t part = 0ull;
       if (qm * rule.c32 >= rule.screen) {
         uint32_t kb = 0u, cb = 0u;
