@@ -416,6 +416,19 @@ __device__ __forceinline__ void st_coherent_f64(double* p, double v) {
 // Wait until every memory operation this wave issued has completed.
 __device__ __forceinline__ void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
+// A read-only value at a uniform address, through the scalar data cache (a
+// load from the constant address space): such loads count apart from the
+// vector loads, which complete in order, so they do not wait behind a slice
+// in flight.  The address passes through an SGPR pair as an integer, or the
+// compiler would trace it back to a global pointer and load it as such.
+// `p` must be the same in every lane.
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* p) {
+  uint64_t a = (uint64_t)p;
+  asm volatile("" : "+s"(a));
+  return *(const __attribute__((address_space(4))) T*)a;
+}
+
 // Work-group barrier for LDS traffic only: each wave waits for its own LDS
 // (and scalar) operations, not for its global loads, so loads in flight keep
 // streaming across it.  It orders nothing in global memory.

@@ -38,6 +38,9 @@ using namespace dev;
 
 constexpr int kSliceWords = kMaxSliceLen / 32;       // penalty bitmap words
 constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
+// Fourth word of a raw buffer descriptor on gfx9-family parts (32-bit data
+// format; no swizzle, no stride).
+constexpr int kBufferWord3 = 0x00020000;
 
 enum TaskMode { kFused = 0, kStatsOnly = 1, kSelectOnly = 2 };
 
@@ -192,6 +195,17 @@ __device__ __forceinline__ float load_logit(int dt, const char* rowp, int64_t i)
   return load_scalar<LSAMP_DTYPE_F16>(rowp, i);
 }
 
+// The row's parameters, as two 16-byte scalar loads.
+__device__ __forceinline__ lsamp_row_params load_params(const SamplePlan& P, int row) {
+  static_assert(sizeof(lsamp_row_params) == 32, "two 16-byte words");
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4* w = reinterpret_cast<const u32x4*>(P.params + params_index(P, row));
+  struct {
+    u32x4 a, b;
+  } raw = {load_uniform(w), load_uniform(w + 1)};
+  return __builtin_bit_cast(lsamp_row_params, raw);
+}
+
 // Token classes relative to the row's cut.
 constexpr int kDrop = 0, kKept = 1, kCand = 2;
 
@@ -260,41 +274,62 @@ struct SliceEntries {
 };
 
 // The row's first kEntPrefetch * kThreads penalty entries, one per thread and
-// pass, fetched before the slice's logits so that their loads return first
-// and the entry table is built while the slice is still streaming in.
+// pass, requested right behind the slice's logits (the CSR bounds come
+// through scalar loads, so they do not wait for the slice).
 constexpr int kEntPrefetch = 2;
 struct EntryPrefetch {
   int32_t e0, e1;
-  lsamp_penalty_entry ent[kEntPrefetch];
+  lsamp_penalty_entry ent[kEntPrefetch];  // zero past the row's entries
+  __device__ bool has(int tid, int k) const { return e0 + tid + k * kThreads < e1; }
 };
 
 __device__ __forceinline__ void prefetch_entries(const SamplePlan& P, int row, int tid,
                                                  EntryPrefetch& ep) {
+  static_assert(sizeof(lsamp_penalty_entry) == 16, "one 16-byte load per entry");
   ep.e0 = 0;
   ep.e1 = 0;
   if (P.row_ptr && P.entries) {
-    ep.e0 = P.row_ptr[row];
-    ep.e1 = P.row_ptr[row + 1];
+    ep.e0 = load_uniform(P.row_ptr + row);
+    ep.e1 = load_uniform(P.row_ptr + row + 1);
   }
+  // one buffer descriptor over the row's entries: lanes past them read zero,
+  // and no branch holds a load back
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<lsamp_penalty_entry*>(P.entries) + ep.e0, 0,
+      (ep.e1 - ep.e0) * (int)sizeof(lsamp_penalty_entry), kBufferWord3);
 #pragma unroll
   for (int k = 0; k < kEntPrefetch; ++k) {
-    const int32_t e = ep.e0 + tid + k * kThreads;
-    if (e < ep.e1) {
-      ep.ent[k] = P.entries[e];
-    } else {
-      ep.ent[k].token = -1;
-    }
+    const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, (tid + k * kThreads) * 16, 0, 0);
+    ep.ent[k] = __builtin_bit_cast(lsamp_penalty_entry, make_uint4(w[0], w[1], w[2], w[3]));
   }
 }
 
+// The slice's penalty entries in two steps around the pass over the slice.
+// mark_slice_entries sets the bitmap of entry tokens (which the pass
+// excludes) and gives each entry its table slot; the logits of the
+// prefetched entries are requested here and arrive while the pass runs.
+// finish_slice_entries patches them into the table.  Both steps fold the
+// patched values of the calling thread's entries into `emax`.
+struct EntryMarks {
+  int slot[kEntPrefetch];
+  float xr[kEntPrefetch];
+};
+
 template <int DT>
-__device__ __forceinline__ int build_slice_entries(const SamplePlan& P, const RowCtx& c,
-                                                   const lsamp_row_params& prm, int row,
+__device__ __forceinline__ float patched_entry(const SamplePlan& P, const RowCtx& c,
+                                               const lsamp_row_params& prm, const uint32_t* mrow,
+                                               float x, const lsamp_penalty_entry& ent) {
+  x = patch_value(c, prm, x, ent, DT);
+  if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, ent.token)) x = kNegInf;
+  return x != x ? kNegInf : x;
+}
+
+template <int DT>
+__device__ __forceinline__ void mark_slice_entries(const SamplePlan& P, const RowCtx& c,
+                                                   const lsamp_row_params& prm, const uint32_t* mrow,
                                                    const char* rowp, int64_t base, int64_t end,
-                                                   SliceEntries& se, bool* overflow,
-                                                   const EntryPrefetch& ep, int tid) {
-  constexpr int N = Vec<DT>::N;
-  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
+                                                   SliceEntries& se, const EntryPrefetch& ep,
+                                                   int tid, EntryMarks& em, float& emax) {
   for (int i = tid; i < kSliceWords; i += kThreads) se.pen[i] = 0u;
   if (tid == 0) *se.count = 0;
   lds_barrier();
@@ -303,23 +338,14 @@ __device__ __forceinline__ int build_slice_entries(const SamplePlan& P, const Ro
     atomicOr(&se.pen[li >> 5], 1u << (li & 31));
     return atomicAdd(se.count, 1);
   };
-  auto patched = [&](float x, const lsamp_penalty_entry& ent) {
-    x = patch_value(c, prm, x, ent, DT);
-    if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, ent.token)) x = kNegInf;
-    return x != x ? kNegInf : x;
-  };
-  // the prefetched entries: their logits are gathered now and patched below
-  int slot[kEntPrefetch];
-  float xr[kEntPrefetch];
+  // (the gather is unconditional, from the slice's first token when there
+  // is no entry, so that nothing waits for it before it is used)
 #pragma unroll
   for (int k = 0; k < kEntPrefetch; ++k) {
     const int32_t t = ep.ent[k].token;
-    slot[k] = -1;
-    xr[k] = 0.0f;
-    if (t >= base && t < end) {
-      slot[k] = mark(t);
-      xr[k] = load_scalar<DT>(rowp, t);
-    }
+    const bool in = ep.has(tid, k) && t >= base && t < end;
+    em.slot[k] = in ? mark(t) : -1;
+    em.xr[k] = load_scalar<DT>(rowp, in ? t : base);
   }
   // the rest of a long history
   for (int32_t e = ep.e0 + tid + kEntPrefetch * kThreads; e < ep.e1; e += kThreads) {
@@ -327,22 +353,31 @@ __device__ __forceinline__ int build_slice_entries(const SamplePlan& P, const Ro
     if (ent.token >= base && ent.token < end) {
       const int idx = mark(ent.token);
       if (idx < kSliceEntryCap) {
-        se.x[idx] = patched(load_scalar<DT>(rowp, ent.token), ent);
+        const float x = patched_entry<DT>(P, c, prm, mrow, load_scalar<DT>(rowp, ent.token), ent);
+        se.x[idx] = x;
         se.tok[idx] = ent.token;
+        emax = __builtin_fmaxf(emax, x);
       }
     }
   }
+  lds_barrier();  // the bitmap is complete
+}
+
+template <int DT>
+__device__ __forceinline__ void finish_slice_entries(const SamplePlan& P, const RowCtx& c,
+                                                     const lsamp_row_params& prm,
+                                                     const uint32_t* mrow, SliceEntries& se,
+                                                     const EntryPrefetch& ep, const EntryMarks& em,
+                                                     float& emax) {
 #pragma unroll
   for (int k = 0; k < kEntPrefetch; ++k) {
-    if (slot[k] >= 0 && slot[k] < kSliceEntryCap) {
-      se.x[slot[k]] = patched(xr[k], ep.ent[k]);
-      se.tok[slot[k]] = ep.ent[k].token;
+    if (em.slot[k] >= 0 && em.slot[k] < kSliceEntryCap) {
+      const float x = patched_entry<DT>(P, c, prm, mrow, em.xr[k], ep.ent[k]);
+      se.x[em.slot[k]] = x;
+      se.tok[em.slot[k]] = ep.ent[k].token;
+      emax = __builtin_fmaxf(emax, x);
     }
   }
-  lds_barrier();
-  const int n_all = *se.count;
-  *overflow = n_all > kSliceEntryCap;
-  return n_all < kSliceEntryCap ? n_all : kSliceEntryCap;
 }
 
 // ----------------------------------------------------------------- LDS
@@ -1561,36 +1596,43 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   constexpr int ES = Vec<DT>::ESIZE;
   const int tid = fresh_tid();
   const int G = P.slices;
-  const lsamp_row_params prm = P.params[params_index(P, row)];
-  const RowCtx c = make_ctx(P.semantics, prm);
   const int64_t V = P.vocab;
   const int64_t base = (int64_t)slice * P.slice_len;
   const int64_t end = (base + P.slice_len < V) ? base + P.slice_len : V;
   const char* rowp = row_base(P, row);
-  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
   const bool aligned = P.aligned != 0;
   // Token positions within a row fit in 32 bits (vocab <= kMaxVocab).
   const int32_t base32 = (int32_t)base, end32 = (int32_t)end;
   const int nq = (P.slice_len + kThreads * N - 1) / (kThreads * N);  // quads per thread
 
   // ---------------------------------------------------- A: loads + entries
+  // The slice's logits are requested first, as 16-byte vectors all in flight
+  // at once, through one buffer descriptor over the slice: the lane's byte
+  // offset is fixed and the quad's is a scalar, and lanes past the slice end
+  // read as zero (range check) until the exclusion pass.
+  Slab<DT> S;
+  if (aligned) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(rowp) + (size_t)base32 * ES, 0, (end32 - base32) * ES, kBufferWord3);
+    const int lane_off = tid * 16;
+#pragma unroll
+    for (int g = 0; g < Q; ++g) {
+      if (g < nq) {
+        const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, g * kThreads * 16, 0);
+        quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, make_uint4(w[0], w[1], w[2], w[3]));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < Q; ++g)
+      if (g < nq) quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, make_uint4(0u, 0u, 0u, 0u));
+  }
+  // the row's parameters (scalar loads) and its first penalty entries
+  const lsamp_row_params prm = load_params(P, row);
+  const RowCtx c = make_ctx(P.semantics, prm);
+  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
   EntryPrefetch ep;
   prefetch_entries(P, row, tid, ep);
-  // Aligned whole quads are read as 16-byte vectors, all in flight at once;
-  // lanes past the slice end read as zero until the exclusion pass.
-  // (uniform base address per quad + the lane's 32-bit byte offset)
-  Slab<DT> S;
-  const uint32_t lane_off = (uint32_t)tid * 16u;
-#pragma unroll
-  for (int g = 0; g < Q; ++g) {
-    if (g < nq) {
-      const int32_t i0 = base32 + (tid + g * kThreads) * N;
-      const char* qbase = rowp + ((size_t)base32 + (size_t)g * kThreads * N) * ES;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (aligned && i0 + N <= end32) v = *reinterpret_cast<const uint4*>(qbase + lane_off);
-      quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, v);
-    }
-  }
   if (!aligned || (end32 & (N - 1)) != 0) {
     // unaligned rows, or the row's last partial quad: element by element
     for_quads(S, nq, [&](int g, uint4& v) -> bool {
@@ -1617,8 +1659,9 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     L.ncand = 0;
   }
   SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
-  bool ent_overflow = false;
-  const int n_ent = build_slice_entries<DT>(P, c, prm, row, rowp, base, end, se, &ent_overflow, ep, tid);
+  EntryMarks em;
+  float emax = kNegInf;  // this thread's patched entry values
+  mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
 
   // Masked tokens, tokens of the entry table (their patched values live in
   // L.ex) and lanes past the slice end become -inf in the register copy, and
@@ -1656,14 +1699,15 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     const uint32_t tail = ~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem));
     uint32_t ex = ((pcur >> pen_shift) | tail) & FULL;
     if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
-    if (ex != 0u || nonfinite_seen<DT>(probe)) {
+    // (two branches: a wave meets an entry token in most quads, a NaN rarely)
+    if (nonfinite_seen<DT>(probe)) {
 #pragma unroll
       for (int e = 0; e < N; ++e) {
         const float x = vec_elem<DT>(v, e);
         if (x != x) ex |= 1u << e;
       }
-      exclude_elems<DT>(v, ex);
     }
+    if (ex != 0u) exclude_elems<DT>(v, ex);
     if (MODE != kSelectOnly) {
       const float qm = vec_max_nn<DT>(v);  // NaNs are excluded by now
       xmax = __builtin_elementwise_maximum(xmax, qm);
@@ -1683,12 +1727,17 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     return true;
   });
   const bool zref = nbz < __FLT_MAX__;
+  finish_slice_entries<DT>(P, c, prm, mrow, se, ep, em, emax);
+  xmax = __builtin_fmaxf(xmax, emax);
+  lds_barrier();  // the entry table is complete
+  const int n_all = L.ecount;
+  const bool ent_overflow = n_all > kSliceEntryCap;
+  const int n_ent = n_all < kSliceEntryCap ? n_all : kSliceEntryCap;
   const bool nonfinite = nonfinite_seen<DT>(nf_acc);
 
   RowInfo info;
   if (MODE != kSelectOnly) {
     // ------------------------------------------------ B: max
-    for (int j = tid; j < n_ent; j += kThreads) xmax = __builtin_fmaxf(xmax, L.ex[j]);
     if (nonfinite) atomicOr(&L.flags, LSAMP_ROW_NONFINITE);
     const float tmax = xmax;  // this thread's largest (transformed) logit
     float tlo = kPosInf;      // smallest finite thread maximum (short lists, k > 1)
