@@ -416,6 +416,20 @@ __device__ __forceinline__ void st_coherent_f64(double* p, double v) {
 // Wait until every memory operation this wave issued has completed.
 __device__ __forceinline__ void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
+// r + (a > b) for 64-bit unsigned a and b: the borrow out of b - a, carried
+// into r (three VALU operations through VCC; the compiler's 64-bit compare
+// writes a lane mask that a select then has to read back).
+__device__ __forceinline__ int add_gt_u64(int r, uint64_t a, uint64_t b) {
+  uint32_t t;
+  asm("v_sub_co_u32_e32 %1, vcc, %2, %3\n\t"
+      "v_subb_co_u32_e32 %1, vcc, %4, %5, vcc\n\t"
+      "v_addc_co_u32_e32 %0, vcc, 0, %0, vcc"
+      : "+v"(r), "=&v"(t)
+      : "v"((uint32_t)b), "v"((uint32_t)a), "v"((uint32_t)(b >> 32)), "v"((uint32_t)(a >> 32))
+      : "vcc");
+  return r;
+}
+
 // A read-only value at a uniform address, through the scalar data cache (a
 // load from the constant address space): such loads count apart from the
 // vector loads, which complete in order, so they do not wait behind a slice

@@ -76,7 +76,7 @@ struct SliceSummary {
   double z;          // histogram mass relative to the top edge of bin top_bin
   double zs;         // short-list rows: sum exp((x - x_max) / T_f) over the slice
   int32_t npub;      // short-list rows: published keys (top-k plus ties)
-  int32_t pad;
+  float ylo;         // short-list rows: no published key's value is below it
   uint64_t hist[kHist];
 };
 

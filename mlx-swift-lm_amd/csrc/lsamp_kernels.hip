@@ -41,6 +41,10 @@ constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
 // Fourth word of a raw buffer descriptor on gfx9-family parts (32-bit data
 // format; no swizzle, no stride).
 constexpr int kBufferWord3 = 0x00020000;
+// Buckets of the short-list finalize's counting sort (by a key's high word);
+// their counts and starts live in the thread-maximum histogram.
+constexpr int kRankBuckets = 512;
+static_assert(2 * kRankBuckets <= kTauBins, "bucket counts and starts fit");
 
 enum TaskMode { kFused = 0, kStatsOnly = 1, kSelectOnly = 2 };
 
@@ -727,8 +731,9 @@ constexpr int kSlotsPerLane = kChunk / 64;           // draw slots per lane
 // of kSlotsPerLane with one pad word per run (no bank conflicts).
 __device__ __forceinline__ int draw_slot(int o) { return o + (o >> 4); }
 
+__device__ __forceinline__ uint32_t key_hi(float y) { return ordered_key(y == 0.0f ? 0.0f : y); }
 __device__ __forceinline__ uint64_t cand_key(float y, int32_t id) {
-  return ((uint64_t)ordered_key(y == 0.0f ? 0.0f : y) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+  return ((uint64_t)key_hi(y) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
 }
 
 // What the finalize tail needs besides the sorted candidates in F.keys.
@@ -1322,12 +1327,14 @@ __device__ __forceinline__ bool short_gather(const Workspace& ws, const SamplePl
     int32_t hn = 0, hp = 0;
     uint32_t hf = 0u;
     double hz = 0.0;
+    float hl = kPosInf;
     if (l < G) {
       hx = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&summ[l].x_max)));
       hn = ld_coherent(&summ[l].n_finite);
       hp = ld_coherent(&summ[l].npub);
       hf = ld_coherent(&summ[l].flags);
       hz = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&summ[l].zs)));
+      hl = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&summ[l].ylo)));
     }
     float u = 0.0f;
     int32_t pr = -1;
@@ -1350,6 +1357,11 @@ __device__ __forceinline__ bool short_gather(const Workspace& ws, const SamplePl
     if (l < G) L.soff[l] = ip - hpv;
     if (l == G - 1) L.soff[G] = ip;
     const float y_max = any ? to_filter(c, row_max) : 0.0f;
+    // buckets of the finalize's counting sort: equal widths in value from
+    // the row's largest down to the lowest slice bound
+    const float y_low = wave_min(live && hpv > 0 ? hl : kPosInf);
+    const float span = y_max - y_low;
+    const float bscale = span > 0.0f && span < kPosInf ? (float)kRankBuckets / span : 0.0f;
     // slice s summed exp((x - x_s) / T_f); rescaled to e^y_max
     double z = 0.0;
     if (any && c.kind != LSAMP_KIND_ARGMAX)
@@ -1374,8 +1386,11 @@ __device__ __forceinline__ bool short_gather(const Workspace& ws, const SamplePl
       L.misc[7] = npmax;
       L.misc64[0] = __float_as_uint(u);
       L.misc[4] = pr;
+      L.misc[0] = (int32_t)__float_as_uint(y_max);
+      L.misc[1] = (int32_t)__float_as_uint(bscale);
     }
   }
+  for (int i = tid; i < kRankBuckets; i += kThreads) L.sh.tcnt[i] = 0u;
   __syncthreads();
   if (L.misc[5]) return false;
   if (ks < G && kj < L.soff[ks + 1] - L.soff[ks]) L.ssrc[L.soff[ks] + kj] = kspec;
@@ -1421,7 +1436,66 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   int32_t* racc = reinterpret_cast<int32_t*>(F.dw);  // [n_tot] partial ranks (n_tot <= kCandCap)
   int32_t* rk = racc;
   const int parts = n_tot > 0 && n_tot <= kThreads / 2 ? kThreads / n_tot : 1;
-  if (parts > 1) {
+  if (n_tot <= kThreads) {
+    // counting sort by the key's high word (bucket 0: the largest keys), then
+    // the rank within the bucket: the bucket's start plus its keys above
+    uint32_t* bcnt = L.sh.tcnt;                  // [kRankBuckets], zeroed
+    uint32_t* bstart = L.sh.tcnt + kRankBuckets;  // [kRankBuckets]
+    uint64_t* tmp = reinterpret_cast<uint64_t*>(F.dw);  // keys grouped by bucket
+    const float y_top = __uint_as_float((uint32_t)L.misc[0]);
+    const float bscale = __uint_as_float((uint32_t)L.misc[1]);
+    if (tid == 0) L.misc[6] = n_tot;
+    const bool have = tid < n_tot;
+    uint64_t key = 0ull;
+    int b = 0, slot = 0;
+    if (have) {
+      key = L.ssrc[tid];
+      // (monotone in the key: a larger value never lands in a later bucket)
+      const float d = (y_top - key_y(key)) * bscale;
+      b = d < (float)(kRankBuckets - 1) ? (int)d : kRankBuckets - 1;
+      b = b > 0 ? b : 0;
+      slot = (int)atomicAdd(&bcnt[b], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      constexpr int kPer = kRankBuckets / 64;
+      uint32_t cb[kPer];
+      uint32_t cs = 0u;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        cb[i] = bcnt[kPer * tid + i];
+        cs += cb[i];
+      }
+      uint32_t acc = wave_incl_scan(cs) - cs;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        bstart[kPer * tid + i] = acc;
+        acc += cb[i];
+      }
+    }
+    __syncthreads();
+    int s0 = 0, cnt = 0;
+    if (have) {
+      s0 = (int)bstart[b];
+      cnt = (int)bcnt[b];
+      tmp[s0 + slot] = key;
+    }
+    __syncthreads();
+    if (have) {
+      int r = s0;
+      int j = s0;
+      const int je = s0 + cnt;
+      for (; j + 4 <= je; j += 4) {
+        uint64_t k4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) k4[q] = tmp[j + q];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r = add_gt_u64(r, k4[q], key);
+      }
+      for (; j < je; ++j) r = add_gt_u64(r, tmp[j], key);
+      F.keys[r] = key;
+    }
+  } else if (parts > 1) {
     for (int i = tid; i < n_tot; i += kThreads) racc[i] = 0;
     if (tid == 0) L.misc[6] = n_tot;
     __syncthreads();
@@ -1793,6 +1867,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       // least k tokens at or above it; those few are sorted, and the slice's
       // top-k plus ties is published.
       int32_t npub = 0;
+      float ylo = kNegInf;
       double zsum = 0.0;
       if (has_finite && !ent_overflow) {
         float tau = xmax;  // k = 1: the maximum itself
@@ -1939,6 +2014,8 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
             const int j = tid + __builtin_ctz(ebits) * kThreads;
             st_coherent(&pub[w++], cand_key(to_filter(c, L.ex[j]), L.etok[j]));
           }
+          // a lower bound on the values of the published keys
+          ylo = to_filter(c, tcp);
         }
       }
       if (tid == 0) {
@@ -1948,6 +2025,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         st_coherent(&Ssum->n_finite, (has_finite || posinf) ? 1 : 0);
         st_coherent_f64(&Ssum->zs, zsum);
         st_coherent(&Ssum->npub, npub);
+        st_coherent_f32(&Ssum->ylo, ylo);
       }
       if (MODE == kFused) {
         // first exchange of a short-list row: the last slice to publish
