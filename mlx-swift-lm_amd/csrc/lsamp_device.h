@@ -84,13 +84,31 @@ __device__ __forceinline__ void exclude_elems(uint4& r, uint32_t excl) {
       w[k] = (w[k] & ~m) | (Vec<DT>::NEG_INF_BITS & m);
     }
   } else {
-    constexpr uint32_t pair = Vec<DT>::NEG_INF_BITS * 0x10001u;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t m = ((0u - ((excl >> (2 * k)) & 1u)) & 0xffffu) |
-                         ((0u - ((excl >> (2 * k + 1)) & 1u)) & 0xffff0000u);
-      w[k] = (w[k] & ~m) | (pair & m);
-    }
+    // bits 2k and 2k+1 of `excl` moved to bits 15 and 31 of a word, whose two
+    // halves an arithmetic 16-bit shift turns into masks, then a bitfield
+    // select from the -inf pair (three instructions a word, written out: the
+    // compiler otherwise selects each half apart)
+    const uint32_t pair = Vec<DT>::NEG_INF_BITS * 0x10001u;
+    const uint32_t sp = excl | (excl << 15);  // bit j at j and at j + 15
+    uint32_t m0, m1, m2, m3;
+    // (the 16-bit shift counts are in a register: an inline constant would
+    // reach only the low half)
+    const uint32_t sh = 0x000f000fu;
+    asm("v_lshlrev_b32 %0, 15, %8\n\t"
+        "v_lshlrev_b32 %1, 13, %8\n\t"
+        "v_lshlrev_b32 %2, 11, %8\n\t"
+        "v_lshlrev_b32 %3, 9, %8\n\t"
+        "v_pk_ashrrev_i16 %0, %10, %0\n\t"
+        "v_pk_ashrrev_i16 %1, %10, %1\n\t"
+        "v_pk_ashrrev_i16 %2, %10, %2\n\t"
+        "v_pk_ashrrev_i16 %3, %10, %3\n\t"
+        "v_bfi_b32 %4, %0, %9, %4\n\t"
+        "v_bfi_b32 %5, %1, %9, %5\n\t"
+        "v_bfi_b32 %6, %2, %9, %6\n\t"
+        "v_bfi_b32 %7, %3, %9, %7"
+        : "=&v"(m0), "=&v"(m1), "=&v"(m2), "=&v"(m3), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]),
+          "+v"(w[3])
+        : "v"(sp), "s"(pair), "s"(sh));
   }
 }
 

@@ -319,6 +319,18 @@ struct EntryMarks {
   float xr[kEntPrefetch];
 };
 
+// Wave-aggregated append to an LDS list: returns this lane's slot or -1.
+__device__ __forceinline__ int wave_append(bool pred, int32_t* counter) {
+  const uint64_t m = __ballot(pred);
+  if (m == 0ull) return -1;
+  const int lane = threadIdx.x & 63;
+  const int leader = __ffsll((unsigned long long)m) - 1;
+  int b = 0;
+  if (lane == leader) b = atomicAdd(counter, (int)__popcll(m));
+  b = __shfl(b, leader, 64);
+  return pred ? b + (int)__popcll(m & ((1ull << lane) - 1ull)) : -1;
+}
+
 template <int DT>
 __device__ __forceinline__ float patched_entry(const SamplePlan& P, const RowCtx& c,
                                                const lsamp_row_params& prm, const uint32_t* mrow,
@@ -342,13 +354,19 @@ __device__ __forceinline__ void mark_slice_entries(const SamplePlan& P, const Ro
     atomicOr(&se.pen[li >> 5], 1u << (li & 31));
     return atomicAdd(se.count, 1);
   };
-  // (the gather is unconditional, from the slice's first token when there
-  // is no entry, so that nothing waits for it before it is used)
+  // The prefetched entries take their slots a wave at a time (one counter
+  // update per wave, not one per entry); their gather is unconditional, from
+  // the slice's first token when there is no entry, so that nothing waits
+  // for it before it is used.
 #pragma unroll
   for (int k = 0; k < kEntPrefetch; ++k) {
     const int32_t t = ep.ent[k].token;
     const bool in = ep.has(tid, k) && t >= base && t < end;
-    em.slot[k] = in ? mark(t) : -1;
+    if (in) {
+      const int32_t li = t - (int32_t)base;
+      atomicOr(&se.pen[li >> 5], 1u << (li & 31));
+    }
+    em.slot[k] = wave_append(in, se.count);
     em.xr[k] = load_scalar<DT>(rowp, in ? t : base);
   }
   // the rest of a long history
@@ -443,17 +461,6 @@ struct TaskLds {
   uint32_t flags;
 };
 
-// Wave-aggregated append to an LDS list: returns this lane's slot or -1.
-__device__ __forceinline__ int wave_append(bool pred, int32_t* counter) {
-  const uint64_t m = __ballot(pred);
-  if (m == 0ull) return -1;
-  const int lane = threadIdx.x & 63;
-  const int leader = __ffsll((unsigned long long)m) - 1;
-  int b = 0;
-  if (lane == leader) b = atomicAdd(counter, (int)__popcll(m));
-  b = __shfl(b, leader, 64);
-  return pred ? b + (int)__popcll(m & ((1ull << lane) - 1ull)) : -1;
-}
 
 __device__ __forceinline__ int32_t key_id(uint64_t key) {
   return (int32_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
@@ -1680,35 +1687,52 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   const int nq = (P.slice_len + kThreads * N - 1) / (kThreads * N);  // quads per thread
 
   // ---------------------------------------------------- A: loads + entries
-  // The slice's logits are requested first, as 16-byte vectors all in flight
-  // at once, through one buffer descriptor over the slice: the lane's byte
-  // offset is fixed and the quad's is a scalar, and lanes past the slice end
-  // read as zero (range check) until the exclusion pass.
-  Slab<DT> S;
-  if (aligned) {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char*>(rowp) + (size_t)base32 * ES, 0, (end32 - base32) * ES, kBufferWord3);
-    const int lane_off = tid * 16;
-#pragma unroll
-    for (int g = 0; g < Q; ++g) {
-      if (g < nq) {
-        const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, g * kThreads * 16, 0);
-        quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, make_uint4(w[0], w[1], w[2], w[3]));
-      }
-    }
-  } else {
-#pragma unroll
-    for (int g = 0; g < Q; ++g)
-      if (g < nq) quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, make_uint4(0u, 0u, 0u, 0u));
-  }
-  // the row's parameters (scalar loads) and its first penalty entries
+  // The row's parameters and the CSR bounds of its penalty entries come
+  // through scalar loads; the first entries are requested ahead of the
+  // slice's logits (vector loads complete in order), so the entry bitmap is
+  // built while the slice streams in and the pass over the slice starts on
+  // each quad as it lands.
   const lsamp_row_params prm = load_params(P, row);
   const RowCtx c = make_ctx(P.semantics, prm);
   const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
   EntryPrefetch ep;
   prefetch_entries(P, row, tid, ep);
+  // The slice's logits: 16-byte vectors all in flight at once, through one
+  // buffer descriptor over the slice (the lane's byte offset is fixed and
+  // the quad's is a scalar; lanes past the slice end read as zero, by the
+  // range check, until the exclusion pass).
+  Slab<DT> S;
+  {
+    // (an unaligned row gets an empty range, so every load reads zero and
+    // the element-by-element path fills the slab in; the loads are issued
+    // either way, which keeps later waits exact)
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(rowp) + (size_t)base32 * ES, 0, aligned ? (end32 - base32) * ES : 0,
+        kBufferWord3);
+    const int lane_off = tid * 16;
+    // (every quad of the slab, without a branch: quads past the slice read
+    // zero, and straight-line loads let each later wait name its own quad)
+#pragma unroll
+    for (int g = 0; g < Q; ++g) {
+      const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, g * kThreads * 16, 0);
+      quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+  }
+  if (MODE != kSelectOnly) {
+    for (int i = tid; i < kHist; i += kThreads) L.u.hist[i] = 0ull;
+    for (int i = tid; i < kTauBins; i += kThreads) L.sh.tcnt[i] = 0u;
+  }
+  if (tid == 0) {
+    L.flags = 0u;
+    L.ncand = 0;
+  }
+  SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
+  EntryMarks em;
+  float emax = kNegInf;  // this thread's patched entry values
+  mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
   if (!aligned || (end32 & (N - 1)) != 0) {
     // unaligned rows, or the row's last partial quad: element by element
+    // (after the entry bitmap, whose wait these loads would otherwise delay)
     for_quads(S, nq, [&](int g, uint4& v) -> bool {
       const int32_t i0 = base32 + (tid + g * kThreads) * N;
       if (i0 >= end32 || (aligned && i0 + N <= end32)) return false;
@@ -1724,18 +1748,6 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       return true;
     });
   }
-  if (MODE != kSelectOnly) {
-    for (int i = tid; i < kHist; i += kThreads) L.u.hist[i] = 0ull;
-    for (int i = tid; i < kTauBins; i += kThreads) L.sh.tcnt[i] = 0u;
-  }
-  if (tid == 0) {
-    L.flags = 0u;
-    L.ncand = 0;
-  }
-  SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
-  EntryMarks em;
-  float emax = kNegInf;  // this thread's patched entry values
-  mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
 
   // Masked tokens, tokens of the entry table (their patched values live in
   // L.ex) and lanes past the slice end become -inf in the register copy, and
@@ -1773,7 +1785,8 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     const uint32_t tail = ~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem));
     uint32_t ex = ((pcur >> pen_shift) | tail) & FULL;
     if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
-    // (two branches: a wave meets an entry token in most quads, a NaN rarely)
+    // (NaNs are rare, behind a branch; entry tokens are in most quads of a
+    // wave, so the exclusion runs unconditionally, a no-op without bits)
     if (nonfinite_seen<DT>(probe)) {
 #pragma unroll
       for (int e = 0; e < N; ++e) {
@@ -1781,7 +1794,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         if (x != x) ex |= 1u << e;
       }
     }
-    if (ex != 0u) exclude_elems<DT>(v, ex);
+    exclude_elems<DT>(v, ex);
     if (MODE != kSelectOnly) {
       const float qm = vec_max_nn<DT>(v);  // NaNs are excluded by now
       xmax = __builtin_elementwise_maximum(xmax, qm);
