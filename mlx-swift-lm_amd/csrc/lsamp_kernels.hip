@@ -44,6 +44,10 @@ constexpr int kBufferWord3 = 0x00020000;
 // Buckets of the short-list finalize's counting sort (by a key's high word);
 // their counts and starts live in the thread-maximum histogram.
 constexpr int kRankBuckets = 512;
+// The publish's LDS list holds at most kShortPub raw pairs; threads write the
+// tokens that are not candidates to their own slot from here on.
+constexpr int kExpandDump = kShortPub;
+static_assert(kExpandDump + kThreads <= kCandCap, "dump slots fit the list area");
 static_assert(2 * kRankBuckets <= kTauBins, "bucket counts and starts fit");
 
 enum TaskMode { kFused = 0, kStatsOnly = 1, kSelectOnly = 2 };
@@ -1234,13 +1238,19 @@ __device__ __forceinline__ void short_tail(const Workspace& ws, const SamplePlan
     if (k_lim > 0 && l >= k_lim) keep_p = false;
   }
   const int32_t surv = (in && keep_p && keep_m) ? 1 : 0;
-  const int32_t is = wave_incl_scan(surv);
   bool keep = surv != 0;
-  if (keep && mlx && k_lim > 0) keep = (is - 1) < k_lim;
-  const int32_t ik = wave_incl_scan(keep ? 1 : 0);
-  const int32_t kept_c = read_lane(ik, 63);
+  int32_t ik, kept_c;  // this lane's place among the kept (1-based), their count
+  if (mlx) {
+    const int32_t is = wave_incl_scan(surv);
+    if (keep && k_lim > 0) keep = (is - 1) < k_lim;
+    ik = wave_incl_scan(keep ? 1 : 0);
+    kept_c = read_lane(ik, 63);
+  } else {
+    // each rule keeps a prefix of the sorted candidates, so the kept are one
+    kept_c = (int32_t)__popcll(__ballot(keep));
+    ik = l + 1;
+  }
   const uint64_t w = keep ? weight(y, y_max, c.scale) : 0ull;
-  const uint64_t W = wave_sum(w);
   // the kept tokens in id order (each kept lane counts the kept ids below
   // its own), then a running sum: the token is the one whose run crosses the
   // target
@@ -1266,14 +1276,19 @@ __device__ __forceinline__ void short_tail(const Workspace& ws, const SamplePlan
   const uint64_t wo = l < kept_c ? F.dw[l] : 0ull;
   const int32_t io = l < kept_c ? sid2[l] : -1;
   const uint64_t cum = wave_incl_scan(wo);
+  const uint64_t W = read_lane(cum, 63);  // the kept weights, in any order
   const uint64_t target = W ? scaled_target(uniform_u32(u_draw), W) : 0ull;
   const uint64_t hm = __ballot(wo != 0ull && cum > target && cum - wo <= target);
   const int32_t token = hm ? read_lane(io, __builtin_ctzll(hm)) : -1;
   const uint64_t hp = __ballot(keep && probe >= 0 && id == probe);
   const uint64_t probe_w = hp ? read_lane(w, __builtin_ctzll(hp)) : 0ull;
-  const double cent =
-      wave_sum(keep ? (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale) : 0.0);
-  const float cmin = wave_min(keep ? y : kPosInf);
+  double cent = 0.0;  // statistics only
+  float cmin = kPosInf;
+  if (P.stats) {
+    cent = wave_sum(keep ? (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale)
+                         : 0.0);
+    cmin = wave_min(keep ? y : kPosInf);
+  }
   // kept candidates persist, in key order, for the MTP residual pass
   Candidate* rc = ws.cands + (size_t)row * kCandCap;
   if (keep) {
@@ -2009,23 +2024,47 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         if (n > kShortPub) {
           sflags |= kSliceShortOverflow;
         } else {
-          // every candidate is published (unsorted); the finalize ranks them
+          // every candidate is published (unsorted; the finalize ranks them):
+          // each thread lists its raw (value, id) pairs in LDS, then thread j
+          // forms key j (one division per thread, not a wave's worth of
+          // serial ones) and stores it
           npub = n;
           uint64_t* pub = reinterpret_cast<uint64_t*>(ws.cands + (size_t)row * kCandCap) +
-                          (size_t)slice * kShortPub + off;
-          int w = 0;
-          for (int k = 0; k < qn; ++k) {
-            const uint4 v = sq[k * kThreads];
-            const int32_t i0 = base32 + (tid + (int)((qids >> (5 * k)) & 31u) * kThreads) * N;
+                          (size_t)slice * kShortPub;
+          uint64_t* lst = L.ssrc;  // [n] raw pairs: value bits << 32 | id
+          auto raw = [](float x, int32_t id) {
+            return ((uint64_t)__float_as_uint(x) << 32) | (uint64_t)(uint32_t)id;
+          };
+          // (the staged quads are read at once; a token that is not a
+          // candidate writes to this thread's own slot past the list, so
+          // the expansion does not branch per token)
+          int w = off;
+          uint4 sv[kQStage];
 #pragma unroll
-            for (int e = 0; e < N; ++e) {
-              const float x = vec_elem<DT>(v, e);
-              if (x >= tcp) st_coherent(&pub[w++], cand_key(to_filter(c, x), i0 + e));
+          for (int k = 0; k < kQStage; ++k) sv[k] = sq[k * kThreads];
+          const int dump = kExpandDump + tid;
+#pragma unroll
+          for (int k = 0; k < kQStage; ++k) {
+            if (k < qn) {
+              const int32_t i0 = base32 + (tid + (int)((qids >> (5 * k)) & 31u) * kThreads) * N;
+#pragma unroll
+              for (int e = 0; e < N; ++e) {
+                const float x = vec_elem<DT>(sv[k], e);
+                const bool hit = x >= tcp;
+                lst[hit ? w : dump] = raw(x, i0 + e);
+                w += hit ? 1 : 0;
+              }
             }
           }
           for (; ebits != 0u; ebits &= ebits - 1u) {
             const int j = tid + __builtin_ctz(ebits) * kThreads;
-            st_coherent(&pub[w++], cand_key(to_filter(c, L.ex[j]), L.etok[j]));
+            lst[w++] = raw(L.ex[j], L.etok[j]);
+          }
+          lds_barrier();
+          for (int j = tid; j < n; j += kThreads) {
+            const uint64_t r = lst[j];
+            st_coherent(&pub[j], cand_key(to_filter(c, __uint_as_float((uint32_t)(r >> 32))),
+                                          (int32_t)(uint32_t)r));
           }
           // a lower bound on the values of the published keys
           ylo = to_filter(c, tcp);
