@@ -203,14 +203,11 @@ __device__ __forceinline__ float load_logit(int dt, const char* rowp, int64_t i)
   return load_scalar<LSAMP_DTYPE_F16>(rowp, i);
 }
 
-// The row's parameters, as two 16-byte scalar loads.
+// The row's parameters, as one 32-byte scalar load.
 __device__ __forceinline__ lsamp_row_params load_params(const SamplePlan& P, int row) {
   static_assert(sizeof(lsamp_row_params) == 32, "two 16-byte words");
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4* w = reinterpret_cast<const u32x4*>(P.params + params_index(P, row));
-  struct {
-    u32x4 a, b;
-  } raw = {load_uniform(w), load_uniform(w + 1)};
+  typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+  const u32x8 raw = load_uniform(reinterpret_cast<const u32x8*>(P.params + params_index(P, row)));
   return __builtin_bit_cast(lsamp_row_params, raw);
 }
 
@@ -291,15 +288,23 @@ struct EntryPrefetch {
   __device__ bool has(int tid, int k) const { return e0 + tid + k * kThreads < e1; }
 };
 
-__device__ __forceinline__ void prefetch_entries(const SamplePlan& P, int row, int tid,
-                                                 EntryPrefetch& ep) {
-  static_assert(sizeof(lsamp_penalty_entry) == 16, "one 16-byte load per entry");
+// The row's CSR bounds (scalar loads; the row's parameters are requested
+// just before, so that both arrive in one round).
+__device__ __forceinline__ void entry_bounds(const SamplePlan& P, int row, EntryPrefetch& ep) {
   ep.e0 = 0;
   ep.e1 = 0;
   if (P.row_ptr && P.entries) {
-    ep.e0 = load_uniform(P.row_ptr + row);
-    ep.e1 = load_uniform(P.row_ptr + row + 1);
+    // (one laundered address for both words: see load_uniform)
+    uint64_t a = (uint64_t)(P.row_ptr + row);
+    asm volatile("" : "+s"(a));
+    const __attribute__((address_space(4))) int32_t* q = (const __attribute__((address_space(4))) int32_t*)a;
+    ep.e0 = q[0];
+    ep.e1 = q[1];
   }
+}
+
+__device__ __forceinline__ void prefetch_entries(const SamplePlan& P, int tid, EntryPrefetch& ep) {
+  static_assert(sizeof(lsamp_penalty_entry) == 16, "one 16-byte load per entry");
   // one buffer descriptor over the row's entries: lanes past them read zero,
   // and no branch holds a load back
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -1708,10 +1713,11 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   // built while the slice streams in and the pass over the slice starts on
   // each quad as it lands.
   const lsamp_row_params prm = load_params(P, row);
+  EntryPrefetch ep;
+  entry_bounds(P, row, ep);
   const RowCtx c = make_ctx(P.semantics, prm);
   const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
-  EntryPrefetch ep;
-  prefetch_entries(P, row, tid, ep);
+  prefetch_entries(P, tid, ep);
   // The slice's logits: 16-byte vectors all in flight at once, through one
   // buffer descriptor over the slice (the lane's byte offset is fixed and
   // the quad's is a scalar; lanes past the slice end read as zero, by the
@@ -2406,12 +2412,38 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
 }
 
 // ================================================================ kernels
-template <int DT>
-__global__ __launch_bounds__(kThreads) void k_fused(Workspace ws, SamplePlan P) {
+// A copy of a kernel argument whose every dword went through an SGPR as an
+// opaque value: all of its scalar loads are issued together, and none is
+// repeated later.
+template <typename T>
+__device__ __forceinline__ T in_sgprs(const T& v) {
+  constexpr int kW = (int)((sizeof(T) + 3) / 4);
+  uint32_t w[kW];
+  __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+  for (int i = 0; i < kW; ++i) asm volatile("" : "+s"(w[i]));
+  T out;
+  __builtin_memcpy(&out, w, sizeof(T));
+  return out;
+}
+
+// ONE: every row fits one round of the grid (no loop over rounds, so nothing
+// is hoisted out of one and spilled before the first load).
+template <int DT, bool ONE>
+__global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk) {
   __shared__ TaskLds L;
+  // The kernel arguments are read in one round of scalar loads and held as
+  // opaque values (otherwise they are fetched lazily, over several dependent
+  // rounds, before the first global load can be issued).
+  const Workspace ws = in_sgprs(wsk);
+  const SamplePlan P = in_sgprs(Pk);
   const int G = P.slices;
   const int rowslot = (int)blockIdx.x / G;
   const int slice = (int)blockIdx.x % G;
+  if (ONE) {
+    if (rowslot < P.rows) run_task<DT, kFused>(ws, P, rowslot, slice, L);
+    return;
+  }
   for (int r0 = 0; r0 < P.rows; r0 += P.rows_per_round) {
     const int row = r0 + rowslot;
     if (row < P.rows) run_task<DT, kFused>(ws, P, row, slice, L);
@@ -2439,7 +2471,8 @@ int launch_dt(const Workspace& ws, const SamplePlan& P, hipStream_t st, void* co
   mark(0);
   if (P.fused) {
     const int rounds_rows = P.rows < P.rows_per_round ? P.rows : P.rows_per_round;
-    hipLaunchKernelGGL(k_fused<DT>, dim3((unsigned)(rounds_rows * P.slices)), dim3(kThreads), 0, st,
+    auto kf = P.rows <= P.rows_per_round ? k_fused<DT, true> : k_fused<DT, false>;
+    hipLaunchKernelGGL(kf, dim3((unsigned)(rounds_rows * P.slices)), dim3(kThreads), 0, st,
                        ws, P);
     mark(1);
   } else {
@@ -2646,13 +2679,13 @@ int fused_blocks_per_cu(int dtype) {
   hipError_t e;
   switch (dtype) {
     case LSAMP_DTYPE_F32:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_F32>, kThreads, 0);
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_F32, false>, kThreads, 0);
       break;
     case LSAMP_DTYPE_BF16:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_BF16>, kThreads, 0);
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_BF16, false>, kThreads, 0);
       break;
     default:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_F16>, kThreads, 0);
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_F16, false>, kThreads, 0);
       break;
   }
   return e == hipSuccess ? n : 0;
