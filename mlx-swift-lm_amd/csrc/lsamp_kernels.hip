@@ -1438,7 +1438,12 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   const int64_t V = P.vocab;
   FinalLds& F = L.u.f;
   const uint64_t* pub = reinterpret_cast<const uint64_t*>(ws.cands + (size_t)row * kCandCap);
-  if (P.fused && tid == 64) short_depart(ws, row, G);  // overlaps the rest
+  // the departure ticket is taken now and checked at the end, so its round
+  // trip overlaps the rest (the barriers below order LDS only, not memory)
+  uint32_t ticket = 0u;
+  if (P.fused && tid == 64)
+    ticket = __hip_atomic_fetch_add(&ws.arrive_select[row], 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
   const int n_tot = L.soff[G];
   const int npmax = L.misc[7];
   if (npmax > 64) {
@@ -1454,8 +1459,10 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
     // the row is dropped
     uint8_t* kr = P.keep + (size_t)row * (size_t)V;
     for (int64_t i = tid; i < V; i += kThreads) kr[i] = 0;
+    __syncthreads();  // (these stores land before the tail's)
+  } else {
+    lds_barrier();
   }
-  __syncthreads();
   // rank of each key in the union (keys are distinct: token ids are): the
   // keys above it.  The comparisons of a key are split over `parts` threads
   // (the whole work-group works), each reading its share of the keys 16 at a
@@ -1483,7 +1490,7 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
       b = b > 0 ? b : 0;
       slot = (int)atomicAdd(&bcnt[b], 1u);
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < 64) {
       constexpr int kPer = kRankBuckets / 64;
       uint32_t cb[kPer];
@@ -1500,14 +1507,14 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
         acc += cb[i];
       }
     }
-    __syncthreads();
+    lds_barrier();
     int s0 = 0, cnt = 0;
     if (have) {
       s0 = (int)bstart[b];
       cnt = (int)bcnt[b];
       tmp[s0 + slot] = key;
     }
-    __syncthreads();
+    lds_barrier();
     if (have) {
       int r = s0;
       int j = s0;
@@ -1525,7 +1532,7 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   } else if (parts > 1) {
     for (int i = tid; i < n_tot; i += kThreads) racc[i] = 0;
     if (tid == 0) L.misc[6] = n_tot;
-    __syncthreads();
+    lds_barrier();
     const int i = tid % n_tot, part = tid / n_tot;
     if (part < parts) {
       const uint64_t key = L.ssrc[i];
@@ -1542,7 +1549,7 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
       for (; j < j1; ++j) r += L.ssrc[j] > key ? 1 : 0;
       atomicAdd(&racc[i], r);
     }
-    __syncthreads();
+    lds_barrier();
     for (int i2 = tid; i2 < n_tot; i2 += kThreads) F.keys[rk[i2]] = L.ssrc[i2];
   } else {
     if (tid == 0) L.misc[6] = n_tot;
@@ -1561,7 +1568,7 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
       F.keys[r] = key;
     }
   }
-  __syncthreads();
+  lds_barrier();
   // the row's top-k and every token tied with the k-th: the first position
   // past K - 1 whose value is below the k-th's
   if (n_tot > K) {
@@ -1569,8 +1576,14 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
     for (int i = K + tid; i < n_tot; i += kThreads)
       if ((uint32_t)(F.keys[i] >> 32) < kv && (uint32_t)(F.keys[i - 1] >> 32) >= kv) L.misc[6] = i;
   }
-  __syncthreads();
-  if (!wave0) return;
+  lds_barrier();
+  if (!wave0) {
+    if (P.fused && tid == 64 && ticket + 1u == (uint32_t)G) {
+      st_coherent(&ws.arrive_stats[row], 0u);
+      st_coherent(&ws.arrive_select[row], 0u);
+    }
+    return;
+  }
   int nc = L.misc[6];
   const RowInfo info = L.info;
   if (info.mode != kModeNormal) nc = 0;
