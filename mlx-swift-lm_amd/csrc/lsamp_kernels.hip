@@ -1797,6 +1797,10 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   // penalty-bitmap word of quad g (the bitmap is zeroed over the largest
   // slice, so every quad's word is in bounds); fetched one quad ahead so the
   // LDS read overlaps the current quad
+  // the quad maxima, kept for the screening pass (16-bit types: they fill
+  // the short list's LDS area, which is idle until the publish)
+  constexpr bool kKeepQm = Q * kThreads * sizeof(float) <= sizeof(L.ssrc);
+  float* qmc = reinterpret_cast<float*>(L.ssrc);
   const uint32_t* penw = L.pen + ((tid * N) >> 5);
   constexpr int kQuadWords = kThreads * N / 32;  // bitmap words per quad row
   const uint32_t pen_shift = (uint32_t)((tid * N) & 31);
@@ -1831,6 +1835,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     exclude_elems<DT>(v, ex);
     if (MODE != kSelectOnly) {
       const float qm = vec_max_nn<DT>(v);  // NaNs are excluded by now
+      if constexpr (kKeepQm) qmc[g * kThreads + tid] = qm;
       xmax = __builtin_elementwise_maximum(xmax, qm);
       if (zon) {
         // re-anchor when the quad's terms could pass 2^64 (an exact power-of-
@@ -1986,8 +1991,15 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         uint4* sq = L.sh.squad + tid;
         int qn = 0, cnt = 0;
         uint32_t qids = 0u;  // staged quad numbers, 5 bits per slot
+        // (the kept quad maxima are read into registers at once: the
+        // staging stores below would otherwise hold each read back)
+        float qv[Q];
+        if constexpr (kKeepQm) {
+#pragma unroll
+          for (int g = 0; g < Q; ++g) qv[g] = qmc[g * kThreads + tid];
+        }
         for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
-          if (vec_max_nn<DT>(v) >= tcp) {
+          if ((kKeepQm ? qv[g] : vec_max_nn<DT>(v)) >= tcp) {
 #pragma unroll
             for (int e = 0; e < N; ++e) cnt += vec_elem<DT>(v, e) >= tcp ? 1 : 0;
             const int slot = qn < kQStage ? qn : kQStage;
@@ -1997,15 +2009,17 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
           }
           return false;
         });
-        // the entry table's order depends on atomics: its terms are summed
-        // in fixed point (exact in any order), so the slice's sum is the
-        // same in every run and in both kernel arrangements
+        // The slice's sum is kept in 2^40 fixed point (exact in any order):
+        // the entry table's order depends on atomics, and the sum must be
+        // the same in every run and in both kernel arrangements.  The entry
+        // terms carry nb's rounding error back as a factor.
+        const float enb = __builtin_amdgcn_exp2f(nb_err);
         uint64_t ze = 0ull;
         uint32_t ebits = 0u;  // bit k: entry tid + k * kThreads is a candidate
         for (int j = tid, k = 0; j < n_ent; j += kThreads, ++k) {
           const float x = L.ex[j];
           if (!(x > kNegInf)) continue;
-          if (zon) ze += (uint64_t)(__builtin_amdgcn_exp2f(__builtin_fmaf(x, lgz, nb)) * 0x1p40f);
+          if (zon) ze += (uint64_t)(__builtin_amdgcn_exp2f(__builtin_fmaf(x, lgz, nb)) * enb * 0x1p40f);
           if (x >= tcp) {
             ebits |= 1u << k;
             ++cnt;
@@ -2019,27 +2033,23 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         const float bh = xmax * lgz;
         const float bl = __builtin_fmaf(xmax, lgz, -bh);
         const float zr = (zon && zref) ? zt * __builtin_amdgcn_exp2f((-nbz - bh) - bl) : 0.0f;
-        double zd = wave_sum((double)zr);
+        // (each term is at most 1, so zr <= 128; out-of-range rows fall back)
+        ze += zr < 0x1p20f ? (uint64_t)(zr * 0x1p40f) : 0ull;
         ze = wave_sum(ze);
         const int wv = tid >> 6;
         __syncthreads();
-        if ((tid & 63) == 0) {
-          L.redd[wv] = zd;
-          L.redu[wv] = ze;
-        }
+        if ((tid & 63) == 0) L.redu[wv] = ze;
         if ((tid & 63) == 63) L.redi[wv] = ci;
         __syncthreads();
-        zd = 0.0;
         ze = 0ull;
         int n = 0, off = ci - cw;
 #pragma unroll
         for (int i = 0; i < kWaves; ++i) {
-          zd += L.redd[i];
           ze += L.redu[i];
           off += i < wv ? L.redi[i] : 0;
           n += L.redi[i];
         }
-        zsum = zd + (double)ze * 0x1p-40 * (double)__builtin_amdgcn_exp2f(nb_err);
+        zsum = (double)ze * 0x1p-40;
         if (n > kShortPub) {
           sflags |= kSliceShortOverflow;
         } else {
