@@ -106,6 +106,8 @@ typedef enum lsamp_mask_tail {
 #define LSAMP_ROW_EMPTY 2u     /* no token survived masking; token = -1       */
 #define LSAMP_ROW_OVERFLOW 4u  /* the cut bucket held more candidates than the
                                   context's candidate capacity; token = -1   */
+#define LSAMP_ROW_TOKEN_RANGE 8u /* lsamp_logprobs: the row's token lies outside
+                                    [0, vocab); its log-probability is NaN  */
 
 /* ---- per-row inputs ------------------------------------------------------- */
 
@@ -276,6 +278,50 @@ lsamp_status lsamp_context_last_launch(lsamp_context* ctx, lsamp_launch_info* ou
 
 /* Enqueue one MTP verification on `stream`. */
 lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* args, void* stream);
+
+/* ---- ranking of raw logits: exact top-2 and log-probabilities -------------
+ * Both calls read a row's logits once (one kernel) and order tokens as the
+ * reference's shared top-2 reduction does (CBv2TopTwo.swift:29-47): value
+ * descending, token id ascending on exact ties (+0 and -0 tie), NaN last.
+ * Strides are in elements and may describe any view (rows may overlap). */
+typedef struct lsamp_top2_args {
+  int32_t rows;       /* >= 1, <= the context's max_rows                       */
+  int32_t vocab;      /* >= 2                                                  */
+  int32_t dtype;      /* lsamp_dtype                                           */
+  int64_t row_stride; /* elements between rows (>= 0)                          */
+  int64_t col_stride; /* elements between tokens (>= 1; 1 = contiguous)        */
+  const void* logits;
+  int32_t* ids;       /* [rows, 2] out                                         */
+  float* values;      /* [rows, 2] out: the logits converted to float32
+                         (exact; NaN stays NaN)                                */
+} lsamp_top2_args;
+
+/* cbv2TopTwoRows (CBv2TopTwo.swift:191-212): ids and values of the two best
+ * tokens of every row. */
+lsamp_status lsamp_top2(lsamp_context* ctx, const lsamp_top2_args* args, void* stream);
+
+typedef struct lsamp_logprobs_args {
+  int32_t rows;       /* >= 1, <= the context's max_rows                       */
+  int32_t vocab;      /* >= 1                                                  */
+  int32_t dtype;      /* lsamp_dtype                                           */
+  int64_t row_stride; /* elements between rows (>= 0)                          */
+  int64_t col_stride; /* elements between tokens (>= 1)                        */
+  const void* logits; /* RAW logits: before bias, penalties, temperature, mask */
+  int32_t top_k;      /* 0 .. 32, <= vocab                                     */
+  const int32_t* tokens; /* [rows] the sampled tokens, or NULL                 */
+  float* chosen;      /* [rows] out (required with tokens): logprob of tokens[r] */
+  float* top_values;  /* [rows, top_k] out: the top_k log-probabilities       */
+  int32_t* top_ids;   /* [rows, top_k] out: their token ids                    */
+  uint32_t* row_flags;/* [rows] out or NULL: LSAMP_ROW_NONFINITE, _TOKEN_RANGE */
+} lsamp_logprobs_args;
+
+/* Log-probabilities of the raw logits, x - logsumexp(x) in float32
+ * (LogitsPipelineV2.process :307-314, Evaluate.swift:800-806), gathered for
+ * the sampled token and the top_k best tokens (CBv2Logprobs.gather,
+ * LogitsPipelineV2.swift:534-549; DeferredTokenLogProbabilities,
+ * Evaluate.swift:818-853).  The log-sum-exp is NaN when a logit is NaN,
+ * +inf when one is +inf, -inf when all are -inf. */
+lsamp_status lsamp_logprobs(lsamp_context* ctx, const lsamp_logprobs_args* args, void* stream);
 
 /* ---- host-side parameter resolution (no device work) ---------------------- */
 

@@ -91,6 +91,43 @@ void plan_slices(int32_t rows, int32_t vocab, int32_t slots, int32_t* slices, in
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Slice option of a ranking launch: the smallest slices (more work-groups)
+// that keep a row within kRankMaxSlices slices and the grid within about two
+// work-groups per CU.
+void plan_rank(int32_t rows, int32_t vocab, int32_t cus, int32_t* option, int32_t* slices) {
+  int32_t o = 0;
+  for (; o < kRankOptions - 1; ++o) {
+    const int32_t g = (vocab + rank_slice_len(o) - 1) / rank_slice_len(o);
+    if (g <= kRankMaxSlices && (int64_t)rows * g <= 2 * (int64_t)cus) break;
+  }
+  *option = o;
+  *slices = (vocab + rank_slice_len(o) - 1) / rank_slice_len(o);
+}
+
+// Shared checks and launch of lsamp_top2 / lsamp_logprobs.
+lsamp_status rank_common(lsamp_context* ctx, RankPlan& P, int32_t min_vocab, void* stream) {
+  if (P.dtype != LSAMP_DTYPE_F32 && P.dtype != LSAMP_DTYPE_BF16 && P.dtype != LSAMP_DTYPE_F16)
+    return fail(LSAMP_ERR_DTYPE, "unsupported dtype %d", P.dtype);
+  if (P.rows <= 0 || P.rows > ctx->ws.max_rows)
+    return fail(P.rows <= 0 ? LSAMP_ERR_SHAPE : LSAMP_ERR_CAPACITY, "rows %d outside [1, %d]",
+                P.rows, ctx->ws.max_rows);
+  if (P.vocab < min_vocab || P.vocab > ctx->ws.max_vocab)
+    return fail(P.vocab < min_vocab ? LSAMP_ERR_SHAPE : LSAMP_ERR_CAPACITY,
+                "vocab %d outside [%d, %d]", P.vocab, min_vocab, ctx->ws.max_vocab);
+  if (P.row_stride < 0 || P.col_stride < 1)
+    return fail(LSAMP_ERR_SHAPE, "row_stride %lld / col_stride %lld invalid",
+                (long long)P.row_stride, (long long)P.col_stride);
+  if (!P.logits) return fail(LSAMP_ERR_INVALID_ARGUMENT, "logits is NULL");
+  const size_t es = P.dtype == LSAMP_DTYPE_F32 ? 4 : 2;
+  P.vec = P.col_stride == 1 && aligned16(P.logits) && ((size_t)P.row_stride * es) % 16 == 0;
+  plan_rank(P.rows, P.vocab, ctx->cus, &P.option, &P.slices);
+  DeviceGuard guard(ctx->device);
+  const int err = launch_rank(ctx->ws, P, stream);
+  if (err != 0)
+    return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -109,6 +146,8 @@ int64_t lsamp_abi_sizeof(const char* name) {
   if (!strcmp(name, "lsamp_generate_parameters")) return (int64_t)sizeof(lsamp_generate_parameters);
   if (!strcmp(name, "lsamp_cbv2_params")) return (int64_t)sizeof(lsamp_cbv2_params);
   if (!strcmp(name, "lsamp_launch_info")) return (int64_t)sizeof(lsamp_launch_info);
+  if (!strcmp(name, "lsamp_top2_args")) return (int64_t)sizeof(lsamp_top2_args);
+  if (!strcmp(name, "lsamp_logprobs_args")) return (int64_t)sizeof(lsamp_logprobs_args);
   return -1;
 }
 
@@ -149,6 +188,8 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   const size_t o_vstats = take(R * sizeof(lsamp_row_stats));
   const size_t o_vtok = take(R * sizeof(int32_t));
   const size_t o_vfl = take(R * sizeof(uint32_t));
+  const size_t o_rpart = take(R * kRankMaxSlices * sizeof(RankSlice));
+  const size_t o_arank = take(R * sizeof(uint32_t));
   const size_t total = off;
 
   void* block = nullptr;
@@ -184,6 +225,8 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   ws.vstats = reinterpret_cast<lsamp_row_stats*>(b + o_vstats);
   ws.vtokens = reinterpret_cast<int32_t*>(b + o_vtok);
   ws.vflags = reinterpret_cast<uint32_t*>(b + o_vfl);
+  ws.rank_part = reinterpret_cast<RankSlice*>(b + o_rpart);
+  ws.arrive_rank = reinterpret_cast<uint32_t*>(b + o_arank);
   *out = ctx;
   return ok();
 }
@@ -351,6 +394,53 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
   if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                             hipGetErrorString((hipError_t)err));
   return ok();
+}
+
+lsamp_status lsamp_top2(lsamp_context* ctx, const lsamp_top2_args* a, void* stream) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (!a->ids || !a->values) return fail(LSAMP_ERR_INVALID_ARGUMENT, "ids and values are required");
+  RankPlan P{};
+  P.rows = a->rows;
+  P.vocab = a->vocab;
+  P.dtype = a->dtype;
+  P.k = 2;
+  P.row_stride = a->row_stride;
+  P.col_stride = a->col_stride;
+  P.lse = 0;
+  P.raw_values = 1;
+  P.logits = a->logits;
+  P.ids = a->ids;
+  P.values = a->values;
+  // precondition(rows > 0 && vocabularySize >= 2), CBv2TopTwo.swift:195
+  return rank_common(ctx, P, 2, stream);
+}
+
+lsamp_status lsamp_logprobs(lsamp_context* ctx, const lsamp_logprobs_args* a, void* stream) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->top_k < 0 || a->top_k > kRankMaxK || a->top_k > a->vocab)
+    return fail(LSAMP_ERR_SHAPE, "top_k %d outside [0, min(%d, vocab)]", a->top_k, kRankMaxK);
+  if (a->top_k > 0 && (!a->top_values || !a->top_ids))
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "top_values and top_ids are required when top_k > 0");
+  if ((a->tokens == nullptr) != (a->chosen == nullptr))
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "tokens and chosen go together");
+  RankPlan P{};
+  P.rows = a->rows;
+  P.vocab = a->vocab;
+  P.dtype = a->dtype;
+  P.k = a->top_k;
+  P.row_stride = a->row_stride;
+  P.col_stride = a->col_stride;
+  P.lse = 1;
+  P.raw_values = 0;
+  P.logits = a->logits;
+  P.tokens = a->tokens;
+  P.chosen = a->chosen;
+  P.values = a->top_values;
+  P.ids = a->top_ids;
+  P.row_flags = a->row_flags;
+  return rank_common(ctx, P, 1, stream);
 }
 
 // ---------------------------------------------------------------- resolution

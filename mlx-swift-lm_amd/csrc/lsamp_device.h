@@ -12,6 +12,10 @@
 namespace lsamp {
 namespace dev {
 
+// Fourth word of a raw buffer descriptor on gfx9-family parts (32-bit data
+// format; no swizzle, no stride).
+constexpr int kBufferWord3 = 0x00020000;
+
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kPosInf = __builtin_huge_valf();
 

@@ -122,6 +122,30 @@ struct KeptItem {
 static_assert(kMaxRowChunks <= kThreads, "the draw keeps one chunk per thread");
 static_assert(kBins == 2 * kThreads, "the merge keeps two bins per thread");
 
+// Ranking of raw logits (exact top-k and log-probabilities).  One 512-thread
+// work-group per slice of a row; a slice is 16,384 / 32,768 / 65,536 tokens
+// (option 0 / 1 / 2, whatever the dtype: 32 / 64 / 128 tokens per thread).
+constexpr int kRankMaxK = 32;
+constexpr int kRankMaxSlices = 16;
+constexpr int kRankOptions = 3;
+constexpr int rank_slice_len(int option) { return 16384 << option; }
+// Slice flags of the ranking.
+constexpr uint32_t kRankNaN = 1u;        // a NaN logit
+constexpr uint32_t kRankPosInf = 2u;     // a +inf logit
+constexpr uint32_t kRankNonfinite = 4u;  // a NaN or +-inf logit
+
+// Per-slice result of the ranking: the slice's k largest sort keys (value
+// descending, then token id ascending, NaN last), 0 past the slice's own
+// tokens, and its log-sum-exp partial.
+struct RankSlice {
+  uint64_t top[kRankMaxK];
+  double s;           // sum exp(x - m) over the slice's finite logits (m finite)
+  float m;            // largest non-NaN logit of the slice (-inf if none)
+  uint32_t flags;     // kRank*
+  uint32_t tok_bits;  // the logit bits of the row's chosen token, if this slice holds it
+  int32_t pad;
+};
+
 struct Workspace {
   int32_t max_rows;
   int32_t max_vocab;
@@ -140,6 +164,29 @@ struct Workspace {
   lsamp_row_stats* vstats;  // [max_rows]
   int32_t* vtokens;         // [max_rows]
   uint32_t* vflags;         // [max_rows]
+  // Top-k / log-probability ranking of raw logits
+  RankSlice* rank_part;     // [max_rows][kRankMaxSlices]
+  uint32_t* arrive_rank;    // [max_rows]
+};
+
+struct RankPlan {
+  int32_t rows;
+  int32_t vocab;
+  int32_t dtype;
+  int32_t k;           // keys reported per row (0..kRankMaxK)
+  int64_t row_stride;  // elements between rows
+  int64_t col_stride;  // elements between tokens
+  int32_t slices;      // per row
+  int32_t option;      // slice option (rank_slice_len)
+  int32_t vec;         // 16-byte vector loads (col_stride 1, aligned rows)
+  int32_t lse;         // compute the log-sum-exp
+  int32_t raw_values;  // values = raw logits (else log-probabilities)
+  const void* logits;
+  const int32_t* tokens;  // chosen token per row (NULL: no chosen output)
+  float* chosen;          // [rows]
+  float* values;          // [rows, k]
+  int32_t* ids;           // [rows, k]
+  uint32_t* row_flags;    // [rows] or NULL
 };
 
 // Sticky device status bits.
@@ -212,5 +259,7 @@ int fused_blocks_per_cu(int dtype);
 // Acceptance, residual / bonus draws and outputs of an MTP verification whose
 // rows were sampled by launch_sample into ws.v* (one work-group per sequence).
 int launch_verify_finish(const Workspace& ws, const VerifyPlan& plan, void* stream);
+// Exact top-k of raw logits and their log-probabilities (lsamp_rank.hip).
+int launch_rank(const Workspace& ws, const RankPlan& plan, void* stream);
 
 }  // namespace lsamp

@@ -38,9 +38,6 @@ using namespace dev;
 
 constexpr int kSliceWords = kMaxSliceLen / 32;       // penalty bitmap words
 constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
-// Fourth word of a raw buffer descriptor on gfx9-family parts (32-bit data
-// format; no swizzle, no stride).
-constexpr int kBufferWord3 = 0x00020000;
 // Buckets of the short-list finalize's counting sort (by a key's high word);
 // their counts and starts live in the thread-maximum histogram.
 constexpr int kRankBuckets = 512;

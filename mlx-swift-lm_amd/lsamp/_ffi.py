@@ -28,7 +28,8 @@ SEM_MLXLM, SEM_CBV2 = 0, 1
 KIND_ARGMAX, KIND_FILTERED, KIND_CATEGORICAL = 0, 1, 2
 MASK_TAIL_KEEP, MASK_TAIL_FORBID = 0, 1
 PEN_REPETITION, PEN_PRESENCE = 1, 2
-ROW_NONFINITE, ROW_EMPTY, ROW_OVERFLOW = 1, 2, 4
+ROW_NONFINITE, ROW_EMPTY, ROW_OVERFLOW, ROW_TOKEN_RANGE = 1, 2, 4, 8
+RANK_MAX_K = 32
 VERIFY_RESIDUAL, VERIFY_EXACT, VERIFY_TYPICAL = 0, 1, 2
 MODE_AUTO, MODE_FUSED, MODE_SPLIT = 0, 1, 2
 STATUS_SPIN_TIMEOUT = 1
@@ -158,6 +159,36 @@ class LaunchInfo(Structure):
                 ("rows_per_round", c_int32), ("grid", c_int32)]
 
 
+class Top2Args(Structure):
+    _fields_ = [
+        ("rows", c_int32),
+        ("vocab", c_int32),
+        ("dtype", c_int32),
+        ("row_stride", c_int64),
+        ("col_stride", c_int64),
+        ("logits", c_void_p),
+        ("ids", c_void_p),
+        ("values", c_void_p),
+    ]
+
+
+class LogprobsArgs(Structure):
+    _fields_ = [
+        ("rows", c_int32),
+        ("vocab", c_int32),
+        ("dtype", c_int32),
+        ("row_stride", c_int64),
+        ("col_stride", c_int64),
+        ("logits", c_void_p),
+        ("top_k", c_int32),
+        ("tokens", c_void_p),
+        ("chosen", c_void_p),
+        ("top_values", c_void_p),
+        ("top_ids", c_void_p),
+        ("row_flags", c_void_p),
+    ]
+
+
 class LibraryMissing(RuntimeError):
     pass
 
@@ -193,6 +224,10 @@ def load_library(path: str | None = None):
     lib.lsamp_context_read_timing.restype = c_int32
     lib.lsamp_verify.argtypes = [c_void_p, POINTER(VerifyArgs), c_void_p]
     lib.lsamp_verify.restype = c_int32
+    lib.lsamp_top2.argtypes = [c_void_p, POINTER(Top2Args), c_void_p]
+    lib.lsamp_top2.restype = c_int32
+    lib.lsamp_logprobs.argtypes = [c_void_p, POINTER(LogprobsArgs), c_void_p]
+    lib.lsamp_logprobs.restype = c_int32
     lib.lsamp_resolve_generate_parameters.argtypes = [
         POINTER(GenerateParameters), POINTER(RowParams), POINTER(c_int32)]
     lib.lsamp_resolve_generate_parameters.restype = c_int32

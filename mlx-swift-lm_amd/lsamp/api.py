@@ -134,6 +134,26 @@ class Context:
         return prep.outputs()
 
     # ----------------------------------------------------------------- verify
+    def prepare_top2(self, logits: torch.Tensor) -> "PreparedRank":
+        return PreparedRank(self, logits, top2=True)
+
+    def top2(self, logits: torch.Tensor) -> dict:
+        """cbv2TopTwoRows (CBv2TopTwo.swift:191): ids [rows, 2] int32 and values
+        [rows, 2] float32 of a [rows, vocab] (or [1, rows, vocab]) view."""
+        p = self.prepare_top2(logits)
+        p.launch()
+        return p.outputs()
+
+    def prepare_logprobs(self, logits: torch.Tensor, *, tokens=None, top_k: int = 0) -> "PreparedRank":
+        return PreparedRank(self, logits, top2=False, tokens=tokens, top_k=top_k)
+
+    def logprobs(self, logits: torch.Tensor, *, tokens=None, top_k: int = 0) -> dict:
+        """Raw log-probabilities (LogitsPipelineV2.swift:307-314) gathered for
+        `tokens` and the top_k best tokens (CBv2Logprobs.gather, :534-549)."""
+        p = self.prepare_logprobs(logits, tokens=tokens, top_k=top_k)
+        p.launch()
+        return p.outputs()
+
     def prepare_verify(self, target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens,
                        params, uniforms, *, mode: int = _ffi.VERIFY_RESIDUAL,
                        typical_delta: float = 0.0) -> "PreparedVerify":
@@ -311,6 +331,66 @@ class PreparedVerify:
 
     def outputs(self) -> dict:
         return {"accepted": self.accepted, "tokens": self.tokens, "accept_mask": self.accept_mask}
+
+
+class PreparedRank:
+    """A fully bound lsamp_top2 / lsamp_logprobs call over a 2-D view of
+    logits with any strides (a [1, rows, vocab] view is taken as its rows)."""
+
+    def __init__(self, ctx: Context, logits: torch.Tensor, *, top2: bool, tokens=None,
+                 top_k: int = 0):
+        if logits.dim() == 3 and logits.shape[0] == 1:
+            logits = logits[0]
+        if logits.dim() != 2:
+            raise ValueError("logits must be [rows, vocab] or [1, rows, vocab]")
+        rows, V = logits.shape
+        dev = logits.device
+        self.ctx = ctx
+        self.top2 = top2
+        self.keep_alive = [logits]
+        dt = LSAMP_DTYPE[logits.dtype]
+        rs, cs = logits.stride()
+        if top2:
+            a = _ffi.Top2Args()
+            self.ids = torch.empty((rows, 2), dtype=torch.int32, device=dev)
+            self.values = torch.empty((rows, 2), dtype=torch.float32, device=dev)
+            a.ids, a.values = self.ids.data_ptr(), self.values.data_ptr()
+        else:
+            a = _ffi.LogprobsArgs()
+            a.top_k = top_k
+            self.ids = torch.empty((rows, top_k), dtype=torch.int32, device=dev)
+            self.values = torch.empty((rows, top_k), dtype=torch.float32, device=dev)
+            self.row_flags = torch.empty(rows, dtype=torch.int32, device=dev)
+            a.top_ids = self.ids.data_ptr() if top_k > 0 else None
+            a.top_values = self.values.data_ptr() if top_k > 0 else None
+            a.row_flags = self.row_flags.data_ptr()
+            self.chosen = None
+            if tokens is not None:
+                t = (tokens.to(dev, torch.int32).contiguous() if isinstance(tokens, torch.Tensor)
+                     else torch.from_numpy(np.ascontiguousarray(tokens, np.int32)).to(dev))
+                self.keep_alive.append(t)
+                self.chosen = torch.empty(rows, dtype=torch.float32, device=dev)
+                a.tokens, a.chosen = t.data_ptr(), self.chosen.data_ptr()
+        a.rows, a.vocab, a.dtype = rows, V, dt
+        a.row_stride, a.col_stride = rs, cs
+        a.logits = logits.data_ptr()
+        self.args = a
+        self._byref = ctypes.byref(a)
+
+    def launch(self, stream: Optional[int] = None) -> None:
+        s = stream if stream is not None else current_stream_handle(self.ids.device)
+        fn = self.ctx.lib.lsamp_top2 if self.top2 else self.ctx.lib.lsamp_logprobs
+        st = fn(self.ctx.handle, self._byref, ctypes.c_void_p(s))
+        if st != 0:
+            raise _ffi.LsampError(st, "lsamp_top2" if self.top2 else "lsamp_logprobs")
+
+    def outputs(self) -> dict:
+        if self.top2:
+            return {"ids": self.ids, "values": self.values}
+        out = {"top_ids": self.ids, "top_values": self.values, "row_flags": self.row_flags}
+        if self.chosen is not None:
+            out["chosen"] = self.chosen
+        return out
 
 
 def stats_to_numpy(t: torch.Tensor) -> np.ndarray:

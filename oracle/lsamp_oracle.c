@@ -936,3 +936,98 @@ int32_t lso_verify(const lso_verify_args* a) {
   free(ws);
   return status;
 }
+
+/* ------------------------------------------------------ ranking of raw logits */
+
+/* darkbloom_qwen35_mtp_top2_better, CBv2TopTwo.swift:29-47: a NaN never beats
+ * a number; otherwise the larger value wins and an exact tie (+0 == -0) goes
+ * to the lower id. */
+static int rank_better(float a, int32_t ia, float b, int32_t ib) {
+  const int an = isnan(a), bn = isnan(b);
+  if (an != bn) return !an;
+  if (a > b) return 1;
+  if (a < b) return 0;
+  return ia < ib;
+}
+
+/* log(sum(exp(x))) of one row in double, with MLX's conventions for
+ * non-finite rows (logsumexp: the row maximum is returned where it is
+ * infinite): NaN if any logit is NaN, +inf if one is +inf, -inf if all are
+ * -inf.  The reference evaluates raw - logSumExp(raw) in float32
+ * (LogitsPipelineV2.swift:311; Evaluate.swift:805 logSoftmax). */
+static double row_lse(const void* row, int32_t dtype, int32_t V, int64_t cs, uint32_t* nonfinite) {
+  int nan = 0, pinf = 0;
+  double m = -INFINITY;
+  for (int32_t i = 0; i < V; ++i) {
+    const float x = load_logit(row, dtype, (int64_t)i * cs);
+    if (isnan(x)) {
+      nan = 1;
+    } else {
+      if (x == INFINITY) pinf = 1;
+      if (x > m) m = x;
+    }
+    if (!isfinite(x)) *nonfinite = 1;
+  }
+  if (nan) return NAN;
+  if (pinf) return INFINITY;
+  if (m == -INFINITY) return -INFINITY;
+  double z = 0.0;
+  for (int32_t i = 0; i < V; ++i) z += exp((double)load_logit(row, dtype, (int64_t)i * cs) - m);
+  return m + log(z);
+}
+
+int32_t lso_rank(const lso_rank_args* a) {
+  if (!a || !a->logits || a->rows <= 0 || a->vocab <= 0 || a->k < 0 || a->k > a->vocab ||
+      a->col_stride < 1 || a->row_stride < 0)
+    return LSAMP_ERR_INVALID_ARGUMENT;
+  const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
+  const int32_t V = a->vocab, k = a->k;
+  float* tv = (float*)malloc(sizeof(float) * (size_t)(k > 0 ? k : 1));
+  int32_t* ti = (int32_t*)malloc(sizeof(int32_t) * (size_t)(k > 0 ? k : 1));
+  if (!tv || !ti) {
+    free(tv);
+    free(ti);
+    return LSAMP_ERR_CAPACITY;
+  }
+  for (int32_t r = 0; r < a->rows; ++r) {
+    const char* row = (const char*)a->logits + (size_t)r * (size_t)a->row_stride * es;
+    /* the k best by insertion into a sorted list (CBv2TopTwo.swift:49-79
+     * keeps the best two the same way) */
+    int32_t n = 0;
+    for (int32_t i = 0; i < V; ++i) {
+      const float x = load_logit(row, a->dtype, (int64_t)i * a->col_stride);
+      if (n == k && (k == 0 || !rank_better(x, i, tv[k - 1], ti[k - 1]))) continue;
+      int32_t p = n < k ? n : k - 1;
+      while (p > 0 && rank_better(x, i, tv[p - 1], ti[p - 1])) {
+        tv[p] = tv[p - 1];
+        ti[p] = ti[p - 1];
+        --p;
+      }
+      tv[p] = x;
+      ti[p] = i;
+      if (n < k) ++n;
+    }
+    uint32_t nonfinite = 0;
+    const double lse = row_lse(row, a->dtype, V, a->col_stride, &nonfinite);
+    uint32_t flags = nonfinite ? LSAMP_ROW_NONFINITE : 0u;
+    for (int32_t j = 0; j < k; ++j) {
+      if (a->ids) a->ids[(size_t)r * k + j] = ti[j];
+      if (a->values)
+        a->values[(size_t)r * k + j] = a->raw_values ? tv[j] : (float)((double)tv[j] - lse);
+    }
+    if (a->tokens) {
+      const int32_t t = a->tokens[r];
+      float c = NAN;
+      if (t >= 0 && t < V)
+        c = (float)((double)load_logit(row, a->dtype, (int64_t)t * a->col_stride) - lse);
+      else
+        flags |= LSAMP_ROW_TOKEN_RANGE;
+      if (a->chosen) a->chosen[r] = c;
+    }
+    if (a->row_flags) a->row_flags[r] = flags;
+    if (a->lse) a->lse[r] = lse;
+  }
+  free(tv);
+  free(ti);
+  return 0;
+}

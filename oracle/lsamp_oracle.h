@@ -77,6 +77,29 @@ typedef struct lso_verify_args {
 /* MTP verification (RESIDUAL / EXACT / TYPICAL).  Returns 0 or < 0. */
 int32_t lso_verify(const lso_verify_args* a);
 
+typedef struct lso_rank_args {
+  int32_t rows;
+  int32_t vocab;
+  int32_t dtype;
+  int64_t row_stride;  /* elements */
+  int64_t col_stride;  /* elements */
+  const void* logits;
+  int32_t k;           /* best tokens reported per row */
+  int32_t raw_values;  /* 1: values = raw logits (top-2); 0: log-probabilities */
+  const int32_t* tokens; /* [rows] or NULL */
+  /* outputs (NULL = not wanted) */
+  float* chosen;       /* [rows] log-probability of tokens[r] (NaN if out of range) */
+  float* values;       /* [rows, k] */
+  int32_t* ids;        /* [rows, k] */
+  uint32_t* row_flags; /* [rows] LSAMP_ROW_NONFINITE | LSAMP_ROW_TOKEN_RANGE */
+  double* lse;         /* [rows] the log-sum-exp */
+} lso_rank_args;
+
+/* Exact top-k of raw logits and their log-probabilities (top-2:
+ * CBv2TopTwo.swift; log-probabilities: LogitsPipelineV2.swift:307-314,
+ * 534-549).  Returns 0 or < 0. */
+int32_t lso_rank(const lso_rank_args* a);
+
 /* Building blocks exposed for known-answer tests. */
 float lso_dexp(float d);
 uint64_t lso_weight(float y, float y_max, float scale);

@@ -46,6 +46,15 @@ class LsoVerifyArgs(Structure):
     ]
 
 
+class LsoRankArgs(Structure):
+    _fields_ = [
+        ("rows", c_int32), ("vocab", c_int32), ("dtype", c_int32), ("row_stride", c_int64),
+        ("col_stride", c_int64), ("logits", c_void_p), ("k", c_int32), ("raw_values", c_int32),
+        ("tokens", c_void_p), ("chosen", c_void_p), ("values", c_void_p), ("ids", c_void_p),
+        ("row_flags", c_void_p), ("lse", c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -57,6 +66,8 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         L.lso_sample.argtypes = [POINTER(LsoSampleArgs)]
         L.lso_sample.restype = c_int32
+        L.lso_rank.argtypes = [POINTER(LsoRankArgs)]
+        L.lso_rank.restype = c_int32
         L.lso_verify.argtypes = [POINTER(LsoVerifyArgs)]
         L.lso_verify.restype = c_int32
         L.lso_dexp.argtypes = [c_float]
@@ -222,6 +233,43 @@ def verify(*, mode, target, draft, draft_tokens, dtype, params, uniforms, typica
     st = lib().lso_verify(ctypes.byref(a))
     if st != 0:
         raise RuntimeError(f"lso_verify failed: {st}")
+    return out
+
+
+def rank(storage, *, dtype, k, raw_values, rows=None, vocab=None, row_stride=None,
+         col_stride=1, tokens=None):
+    """Exact top-k (and log-probabilities) of the [rows, vocab] view of
+    `storage` (logit bits: uint16 for bf16 / f16, float32 for f32) with the
+    given element strides.  Returns ids, values, chosen, row_flags, lse."""
+    storage = np.ascontiguousarray(storage)
+    if rows is None:
+        rows, vocab = storage.shape
+        row_stride = vocab
+    if row_stride is None:
+        row_stride = vocab
+    out = {"ids": np.zeros((rows, k), np.int32), "values": np.zeros((rows, k), np.float32),
+           "chosen": np.zeros(rows, np.float32), "row_flags": np.zeros(rows, np.uint32),
+           "lse": np.zeros(rows, np.float64)}
+    a = LsoRankArgs()
+    a.rows, a.vocab, a.dtype = rows, vocab, dtype
+    a.row_stride, a.col_stride = row_stride, col_stride
+    a.logits = _ptr(storage)
+    a.k = k
+    a.raw_values = 1 if raw_values else 0
+    tok = None
+    if tokens is not None:
+        tok = np.ascontiguousarray(tokens, np.int32)
+        a.tokens = _ptr(tok)
+        a.chosen = _ptr(out["chosen"])
+    a.values = _ptr(out["values"])
+    a.ids = _ptr(out["ids"])
+    a.row_flags = _ptr(out["row_flags"])
+    a.lse = _ptr(out["lse"])
+    st = lib().lso_rank(ctypes.byref(a))
+    if st != 0:
+        raise RuntimeError(f"lso_rank failed: {st}")
+    if tokens is None:
+        del out["chosen"]
     return out
 
 
