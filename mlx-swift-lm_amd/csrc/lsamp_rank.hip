@@ -12,8 +12,8 @@
 //   1. each thread takes its largest key (and, for log-probabilities, the
 //      sum of exp(x - m) over its logits, m its largest non-NaN logit);
 //   2. tau = the k-th largest of the 512 thread maxima: a rank inside each
-//      wave (64 lane reads), then a rank in the 8 sorted wave lists (binary
-//      searches);
+//      wave (a count over the wave's 64 maxima in LDS), then a rank in the 8
+//      sorted wave lists (binary searches);
 //   3. every key >= tau is a candidate: they include the slice's top k (the k
 //      threads at or above tau hold k distinct keys >= tau) and come from k
 //      threads only, so there are at most k * (tokens per thread).  Those
@@ -144,6 +144,7 @@ struct alignas(16) RankLds {
   } u;
   uint4 stage[kRankMaxK * kRankMaxVecs];  // logits of the threads at or above tau
   int32_t stage_tid[kRankMaxK];
+  uint64_t wt[kWaves][64];           // each wave's thread maxima
   uint64_t tops[kWaves][kRankMaxK];  // each wave's largest thread maxima (0-padded)
   uint64_t out[kRankMaxK];           // finalize: the row's top k
   float wm[kWaves];                  // per wave: largest finite thread maximum
@@ -366,9 +367,10 @@ __global__ __launch_bounds__(kThreads) void k_rank(Workspace ws, RankPlan P) {
       wsum = wave_sum(term);
     }
     if (k > 0) {
-      int rank = 0;
-#pragma unroll 4
-      for (int j = 0; j < 64; ++j) rank += read_lane(tcomp, j) > tcomp ? 1 : 0;
+      // (the wave's own LDS row: its writes are visible to its reads)
+      L.wt[wv][lane] = tcomp;
+      __builtin_amdgcn_wave_barrier();
+      const int rank = count_gt16(L.wt[wv], 64 / 16, tcomp);
       if (rank < kRankMaxK) L.tops[wv][rank] = rank < k ? tcomp : 0ull;
     }
     if (lane == 0) {
@@ -469,7 +471,8 @@ __global__ __launch_bounds__(kThreads) void k_rank(Workspace ws, RankPlan P) {
     const int g = i / k, rr = i - g * k;
     const uint64_t v = L.u.lists[g][rr];
     if (v != 0ull) {
-      const int rk = rank_in_sorted<kRankMaxSlices>(L.u.lists, G, v);
+      const int rk = G <= 8 ? rank_in_sorted<8>(L.u.lists, G, v)
+                            : rank_in_sorted<kRankMaxSlices>(L.u.lists, G, v);
       if (rk < k) L.out[rk] = v;
     }
   }
