@@ -185,6 +185,11 @@ typedef struct lsamp_sample_args {
   uint8_t* keep;          /* [rows, vocab] out or NULL: 1 where the token
                              survives the filters (parity mode)               */
   lsamp_row_stats* stats; /* [rows] out or NULL                                 */
+
+  /* [rows] or NULL: row r's entries are penalty_entries[penalty_row_ptr[r] ..
+   * penalty_row_ptr[r] + penalty_row_len[r]) instead of .. penalty_row_ptr[r+1]
+   * (a fixed-capacity table that lsamp_commit keeps up to date)             */
+  const int32_t* penalty_row_len;
 } lsamp_sample_args;
 
 /* ---- MTP verification ----------------------------------------------------- */
@@ -322,6 +327,49 @@ typedef struct lsamp_logprobs_args {
  * Evaluate.swift:818-853).  The log-sum-exp is NaN when a logit is NaN,
  * +inf when one is +inf, -inf when all are -inf. */
 lsamp_status lsamp_logprobs(lsamp_context* ctx, const lsamp_logprobs_args* args, void* stream);
+
+/* ---- device-side penalty state ---------------------------------------------
+ * The incremental state of LogitsPipelineV2 (outputCounts, repWindow,
+ * repWindowCounts, ringPos; LogitsPipelineV2.swift:127-141) kept on the device
+ * as a fixed-capacity sparse table that lsamp_sample reads directly
+ * (penalty_row_ptr[r] = r * capacity, penalty_row_len = row_len).  Entries
+ * hold {token, output count, LSAMP_PEN_REPETITION while the token is in the
+ * repetition window, logit bias}; build the initial table from the request's
+ * prompt / output history on the host once. */
+#define LSAMP_STATE_COUNTS 1u     /* frequency or presence penalty on           */
+#define LSAMP_STATE_REPETITION 2u /* repetition penalty on: keep the window ring */
+
+typedef struct lsamp_penalty_table {
+  int32_t rows;
+  int32_t capacity;        /* entry slots per row                              */
+  int32_t window_capacity; /* ring slots per row (>= every window_size)        */
+  lsamp_penalty_entry* entries; /* [rows, capacity]; slots [0, row_len[r]) used */
+  int32_t* row_len;        /* [rows]                                           */
+  int32_t* window_count;   /* [rows, capacity]: occurrences of the entry's token
+                              in the repetition window                         */
+  int32_t* window;         /* [rows, window_capacity]: the ring, -1 = empty     */
+  int32_t* ring_pos;       /* [rows]: the slot the next token overwrites       */
+  const int32_t* window_size; /* [rows]: W >= 1 (repetitionContextSize)        */
+  const uint32_t* mode;    /* [rows]: LSAMP_STATE_* bits                        */
+} lsamp_penalty_table;
+
+typedef struct lsamp_commit_args {
+  lsamp_penalty_table table;
+  int32_t vocab;
+  const int32_t* tokens; /* [rows] the sampled tokens; ids outside [0, vocab)
+                            (an EMPTY row's -1) commit nothing               */
+  uint32_t* row_flags;   /* [rows] out or NULL: LSAMP_ROW_OVERFLOW when a new
+                            entry did not fit in the row's capacity          */
+} lsamp_commit_args;
+
+/* LogitsPipelineV2.commit (LogitsPipelineV2.swift:357-384) for every row, on
+ * the device: the sampled token's output count += 1 (COUNTS rows); the
+ * repetition ring evicts the token at ring_pos (its window count -= 1, the
+ * REPETITION flag cleared at 0) and takes the sampled token (window count
+ * += 1, flag set), ring_pos = (ring_pos + 1) % W (REPETITION rows).  Entries
+ * that end with no count, flag or bias are removed (the last entry of the
+ * row takes the slot). */
+lsamp_status lsamp_commit(lsamp_context* ctx, const lsamp_commit_args* args, void* stream);
 
 /* ---- host-side parameter resolution (no device work) ---------------------- */
 

@@ -57,6 +57,8 @@ struct lsamp_context {
   int32_t mode = LSAMP_MODE_AUTO;
   int32_t blocks_per_cu[3] = {0, 0, 0};  // fused-kernel occupancy per dtype
   Workspace ws;
+  RankSlice* rank_part;  // [max_rows][kRankMaxSlices] (in `block`)
+  uint32_t* arrive_rank; // [max_rows] (in `block`)
   void* block;  // single device allocation backing the workspace
   size_t bytes;
   // timing hook
@@ -121,8 +123,10 @@ lsamp_status rank_common(lsamp_context* ctx, RankPlan& P, int32_t min_vocab, voi
   const size_t es = P.dtype == LSAMP_DTYPE_F32 ? 4 : 2;
   P.vec = P.col_stride == 1 && aligned16(P.logits) && ((size_t)P.row_stride * es) % 16 == 0;
   plan_rank(P.rows, P.vocab, ctx->cus, &P.option, &P.slices);
+  P.part = ctx->rank_part;
+  P.arrive = ctx->arrive_rank;
   DeviceGuard guard(ctx->device);
-  const int err = launch_rank(ctx->ws, P, stream);
+  const int err = launch_rank(P, stream);
   if (err != 0)
     return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
   return ok();
@@ -147,6 +151,8 @@ int64_t lsamp_abi_sizeof(const char* name) {
   if (!strcmp(name, "lsamp_cbv2_params")) return (int64_t)sizeof(lsamp_cbv2_params);
   if (!strcmp(name, "lsamp_launch_info")) return (int64_t)sizeof(lsamp_launch_info);
   if (!strcmp(name, "lsamp_top2_args")) return (int64_t)sizeof(lsamp_top2_args);
+  if (!strcmp(name, "lsamp_penalty_table")) return (int64_t)sizeof(lsamp_penalty_table);
+  if (!strcmp(name, "lsamp_commit_args")) return (int64_t)sizeof(lsamp_commit_args);
   if (!strcmp(name, "lsamp_logprobs_args")) return (int64_t)sizeof(lsamp_logprobs_args);
   return -1;
 }
@@ -225,8 +231,8 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   ws.vstats = reinterpret_cast<lsamp_row_stats*>(b + o_vstats);
   ws.vtokens = reinterpret_cast<int32_t*>(b + o_vtok);
   ws.vflags = reinterpret_cast<uint32_t*>(b + o_vfl);
-  ws.rank_part = reinterpret_cast<RankSlice*>(b + o_rpart);
-  ws.arrive_rank = reinterpret_cast<uint32_t*>(b + o_arank);
+  ctx->rank_part = reinterpret_cast<RankSlice*>(b + o_rpart);
+  ctx->arrive_rank = reinterpret_cast<uint32_t*>(b + o_arank);
   *out = ctx;
   return ok();
 }
@@ -333,6 +339,8 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
     return fail(LSAMP_ERR_INVALID_ARGUMENT, "either uniforms or philox_keys is required");
   if ((a->penalty_row_ptr == nullptr) != (a->penalty_entries == nullptr))
     return fail(LSAMP_ERR_INVALID_ARGUMENT, "penalty_row_ptr and penalty_entries go together");
+  if (a->penalty_row_len && !a->penalty_row_ptr)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "penalty_row_len needs penalty_row_ptr");
   if (a->bitmask) {
     if (a->mask_words <= 0 || a->mask_bits < 0)
       return fail(LSAMP_ERR_SHAPE, "mask_words %d / mask_bits %d invalid", a->mask_words,
@@ -361,6 +369,7 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
   P.rows_split = a->rows;
   P.params = a->params;
   P.row_ptr = a->penalty_row_ptr;
+  P.row_len = a->penalty_row_len;
   P.entries = a->penalty_entries;
   P.bitmask = a->bitmask;
   P.mask_words = a->mask_words;
@@ -441,6 +450,24 @@ lsamp_status lsamp_logprobs(lsamp_context* ctx, const lsamp_logprobs_args* a, vo
   P.ids = a->top_ids;
   P.row_flags = a->row_flags;
   return rank_common(ctx, P, 1, stream);
+}
+
+lsamp_status lsamp_commit(lsamp_context* ctx, const lsamp_commit_args* a, void* stream) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  const lsamp_penalty_table& t = a->table;
+  if (t.rows <= 0 || t.capacity <= 0 || t.window_capacity <= 0)
+    return fail(LSAMP_ERR_SHAPE, "rows %d / capacity %d / window_capacity %d must be positive",
+                t.rows, t.capacity, t.window_capacity);
+  if (a->vocab <= 0) return fail(LSAMP_ERR_SHAPE, "vocab %d must be positive", a->vocab);
+  if (!t.entries || !t.row_len || !t.window_count || !t.window || !t.ring_pos ||
+      !t.window_size || !t.mode || !a->tokens)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "every table array and tokens are required");
+  DeviceGuard guard(ctx->device);
+  const int err = launch_commit(*a, stream);
+  if (err != 0)
+    return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+  return ok();
 }
 
 // ---------------------------------------------------------------- resolution

@@ -164,9 +164,6 @@ struct Workspace {
   lsamp_row_stats* vstats;  // [max_rows]
   int32_t* vtokens;         // [max_rows]
   uint32_t* vflags;         // [max_rows]
-  // Top-k / log-probability ranking of raw logits
-  RankSlice* rank_part;     // [max_rows][kRankMaxSlices]
-  uint32_t* arrive_rank;    // [max_rows]
 };
 
 struct RankPlan {
@@ -187,6 +184,9 @@ struct RankPlan {
   float* values;          // [rows, k]
   int32_t* ids;           // [rows, k]
   uint32_t* row_flags;    // [rows] or NULL
+  // the context's ranking workspace
+  RankSlice* part;        // [max_rows][kRankMaxSlices]
+  uint32_t* arrive;       // [max_rows]
 };
 
 // Sticky device status bits.
@@ -216,6 +216,7 @@ struct SamplePlan {
   int32_t vwin;
   const lsamp_row_params* params;
   const int32_t* row_ptr;
+  const int32_t* row_len;  // or NULL: rows end at row_ptr[row + 1]
   const lsamp_penalty_entry* entries;
   const uint32_t* bitmask;
   int32_t mask_words;
@@ -260,6 +261,8 @@ int fused_blocks_per_cu(int dtype);
 // rows were sampled by launch_sample into ws.v* (one work-group per sequence).
 int launch_verify_finish(const Workspace& ws, const VerifyPlan& plan, void* stream);
 // Exact top-k of raw logits and their log-probabilities (lsamp_rank.hip).
-int launch_rank(const Workspace& ws, const RankPlan& plan, void* stream);
+int launch_rank(const RankPlan& plan, void* stream);
+// Incremental penalty-state update after a draw (lsamp_commit.hip).
+int launch_commit(const lsamp_commit_args& args, void* stream);
 
 }  // namespace lsamp

@@ -291,12 +291,16 @@ __device__ __forceinline__ void entry_bounds(const SamplePlan& P, int row, Entry
   ep.e0 = 0;
   ep.e1 = 0;
   if (P.row_ptr && P.entries) {
-    // (one laundered address for both words: see load_uniform)
+    // (laundered addresses: see load_uniform; the second word is the next
+    // row's start, or the row's length in a fixed-capacity table, chosen by
+    // a scalar select so both loads go out in one round)
     uint64_t a = (uint64_t)(P.row_ptr + row);
-    asm volatile("" : "+s"(a));
-    const __attribute__((address_space(4))) int32_t* q = (const __attribute__((address_space(4))) int32_t*)a;
-    ep.e0 = q[0];
-    ep.e1 = q[1];
+    uint64_t b = P.row_len ? (uint64_t)(P.row_len + row) : a + sizeof(int32_t);
+    asm volatile("" : "+s"(a), "+s"(b));
+    typedef const __attribute__((address_space(4))) int32_t* CI;
+    const int32_t w0 = *(CI)a, w1 = *(CI)b;
+    ep.e0 = w0;
+    ep.e1 = P.row_len ? w0 + w1 : w1;
   }
 }
 
@@ -940,7 +944,7 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
       int32_t e0 = 0, e1 = 0;
       if (P.row_ptr && P.entries) {
         e0 = P.row_ptr[row];
-        e1 = P.row_ptr[row + 1];
+        e1 = P.row_len ? e0 + P.row_len[row] : P.row_ptr[row + 1];
       }
       for (int32_t e = e0 + l; e < e1; e += 64) {
         const lsamp_penalty_entry ent = P.entries[e];
@@ -993,7 +997,7 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
     int32_t e0 = 0, e1 = 0;
     if (P.row_ptr && P.entries) {
       e0 = P.row_ptr[row];
-      e1 = P.row_ptr[row + 1];
+      e1 = P.row_len ? e0 + P.row_len[row] : P.row_ptr[row + 1];
     }
     int32_t pe = -1;
     for (int32_t e = e0 + l; e < e1; e += 64)

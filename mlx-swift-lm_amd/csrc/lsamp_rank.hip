@@ -197,7 +197,7 @@ __device__ __forceinline__ int rank_in_sorted(const uint64_t (*a)[kRankMaxK], in
 }
 
 template <int DT, int OPT, bool VEC>
-__global__ __launch_bounds__(kThreads) void k_rank(Workspace ws, RankPlan P) {
+__global__ __launch_bounds__(kThreads) void k_rank(RankPlan P) {
   using B = RankBits<DT>;
   using BT = Best<DT>;
   constexpr int N = B::N;
@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void k_rank(Workspace ws, RankPlan P) {
   const int k = P.k;
   const char* rowp =
       reinterpret_cast<const char*>(P.logits) + (size_t)row * (size_t)P.row_stride * ES;
-  RankSlice* part = ws.rank_part + (size_t)row * kRankMaxSlices;
+  RankSlice* part = P.part + (size_t)row * kRankMaxSlices;
 
   // the chosen token's logit, read early by the slice that holds it
   const int32_t tok = P.tokens ? P.tokens[row] : -1;
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(kThreads) void k_rank(Workspace ws, RankPlan P) {
     st_coherent(&part[slice].flags, sflags);
     st_coherent(&part[slice].tok_bits, tok_bits);
   }
-  if (!arrive_last(&ws.arrive_rank[row], (uint32_t)G, &L.last)) return;
+  if (!arrive_last(&P.arrive[row], (uint32_t)G, &L.last)) return;
 
   // ---- the row's last work-group: every slice record in one round of reads
   for (int i = tid; i < G * kRankMaxK; i += kThreads) {
@@ -506,7 +506,7 @@ __global__ __launch_bounds__(kThreads) void k_rank(Workspace ws, RankPlan P) {
         P.chosen[row] = c;
       }
       if (P.row_flags) P.row_flags[row] = of;
-      st_coherent(&ws.arrive_rank[row], 0u);
+      st_coherent(&P.arrive[row], 0u);
     }
   }
   __syncthreads();
@@ -519,31 +519,31 @@ __global__ __launch_bounds__(kThreads) void k_rank(Workspace ws, RankPlan P) {
 }
 
 template <int DT, int OPT>
-void launch_rank_t(const Workspace& ws, const RankPlan& P, hipStream_t st) {
+void launch_rank_t(const RankPlan& P, hipStream_t st) {
   const dim3 grid((unsigned)(P.rows * P.slices));
   if (P.vec)
-    hipLaunchKernelGGL((k_rank<DT, OPT, true>), grid, dim3(kThreads), 0, st, ws, P);
+    hipLaunchKernelGGL((k_rank<DT, OPT, true>), grid, dim3(kThreads), 0, st, P);
   else
-    hipLaunchKernelGGL((k_rank<DT, OPT, false>), grid, dim3(kThreads), 0, st, ws, P);
+    hipLaunchKernelGGL((k_rank<DT, OPT, false>), grid, dim3(kThreads), 0, st, P);
 }
 
 template <int DT>
-void launch_rank_dt(const Workspace& ws, const RankPlan& P, hipStream_t st) {
+void launch_rank_dt(const RankPlan& P, hipStream_t st) {
   switch (P.option) {
-    case 0: launch_rank_t<DT, 0>(ws, P, st); break;
-    case 1: launch_rank_t<DT, 1>(ws, P, st); break;
-    default: launch_rank_t<DT, 2>(ws, P, st); break;
+    case 0: launch_rank_t<DT, 0>(P, st); break;
+    case 1: launch_rank_t<DT, 1>(P, st); break;
+    default: launch_rank_t<DT, 2>(P, st); break;
   }
 }
 
 }  // namespace
 
-int launch_rank(const Workspace& ws, const RankPlan& P, void* stream) {
+int launch_rank(const RankPlan& P, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (P.dtype) {
-    case LSAMP_DTYPE_F32: launch_rank_dt<LSAMP_DTYPE_F32>(ws, P, st); break;
-    case LSAMP_DTYPE_BF16: launch_rank_dt<LSAMP_DTYPE_BF16>(ws, P, st); break;
-    default: launch_rank_dt<LSAMP_DTYPE_F16>(ws, P, st); break;
+    case LSAMP_DTYPE_F32: launch_rank_dt<LSAMP_DTYPE_F32>(P, st); break;
+    case LSAMP_DTYPE_BF16: launch_rank_dt<LSAMP_DTYPE_BF16>(P, st); break;
+    default: launch_rank_dt<LSAMP_DTYPE_F16>(P, st); break;
   }
   return (int)hipGetLastError();
 }

@@ -32,6 +32,7 @@ ROW_NONFINITE, ROW_EMPTY, ROW_OVERFLOW, ROW_TOKEN_RANGE = 1, 2, 4, 8
 RANK_MAX_K = 32
 VERIFY_RESIDUAL, VERIFY_EXACT, VERIFY_TYPICAL = 0, 1, 2
 MODE_AUTO, MODE_FUSED, MODE_SPLIT = 0, 1, 2
+STATE_COUNTS, STATE_REPETITION = 1, 2
 STATUS_SPIN_TIMEOUT = 1
 
 
@@ -95,6 +96,31 @@ class SampleArgs(Structure):
         ("processed", c_void_p),
         ("keep", c_void_p),
         ("stats", c_void_p),
+        ("penalty_row_len", c_void_p),
+    ]
+
+
+class PenaltyTable(Structure):
+    _fields_ = [
+        ("rows", c_int32),
+        ("capacity", c_int32),
+        ("window_capacity", c_int32),
+        ("entries", c_void_p),
+        ("row_len", c_void_p),
+        ("window_count", c_void_p),
+        ("window", c_void_p),
+        ("ring_pos", c_void_p),
+        ("window_size", c_void_p),
+        ("mode", c_void_p),
+    ]
+
+
+class CommitArgs(Structure):
+    _fields_ = [
+        ("table", PenaltyTable),
+        ("vocab", c_int32),
+        ("tokens", c_void_p),
+        ("row_flags", c_void_p),
     ]
 
 
@@ -224,6 +250,8 @@ def load_library(path: str | None = None):
     lib.lsamp_context_read_timing.restype = c_int32
     lib.lsamp_verify.argtypes = [c_void_p, POINTER(VerifyArgs), c_void_p]
     lib.lsamp_verify.restype = c_int32
+    lib.lsamp_commit.argtypes = [c_void_p, POINTER(CommitArgs), c_void_p]
+    lib.lsamp_commit.restype = c_int32
     lib.lsamp_top2.argtypes = [c_void_p, POINTER(Top2Args), c_void_p]
     lib.lsamp_top2.restype = c_int32
     lib.lsamp_logprobs.argtypes = [c_void_p, POINTER(LogprobsArgs), c_void_p]

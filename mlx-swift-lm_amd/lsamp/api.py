@@ -120,9 +120,15 @@ class Context:
                        row_ptr=None, entries=None, bitmask=None, mask_bits: Optional[int] = None,
                        mask_tail: int = _ffi.MASK_TAIL_KEEP, uniforms=None, philox_keys=None,
                        probe_tokens=None, want_processed: bool = False, want_keep: bool = False,
-                       want_stats: bool = False) -> "PreparedSample":
+                       want_stats: bool = False, table: Optional["PenaltyTable"] = None
+                       ) -> "PreparedSample":
+        """`table`: read the penalty entries from a device PenaltyTable
+        (instead of row_ptr / entries)."""
+        row_len = None
+        if table is not None:
+            row_ptr, entries, row_len = table.row_ptr, table.entries, table.row_len
         return PreparedSample(self, logits, params, semantics=semantics, vocab=vocab,
-                              row_ptr=row_ptr, entries=entries, bitmask=bitmask,
+                              row_ptr=row_ptr, entries=entries, row_len=row_len, bitmask=bitmask,
                               mask_bits=mask_bits, mask_tail=mask_tail, uniforms=uniforms,
                               philox_keys=philox_keys, probe_tokens=probe_tokens,
                               want_processed=want_processed, want_keep=want_keep,
@@ -178,7 +184,7 @@ class PreparedSample:
 
     def __init__(self, ctx: Context, logits: torch.Tensor, params, *, semantics, vocab, row_ptr,
                  entries, bitmask, mask_bits, mask_tail, uniforms, philox_keys, probe_tokens,
-                 want_processed, want_keep, want_stats):
+                 want_processed, want_keep, want_stats, row_len=None):
         dev = logits.device
         if logits.dim() != 2:
             raise ValueError("logits must be [rows, row_stride]")
@@ -222,6 +228,10 @@ class PreparedSample:
             self.keep_alive += [rp, en]
             a.penalty_row_ptr = rp.data_ptr()
             a.penalty_entries = en.data_ptr()
+            if row_len is not None:
+                rl = dev_tensor(row_len, np.int32, torch.int32)
+                self.keep_alive.append(rl)
+                a.penalty_row_len = rl.data_ptr()
         if bitmask is not None:
             bm = dev_tensor(bitmask, np.uint32, torch.int32)
             if bm.dtype != torch.int32:
@@ -331,6 +341,97 @@ class PreparedVerify:
 
     def outputs(self) -> dict:
         return {"accepted": self.accepted, "tokens": self.tokens, "accept_mask": self.accept_mask}
+
+
+class PenaltyTable:
+    """Device-resident CBv2 penalty state (the lsamp_penalty_table of
+    include/lsamp.h): per row a run of entries {token, output count,
+    REPETITION while in the window, bias}, each entry's count in the window,
+    and the repetition ring.  Built once from host histories
+    (history.Cbv2RowState), advanced on the device by `commit` after each
+    draw, and read by `Context.sample(..., table=...)`."""
+
+    def __init__(self, states, *, capacity: int, window_capacity: int, device="cuda"):
+        rows = len(states)
+        cap, wcap = int(capacity), int(window_capacity)
+        ent = np.zeros((rows, cap), PENALTY_DTYPE)
+        wcnt = np.zeros((rows, cap), np.int32)
+        win = np.full((rows, wcap), -1, np.int32)
+        row_len = np.zeros(rows, np.int32)
+        ring = np.zeros(rows, np.int32)
+        wsize = np.ones(rows, np.int32)
+        mode = np.zeros(rows, np.int32)
+        for r, st in enumerate(states):
+            e = st.entries()
+            if len(e) > cap:
+                raise ValueError(f"row {r}: {len(e)} entries exceed capacity {cap}")
+            if st.W > wcap:
+                raise ValueError(f"row {r}: window {st.W} exceeds window_capacity {wcap}")
+            ent[r, :len(e)] = e
+            row_len[r] = len(e)
+            if st.repetition_on:
+                in_win = [t for t in st.window if t >= 0]
+                for j, t in enumerate(e["token"]):
+                    wcnt[r, j] = in_win.count(int(t))
+                win[r, :st.W] = st.window
+            ring[r] = st.ring_pos
+            wsize[r] = st.W
+            mode[r] = (_ffi.STATE_COUNTS if st.counts_on else 0) | (
+                _ffi.STATE_REPETITION if st.repetition_on else 0)
+        t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(device)
+        self.rows, self.capacity, self.window_capacity = rows, cap, wcap
+        self.entries = to_device_bytes(ent.reshape(-1), device)
+        self.window_count = t(wcnt)
+        self.window = t(win)
+        self.row_len = t(row_len)
+        self.ring_pos = t(ring)
+        self.window_size = t(wsize)
+        self.mode = t(mode)
+        self.row_ptr = t(np.arange(rows + 1, dtype=np.int32) * cap)
+        tb = _ffi.PenaltyTable()
+        tb.rows, tb.capacity, tb.window_capacity = rows, cap, wcap
+        tb.entries = self.entries.data_ptr()
+        tb.row_len = self.row_len.data_ptr()
+        tb.window_count = self.window_count.data_ptr()
+        tb.window = self.window.data_ptr()
+        tb.ring_pos = self.ring_pos.data_ptr()
+        tb.window_size = self.window_size.data_ptr()
+        tb.mode = self.mode.data_ptr()
+        self._table = tb
+        self.row_flags = torch.zeros(rows, dtype=torch.int32, device=device)
+
+    def commit(self, ctx: Context, tokens: torch.Tensor, vocab: int,
+               stream: Optional[int] = None) -> torch.Tensor:
+        """LogitsPipelineV2.commit for every row (lsamp_commit); returns the
+        per-row flags (LSAMP_ROW_OVERFLOW)."""
+        if tokens.dtype != torch.int32 or tokens.numel() != self.rows:
+            raise ValueError("tokens must be an int32 tensor with one id per row")
+        a = _ffi.CommitArgs()
+        a.table = self._table
+        a.vocab = int(vocab)
+        a.tokens = tokens.data_ptr()
+        a.row_flags = self.row_flags.data_ptr()
+        s = stream if stream is not None else current_stream_handle(tokens.device)
+        st = ctx.lib.lsamp_commit(ctx.handle, ctypes.byref(a), ctypes.c_void_p(s))
+        if st != 0:
+            raise _ffi.LsampError(st, "lsamp_commit")
+        return self.row_flags
+
+    def host_rows(self):
+        """Per row: (entries sorted by token, window count by token, window,
+        ring position)."""
+        ent = self.entries.cpu().numpy().view(PENALTY_DTYPE).reshape(self.rows, self.capacity)
+        wcnt = self.window_count.cpu().numpy()
+        win = self.window.cpu().numpy()
+        n = self.row_len.cpu().numpy()
+        ring = self.ring_pos.cpu().numpy()
+        out = []
+        for r in range(self.rows):
+            e = ent[r, :n[r]]
+            order = np.argsort(e["token"], kind="stable")
+            wc = {int(e["token"][j]): int(wcnt[r, j]) for j in range(n[r])}
+            out.append((e[order], wc, win[r], int(ring[r])))
+        return out
 
 
 class PreparedRank:

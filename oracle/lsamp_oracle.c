@@ -1031,3 +1031,46 @@ int32_t lso_rank(const lso_rank_args* a) {
   free(ti);
   return 0;
 }
+
+/* ------------------------------------------------- incremental penalty state */
+
+/* buildCounts (LogitsPipelineV2.swift:478-487): ids outside [0, vocab) are
+ * skipped.  buildRepetitionWindow (:494-510): the most recent
+ * min(W, |history|) ids of prompt + output at slots 0.., -1 elsewhere; the
+ * write position is 0 when the window is full, else the first empty slot. */
+void lso_penalty_state_init(int32_t V, const int32_t* prompt, int32_t np, const int32_t* output,
+                            int32_t no, int32_t W, float* counts, float* wcounts,
+                            int32_t* window, int32_t* ring_pos) {
+  memset(counts, 0, sizeof(float) * (size_t)V);
+  memset(wcounts, 0, sizeof(float) * (size_t)V);
+  for (int32_t i = 0; i < no; ++i)
+    if (output[i] >= 0 && output[i] < V) counts[output[i]] += 1.0f;
+  const int32_t n = np + no;
+  const int32_t take = n < W ? n : W;
+  for (int32_t j = 0; j < W; ++j) window[j] = -1;
+  for (int32_t j = 0; j < take; ++j) {
+    const int32_t h = n - take + j;
+    const int32_t t = h < np ? prompt[h] : output[h - np];
+    window[j] = t >= 0 ? t : -1;
+    if (t >= 0 && t < V) wcounts[t] += 1.0f;
+  }
+  *ring_pos = take == W ? 0 : take;
+}
+
+/* commit(sampledTokens:) (LogitsPipelineV2.swift:357-384) for one row:
+ *   outputCounts[t] += 1;
+ *   evicted = window[pos]; repWindowCounts[max(evicted, 0)] -= (evicted >= 0);
+ *   repWindowCounts[t] += 1; window[pos] = t; pos = (pos + 1) % W. */
+void lso_penalty_commit(int32_t V, uint32_t mode, int32_t W, float* counts, float* wcounts,
+                        int32_t* window, int32_t* ring_pos, int32_t t) {
+  if (t < 0 || t >= V) return;
+  if (mode & LSAMP_STATE_COUNTS) counts[t] += 1.0f;
+  if (mode & LSAMP_STATE_REPETITION) {
+    const int32_t pos = *ring_pos;
+    const int32_t ev = window[pos];
+    if (ev >= 0 && ev < V) wcounts[ev] -= 1.0f;
+    wcounts[t] += 1.0f;
+    window[pos] = t;
+    *ring_pos = (pos + 1) % W;
+  }
+}

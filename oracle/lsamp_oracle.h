@@ -100,6 +100,19 @@ typedef struct lso_rank_args {
  * 534-549).  Returns 0 or < 0. */
 int32_t lso_rank(const lso_rank_args* a);
 
+/* The CBv2 incremental penalty state of one row, dense over the vocabulary
+ * (LogitsPipelineV2.setRows :238-256, buildCounts :478-487,
+ * buildRepetitionWindow :494-510): output counts, window counts, the [W]
+ * ring (-1 = empty) and its write position. */
+void lso_penalty_state_init(int32_t vocab, const int32_t* prompt, int32_t n_prompt,
+                            const int32_t* output, int32_t n_output, int32_t window_size,
+                            float* counts, float* window_counts, int32_t* window,
+                            int32_t* ring_pos);
+/* LogitsPipelineV2.commit (:357-384) of one row, dense.  mode: LSAMP_STATE_*
+ * bits; a token outside [0, vocab) commits nothing. */
+void lso_penalty_commit(int32_t vocab, uint32_t mode, int32_t window_size, float* counts,
+                        float* window_counts, int32_t* window, int32_t* ring_pos, int32_t token);
+
 /* Building blocks exposed for known-answer tests. */
 float lso_dexp(float d);
 uint64_t lso_weight(float y, float y_max, float scale);

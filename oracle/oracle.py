@@ -66,6 +66,13 @@ def lib():
         L = ctypes.CDLL(LIB_PATH)
         L.lso_sample.argtypes = [POINTER(LsoSampleArgs)]
         L.lso_sample.restype = c_int32
+        L.lso_penalty_state_init.argtypes = [c_int32, c_void_p, c_int32, c_void_p, c_int32,
+                                             c_int32, c_void_p, c_void_p, c_void_p,
+                                             POINTER(c_int32)]
+        L.lso_penalty_state_init.restype = None
+        L.lso_penalty_commit.argtypes = [c_int32, c_uint32, c_int32, c_void_p, c_void_p,
+                                         c_void_p, POINTER(c_int32), c_int32]
+        L.lso_penalty_commit.restype = None
         L.lso_rank.argtypes = [POINTER(LsoRankArgs)]
         L.lso_rank.restype = c_int32
         L.lso_verify.argtypes = [POINTER(LsoVerifyArgs)]
@@ -271,6 +278,31 @@ def rank(storage, *, dtype, k, raw_values, rows=None, vocab=None, row_stride=Non
     if tokens is None:
         del out["chosen"]
     return out
+
+
+class DenseRowState:
+    """One CBv2 row's dense penalty state (LogitsPipelineV2.swift:238-256,
+    357-384), built and advanced by the oracle."""
+
+    def __init__(self, vocab, prompt, output, window_size, mode):
+        self.V, self.W, self.mode = int(vocab), int(window_size), int(mode)
+        p = np.ascontiguousarray(prompt, np.int32)
+        o = np.ascontiguousarray(output, np.int32)
+        self.counts = np.zeros(self.V, np.float32)
+        self.window_counts = np.zeros(self.V, np.float32)
+        self.window = np.zeros(self.W, np.int32)
+        pos = c_int32(0)
+        lib().lso_penalty_state_init(self.V, _ptr(p), p.size, _ptr(o), o.size, self.W,
+                                     _ptr(self.counts), _ptr(self.window_counts),
+                                     _ptr(self.window), ctypes.byref(pos))
+        self.ring_pos = pos.value
+
+    def commit(self, token):
+        pos = c_int32(self.ring_pos)
+        lib().lso_penalty_commit(self.V, self.mode, self.W, _ptr(self.counts),
+                                 _ptr(self.window_counts), _ptr(self.window), ctypes.byref(pos),
+                                 int(token))
+        self.ring_pos = pos.value
 
 
 def dexp(d):

@@ -1,0 +1,86 @@
+"""CPU tests of the oracle's incremental penalty state (LogitsPipelineV2
+setRows / commit, LogitsPipelineV2.swift:238-256, 357-384), pinned to the
+reference's two commit tests (Tests/MLXLMTests/CBv2SamplingTests.swift:203-266)
+and to the rule those tests state: committing tokens one by one lands in the
+state a rebuild from the longer history gives.  The host builder of the
+sparse entries (lsamp.history.Cbv2RowState) is checked against it too.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from lsamp import _ffi
+from lsamp.history import Cbv2RowState
+
+BOTH = _ffi.STATE_COUNTS | _ffi.STATE_REPETITION
+V = 16
+
+
+def nz(a):
+    return {int(i): float(a[i]) for i in np.nonzero(a)[0]}
+
+
+def test_commit_with_window_eviction():
+    # CBv2SamplingTests.swift:203-238: window 2, prompt [0, 1], tokens 5, 6, 5, 7
+    st = O.DenseRowState(V, [0, 1], [], 2, BOTH)
+    for t in [5, 6, 5, 7]:
+        st.commit(t)
+    assert nz(st.counts) == {5: 2.0, 6: 1.0, 7: 1.0}
+    # "only {5, 7} may carry the repetition penalty"
+    assert nz(st.window_counts) == {5: 1.0, 7: 1.0}
+    assert st.window.tolist() == [5, 7] and st.ring_pos == 0
+
+
+def test_commit_matches_rebuild():
+    # CBv2SamplingTests.swift:240-266: window 3, prompt [1, 2, 3, 4], tokens 8, 9, 8
+    inc = O.DenseRowState(V, [1, 2, 3, 4], [], 3, BOTH)
+    for t in [8, 9, 8]:
+        inc.commit(t)
+    rebuilt = O.DenseRowState(V, [1, 2, 3, 4], [8, 9, 8], 3, BOTH)
+    assert nz(inc.counts) == nz(rebuilt.counts) == {8: 2.0, 9: 1.0}
+    assert nz(inc.window_counts) == nz(rebuilt.window_counts) == {8: 2.0, 9: 1.0}
+
+
+@pytest.mark.parametrize("W", [1, 2, 5, 40])
+@pytest.mark.parametrize("mode", [_ffi.STATE_COUNTS, _ffi.STATE_REPETITION, BOTH])
+def test_random_commits_match_rebuild_and_host_entries(W, mode):
+    rng = np.random.default_rng(W * 10 + mode)
+    prompt = rng.integers(0, V, rng.integers(0, 30)).tolist()
+    output = rng.integers(0, V, rng.integers(0, 10)).tolist()
+    inc = O.DenseRowState(V, prompt, output, W, mode)
+    host = Cbv2RowState(prompt, output, W, repetition_on=bool(mode & 2), counts_on=bool(mode & 1),
+                        vocab=V)
+    out = list(output)
+    for step in range(60):
+        t = int(rng.integers(0, V))
+        inc.commit(t)
+        host.commit(t)
+        out.append(t)
+        ref = O.DenseRowState(V, prompt, out, W, mode)
+        if mode & _ffi.STATE_COUNTS:
+            assert nz(inc.counts) == nz(ref.counts)
+        if mode & _ffi.STATE_REPETITION:
+            assert nz(inc.window_counts) == nz(ref.window_counts)
+            # the same tokens, rotated by the write position
+            rot = np.concatenate([inc.window[inc.ring_pos:], inc.window[:inc.ring_pos]])
+            hist = (prompt + out)[-W:]
+            assert rot[-len(hist):].tolist() == hist
+        e = host.entries()
+        exp = {}
+        for tok in set(nz(inc.counts)) | set(nz(inc.window_counts)):
+            cnt = int(inc.counts[tok]) if mode & _ffi.STATE_COUNTS else 0
+            fl = _ffi.PEN_REPETITION if (mode & 2) and inc.window_counts[tok] > 0 else 0
+            if cnt or fl:
+                exp[tok] = (cnt, fl)
+        assert {int(r["token"]): (int(r["count"]), int(r["flags"])) for r in e} == exp
+
+
+def test_tokens_outside_the_vocabulary_commit_nothing():
+    st = O.DenseRowState(V, [3], [3], 4, BOTH)
+    before = (st.counts.copy(), st.window_counts.copy(), st.window.copy(), st.ring_pos)
+    st.commit(-1)
+    st.commit(V)
+    assert np.array_equal(st.counts, before[0]) and np.array_equal(st.window_counts, before[1])
+    assert np.array_equal(st.window, before[2]) and st.ring_pos == before[3]
