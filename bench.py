@@ -21,6 +21,14 @@ per row.  A "step" is one lsamp_sample call over that batch.
   sorts, dense penalty tensors) timed on the host's cores on whole steps.
 
 Usage: python bench.py [--gpus 1] [--steps 1600] [--warmup 160]
+
+`--path top2 | logprobs | commit` measures one of the stage's other entry
+points on the same batch instead (one JSON line of the same shape; the
+headline line is the default `--path sample`):
+* top2: lsamp_top2 over the 64 x 151,936 bf16 logits;
+* logprobs: lsamp_logprobs of the sampled tokens and the top 20;
+* commit: lsamp_commit of one token per row into the device penalty table
+  built from the workload's histories (repetition window 64 on, counts on).
 """
 from __future__ import annotations
 
@@ -53,7 +61,129 @@ def parse():
                          "(the calibration), then --probe-steps eager steps; no timing")
     ap.add_argument("--probe-copy-mib", type=int, default=256)
     ap.add_argument("--probe-steps", type=int, default=32)
+    ap.add_argument("--path", default="sample", choices=["sample", "top2", "logprobs", "commit"])
+    ap.add_argument("--top-k", type=int, default=20, help="--path logprobs: top_k")
     return ap.parse_args()
+
+
+def bench_aux(args):
+    """One JSON line for lsamp_top2 / lsamp_logprobs / lsamp_commit on the
+    headline batch: launches per second from a HIP graph of `--copies`
+    launches over distinct input copies, the launch duration from HIP events
+    on the launch stream, and the oracle timed on the host as the baseline."""
+    import numpy as np
+    import torch
+
+    from lsamp import _ffi, workloads as W
+    from lsamp.api import Context, PenaltyTable
+    from lsamp.history import Cbv2RowState
+
+    cfg = W.config2()
+    B, V, R = cfg["rows"], cfg["vocab"], args.copies
+    steps = max(R, (args.steps + R - 1) // R * R)
+    warm = max(R, (args.warmup + R - 1) // R * R)
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(11)
+    ctx = Context(0, max_rows=B, max_vocab=V)
+    base = torch.from_numpy(cfg["logits"].view(np.int16)).view(torch.bfloat16)
+    copies = torch.empty((R, B, V), dtype=torch.bfloat16, device=dev)
+    for i in range(R):
+        copies[i].copy_(base)
+        if i:
+            idx = torch.from_numpy(rng.integers(0, V, B)).to(dev)
+            copies[i, torch.arange(B, device=dev), idx] = 0.0
+    tokens = torch.from_numpy(rng.integers(0, V, (R, B)).astype(np.int32)).to(dev)
+    if args.path == "top2":
+        preps = [ctx.prepare_top2(copies[i]) for i in range(R)]
+        launch = preps[0].launch
+        alg = B * V * 2 + B * 2 * 8
+        unit_name, kernel = "top-2 rows/s", "k_rank"
+    elif args.path == "logprobs":
+        preps = [ctx.prepare_logprobs(copies[i], tokens=tokens[i], top_k=args.top_k)
+                 for i in range(R)]
+        alg = B * V * 2 + B * 4 + B * 4 + B * args.top_k * 8 + B * 4
+        unit_name, kernel = "log-prob rows/s", "k_rank"
+    else:
+        # the workload's output histories, as a device table with room to grow
+        states = []
+        for r in range(B):
+            e = cfg["entries"][cfg["row_ptr"][r]:cfg["row_ptr"][r + 1]]
+            hist = np.repeat(e["token"], e["count"])
+            states.append(Cbv2RowState(prompt=[], output=rng.permutation(hist), repetition_window=64,
+                                       repetition_on=True, counts_on=True, vocab=V))
+        cap = max(len(st.entries()) for st in states) + steps + warm + 2 * R + 16
+        table = PenaltyTable(states, capacity=cap, window_capacity=64)
+        # tokens to commit: drawn from each row's own history (mostly repeats)
+        for r in range(B):
+            e = cfg["entries"][cfg["row_ptr"][r]:cfg["row_ptr"][r + 1]]
+            tokens[:, r] = torch.from_numpy(rng.choice(e["token"], R).astype(np.int32)).to(dev)
+
+        class _Commit:
+            def __init__(self, i):
+                self.i = i
+
+            def launch(self, stream=None):
+                table.commit(ctx, tokens[self.i], V, stream)
+        preps = [_Commit(i) for i in range(R)]
+        n_ent = int(table.row_len.sum().item())
+        alg = n_ent * 16 + B * (4 * 8 + 64 * 4)
+        unit_name, kernel = "commit rows/s", "k_commit"
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for p in preps:
+            p.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for p in preps:
+            p.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    for _ in range(warm // R):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(steps // R):
+            graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    launch_us = 1e3 * e0.elapsed_time(e1) / steps
+    achieved = alg / (launch_us * 1e-6) / 1e9
+    out = {
+        "metric": f"{unit_name} at B={B} V={V} (lsamp_{args.path})",
+        "value": B * steps / wall_s, "unit": "rows/s", "n_gpus": 1, "steps": steps,
+        "warmup": warm, "ms_per_step": 1e3 * wall_s / steps, "us_per_launch": launch_us,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u32" if args.path != "logprobs" else "f32", "data": "synthetic",
+        "config": {"workload": f"lsamp_{args.path} B={B} V={V} bf16" +
+                   (f" top_k={args.top_k}" if args.path == "logprobs" else ""),
+                   "input_copies": R},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg,
+                     "kernel": kernel, "launch_us": launch_us},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu and args.path != "commit":
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+        kw = dict(dtype=_ffi.DTYPE_BF16, k=2 if args.path == "top2" else args.top_k,
+                  raw_values=args.path == "top2",
+                  tokens=None if args.path == "top2" else tokens[0].cpu().numpy())
+        n, t0 = 0, time.perf_counter()
+        while True:
+            O.rank(cfg["logits"], **kw)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds and n >= 3:
+                break
+        out["cpu_baseline"] = {"value": B * n / el, "unit": "rows/s", "cores": 1, "kind": "port",
+                               "sample": f"{n} whole batches of {B} rows in {el:.1f} s, one thread"}
+    ctx.close()
+    print(json.dumps(out))
+    return 0
 
 
 def cpu_baseline(cfg, seconds):
@@ -92,6 +222,8 @@ def main():
         print("bench.py runs on one GPU only: the sampling stage is row-parallel and needs no "
               "collective; multi-GPU runs are not part of this build.", file=sys.stderr)
         return 2
+    if args.path != "sample":
+        return bench_aux(args)
     import numpy as np
     import torch
 

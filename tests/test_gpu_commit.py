@@ -158,3 +158,30 @@ def test_decode_loop_on_device_state_matches_host_rebuild(ctx):
             host[r].commit(int(tok_dev[r]))
         torch.cuda.synchronize()
         assert not flags.cpu().numpy().any()
+
+
+def test_rows_longer_than_the_register_scan(ctx):
+    """Rows of about 3,000 entries: the sampled and evicted tokens and the
+    run's last entry sit past the 1,024 entries the lanes hold in registers."""
+    import torch
+    from lsamp.api import PenaltyTable
+    rng = np.random.default_rng(21)
+    vocab, rows = 151936, 4
+    specs = []
+    for r in range(rows):
+        hist = rng.permutation(vocab)[:3000].tolist()
+        w = [64, 1500, 7, 1][r]
+        # 2,500 distinct output tokens (counts), or a 1,500-token window
+        specs.append((hist[:500], hist[500:], w, [BOTH, _ffi.STATE_REPETITION, BOTH,
+                                                   _ffi.STATE_COUNTS][r], {}))
+    table = PenaltyTable(states_of(specs, vocab), capacity=3200, window_capacity=1500)
+    dense = [O.DenseRowState(vocab, p, o, w, m) for p, o, w, m, _ in specs]
+    for step in range(30):
+        tok = np.array([rng.choice(specs[r][1]) if step % 3 else rng.integers(0, vocab)
+                        for r in range(rows)], np.int32)
+        table.commit(ctx, torch.from_numpy(tok).cuda(), vocab)
+        for r in range(rows):
+            dense[r].commit(int(tok[r]))
+    torch.cuda.synchronize()
+    assert (table.row_len.cpu().numpy() > 1024).all()
+    check_table(table, dense, specs, "long rows")
