@@ -225,6 +225,26 @@ typedef struct lsamp_verify_args {
                                  EXACT / TYPICAL write the target draw at every
                                  position                                      */
   uint8_t* accept_mask;       /* [S, W-1] out or NULL: per-position decision   */
+
+  /* Penalty-aware verification (CBv2DefaultSampler.applyWindowPenalties,
+   * DefaultSamplerV2.swift:503-580), EXACT and TYPICAL modes; NULL entries =
+   * none.  Each sequence's confirmed output counts as sparse entries (token,
+   * count; flags and bias are ignored: the reference's verify applies only
+   * frequency / presence), in penalty_entries[penalty_row_ptr[s] ..
+   * + penalty_row_len[s]) (or .. penalty_row_ptr[s+1] when row_len is NULL).
+   * Position j of sequence s also counts the drafts that precede it: chain
+   * positions [0, column_offset + j) of penalty_drafts ([S, drafts_stride];
+   * NULL = draft_tokens with column_offset 0), as CBv2MTPVerifyPenalties
+   * describes them (EngineLoopV2.swift:226-244).                            */
+  const int32_t* penalty_row_ptr;
+  const int32_t* penalty_row_len;
+  const lsamp_penalty_entry* penalty_entries;
+  const int32_t* penalty_drafts;
+  int32_t penalty_drafts_stride;
+  int32_t penalty_column_offset;
+  lsamp_penalty_entry* penalty_scratch; /* [S * W, penalty_scratch_cap] device */
+  int32_t penalty_scratch_cap;          /* entries per position, >= the longest
+                                           sequence run + column_offset + W - 1 */
 } lsamp_verify_args;
 
 /* ---- context ------------------------------------------------------------- */
@@ -267,6 +287,9 @@ lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode);
  * gather all slices of a row (another workload held the CUs); that step's
  * outputs are unreliable. */
 #define LSAMP_STATUS_SPIN_TIMEOUT 1u
+/* a penalty-aware verify position had more entries than penalty_scratch_cap
+ * (its outputs are unreliable) */
+#define LSAMP_STATUS_PENALTY_CAPACITY 2u
 lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
 
 /* Launch shape of the context's last lsamp_sample call (diagnostics; no

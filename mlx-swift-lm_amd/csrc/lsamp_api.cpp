@@ -59,6 +59,8 @@ struct lsamp_context {
   Workspace ws;
   RankSlice* rank_part;  // [max_rows][kRankMaxSlices] (in `block`)
   uint32_t* arrive_rank; // [max_rows] (in `block`)
+  int32_t* vrow_ptr;     // [max_rows] penalty-aware verify: per-position runs (in `block`)
+  int32_t* vrow_len;     // [max_rows] (in `block`)
   void* block;  // single device allocation backing the workspace
   size_t bytes;
   // timing hook
@@ -196,6 +198,8 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   const size_t o_vfl = take(R * sizeof(uint32_t));
   const size_t o_rpart = take(R * kRankMaxSlices * sizeof(RankSlice));
   const size_t o_arank = take(R * sizeof(uint32_t));
+  const size_t o_vrp = take(R * sizeof(int32_t));
+  const size_t o_vrl = take(R * sizeof(int32_t));
   const size_t total = off;
 
   void* block = nullptr;
@@ -233,6 +237,8 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   ws.vflags = reinterpret_cast<uint32_t*>(b + o_vfl);
   ctx->rank_part = reinterpret_cast<RankSlice*>(b + o_rpart);
   ctx->arrive_rank = reinterpret_cast<uint32_t*>(b + o_arank);
+  ctx->vrow_ptr = reinterpret_cast<int32_t*>(b + o_vrp);
+  ctx->vrow_len = reinterpret_cast<int32_t*>(b + o_vrl);
   *out = ctx;
   return ok();
 }
@@ -605,6 +611,36 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   if (rows > ctx->ws.max_rows)
     return fail(LSAMP_ERR_CAPACITY, "verify needs %lld rows, the context holds %d",
                 (long long)rows, ctx->ws.max_rows);
+  const bool penalized = a->penalty_entries != nullptr;
+  WindowEntriesPlan E{};
+  if (penalized) {
+    if (residual)
+      return fail(LSAMP_ERR_INVALID_ARGUMENT,
+                  "penalty-aware verification is for the EXACT and TYPICAL modes");
+    if (!a->penalty_row_ptr || !a->penalty_scratch || a->penalty_scratch_cap <= 0)
+      return fail(LSAMP_ERR_INVALID_ARGUMENT,
+                  "penalty_entries needs penalty_row_ptr, penalty_scratch and a positive cap");
+    const int32_t off = a->penalty_drafts ? a->penalty_column_offset : 0;
+    const int32_t stride = a->penalty_drafts ? a->penalty_drafts_stride : (int32_t)D;
+    if (off < 0 || (int64_t)off + D > 64 || (a->penalty_drafts && stride < off + D))
+      return fail(LSAMP_ERR_SHAPE,
+                  "column_offset %d / drafts_stride %d: at most 64 drafts precede a position",
+                  off, stride);
+    E.sequences = a->sequences;
+    E.window = a->window;
+    E.vocab = a->vocab;
+    E.cap = a->penalty_scratch_cap;
+    E.column_offset = off;
+    E.drafts_stride = stride;
+    E.row_ptr = a->penalty_row_ptr;
+    E.row_len = a->penalty_row_len;
+    E.entries = a->penalty_entries;
+    E.drafts = a->penalty_drafts ? a->penalty_drafts : a->draft_tokens;
+    E.out = a->penalty_scratch;
+    E.out_ptr = ctx->vrow_ptr;
+    E.out_len = ctx->vrow_len;
+    E.status = ctx->ws.status;
+  }
 
   // every target (and, for RESIDUAL, draft) position is one sampling row
   SamplePlan P{};
@@ -628,6 +664,11 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   P.params = a->params;
   P.uniforms = a->uniforms;
   P.probe_tokens = a->draft_tokens;
+  if (penalized) {
+    P.row_ptr = ctx->vrow_ptr;
+    P.row_len = ctx->vrow_len;
+    P.entries = a->penalty_scratch;
+  }
   P.tokens = ctx->ws.vtokens;
   P.row_flags = ctx->ws.vflags;
   P.stats = ctx->ws.vstats;
@@ -648,7 +689,8 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   Q.tokens = a->tokens;
   Q.accept_mask = a->accept_mask;
   DeviceGuard guard(ctx->device);
-  int err = launch_sample(ctx->ws, P, stream, nullptr);
+  int err = penalized ? launch_window_entries(E, stream) : 0;
+  if (err == 0) err = launch_sample(ctx->ws, P, stream, nullptr);
   if (err == 0) err = launch_verify_finish(ctx->ws, Q, stream);
   if (err != 0)
     return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));

@@ -190,7 +190,81 @@ __global__ __launch_bounds__(64) void k_commit(lsamp_commit_args a) {
   if (a.row_flags) a.row_flags[r] = overflow ? LSAMP_ROW_OVERFLOW : 0u;
 }
 
+// ---------------------------------------------------------------------------
+// Penalty-aware verify windows (CBv2DefaultSampler.applyWindowPenalties,
+// DefaultSamplerV2.swift:503-580).  The reference broadcasts each sequence's
+// dense [vocab] output counts over the window and adds a cumulative one-hot
+// of the drafts ([B, W, vocab] floats).  Here each window position gets a
+// sparse run of entries: the sequence's entries with their counts raised by
+// the drafts before the position, then the drafts that are not among them.
+// One wave per position; the drafts sit in LDS and every lane compares its
+// entries with all of them.
+
+constexpr int kMaxWindowDrafts = 64;
+
+__global__ __launch_bounds__(64) void k_window_entries(WindowEntriesPlan P) {
+  __shared__ int32_t drafts[kMaxWindowDrafts];
+  __shared__ unsigned long long found;  // drafts some entry matched
+  const int row = blockIdx.x, lane = threadIdx.x;
+  const int s = row / P.window, j = row - s * P.window;
+  const int nd = P.column_offset + j;  // drafts before this position
+  if (lane < nd) drafts[lane] = P.drafts[(size_t)s * (size_t)P.drafts_stride + lane];
+  if (lane == 0) found = 0ull;
+  __syncthreads();
+  const int32_t e0 = P.row_ptr[s];
+  const int32_t len = P.row_len ? P.row_len[s] : P.row_ptr[s + 1] - e0;
+  lsamp_penalty_entry* out = P.out + (size_t)row * (size_t)P.cap;
+  unsigned long long hit = 0ull;
+#pragma unroll 4
+  for (int k = lane; k < len; k += 64) {
+    const lsamp_penalty_entry e = P.entries[e0 + k];
+    int32_t add = 0;
+    for (int i = 0; i < nd; ++i) {
+      if (drafts[i] == e.token) {
+        ++add;
+        hit |= 1ull << i;
+      }
+    }
+    // counts only: the verify window applies frequency / presence alone
+    if (k < P.cap) out[k] = lsamp_penalty_entry{e.token, e.count + add, 0u, 0.0f};
+  }
+  if (hit) atomicOr(&found, hit);
+  __syncthreads();
+  if (lane != 0) return;
+  // drafts no entry holds: one new entry per distinct token, its count the
+  // number of times it occurs among the drafts before the position
+  int32_t n = len;
+  bool over = len > P.cap;
+  const unsigned long long f = found;
+  for (int i = 0; i < nd; ++i) {
+    const int32_t d = drafts[i];
+    if (((f >> i) & 1ull) || d < 0 || d >= P.vocab) continue;
+    bool seen = false;
+    int32_t c = 0;
+    for (int i2 = 0; i2 < nd; ++i2) {
+      if (drafts[i2] != d) continue;
+      if (i2 < i) seen = true;
+      ++c;
+    }
+    if (seen) continue;
+    if (n < P.cap)
+      out[n] = lsamp_penalty_entry{d, c, 0u, 0.0f};
+    else
+      over = true;
+    ++n;
+  }
+  P.out_ptr[row] = row * P.cap;
+  P.out_len[row] = n < P.cap ? n : P.cap;
+  if (over) atomicOr(P.status, kStatusPenaltyCapacity);
+}
+
 }  // namespace
+
+int launch_window_entries(const WindowEntriesPlan& plan, void* stream) {
+  hipLaunchKernelGGL(k_window_entries, dim3((unsigned)(plan.sequences * plan.window)), dim3(64), 0,
+                     reinterpret_cast<hipStream_t>(stream), plan);
+  return (int)hipGetLastError();
+}
 
 int launch_commit(const lsamp_commit_args& args, void* stream) {
   hipLaunchKernelGGL(k_commit, dim3((unsigned)args.table.rows), dim3(64), 0,

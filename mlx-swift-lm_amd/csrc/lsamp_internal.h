@@ -191,6 +191,7 @@ struct RankPlan {
 
 // Sticky device status bits.
 constexpr uint32_t kStatusSpinTimeout = 1u;  // a fused-kernel barrier wait timed out
+constexpr uint32_t kStatusPenaltyCapacity = 2u;  // a verify position's entries did not fit
 
 // Launch description resolved on the host.
 struct SamplePlan {
@@ -264,5 +265,26 @@ int launch_verify_finish(const Workspace& ws, const VerifyPlan& plan, void* stre
 int launch_rank(const RankPlan& plan, void* stream);
 // Incremental penalty-state update after a draw (lsamp_commit.hip).
 int launch_commit(const lsamp_commit_args& args, void* stream);
+
+// Per-position penalty entries of a penalty-aware verify window: row s * W + j
+// = sequence s's confirmed counts plus the drafts before chain position
+// column_offset + j (lsamp_commit.hip).
+struct WindowEntriesPlan {
+  int32_t sequences;
+  int32_t window;
+  int32_t vocab;
+  int32_t cap;            // entries per position in `out`
+  int32_t column_offset;
+  int32_t drafts_stride;
+  const int32_t* row_ptr;
+  const int32_t* row_len;  // or NULL
+  const lsamp_penalty_entry* entries;
+  const int32_t* drafts;   // [S, drafts_stride]
+  lsamp_penalty_entry* out;  // [S * W, cap]
+  int32_t* out_ptr;        // [S * W]
+  int32_t* out_len;        // [S * W]
+  uint32_t* status;        // sticky status bits
+};
+int launch_window_entries(const WindowEntriesPlan& plan, void* stream);
 
 }  // namespace lsamp

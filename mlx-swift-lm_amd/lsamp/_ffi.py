@@ -34,6 +34,7 @@ VERIFY_RESIDUAL, VERIFY_EXACT, VERIFY_TYPICAL = 0, 1, 2
 MODE_AUTO, MODE_FUSED, MODE_SPLIT = 0, 1, 2
 STATE_COUNTS, STATE_REPETITION = 1, 2
 STATUS_SPIN_TIMEOUT = 1
+STATUS_PENALTY_CAPACITY = 2
 
 
 class RowParams(Structure):
@@ -140,6 +141,14 @@ class VerifyArgs(Structure):
         ("accepted", c_void_p),
         ("tokens", c_void_p),
         ("accept_mask", c_void_p),
+        ("penalty_row_ptr", c_void_p),
+        ("penalty_row_len", c_void_p),
+        ("penalty_entries", c_void_p),
+        ("penalty_drafts", c_void_p),
+        ("penalty_drafts_stride", c_int32),
+        ("penalty_column_offset", c_int32),
+        ("penalty_scratch", c_void_p),
+        ("penalty_scratch_cap", c_int32),
     ]
 
 

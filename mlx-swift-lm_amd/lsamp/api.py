@@ -162,9 +162,17 @@ class Context:
 
     def prepare_verify(self, target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens,
                        params, uniforms, *, mode: int = _ffi.VERIFY_RESIDUAL,
-                       typical_delta: float = 0.0) -> "PreparedVerify":
+                       typical_delta: float = 0.0, penalty_row_ptr=None, penalty_entries=None,
+                       penalty_row_len=None, penalty_drafts=None, column_offset: int = 0,
+                       scratch_cap: int = 0) -> "PreparedVerify":
+        """Penalty-aware verification (EXACT / TYPICAL): `penalty_row_ptr` /
+        `penalty_entries` (/ `penalty_row_len`) hold each sequence's confirmed
+        output counts; `penalty_drafts` [S, >= column_offset + W - 1] is the
+        round's draft chain (default: draft_tokens, offset 0); `scratch_cap`
+        entries per window position (default: the longest run + drafts)."""
         return PreparedVerify(self, target, draft, draft_tokens, params, uniforms, mode,
-                              typical_delta)
+                              typical_delta, penalty_row_ptr, penalty_entries, penalty_row_len,
+                              penalty_drafts, column_offset, scratch_cap)
 
     def verify(self, target: torch.Tensor, draft: Optional[torch.Tensor], draft_tokens, params,
                uniforms, **kw) -> dict:
@@ -291,7 +299,8 @@ class PreparedVerify:
     """A fully bound lsamp_verify call (device buffers kept alive here)."""
 
     def __init__(self, ctx: Context, target, draft, draft_tokens, params, uniforms, mode,
-                 typical_delta):
+                 typical_delta, penalty_row_ptr=None, penalty_entries=None, penalty_row_len=None,
+                 penalty_drafts=None, column_offset=0, scratch_cap=0):
         if target.dim() != 3 or not target.is_contiguous():
             raise ValueError("target must be a contiguous [S, W, V] tensor")
         S, W, V = target.shape
@@ -330,6 +339,35 @@ class PreparedVerify:
         a.accepted = self.accepted.data_ptr()
         a.tokens = self.tokens.data_ptr()
         a.accept_mask = self.accept_mask.data_ptr()
+        if penalty_entries is not None:
+            rp = dev_tensor(penalty_row_ptr, np.int32)
+            if isinstance(penalty_entries, torch.Tensor):
+                en = penalty_entries.to(dev)
+                n_max = None
+            else:
+                e = np.ascontiguousarray(penalty_entries, PENALTY_DTYPE)
+                rpn = np.asarray(penalty_row_ptr, np.int64)
+                n_max = int((rpn[1:S + 1] - rpn[:S]).max()) if S else 0
+                en = to_device_bytes(e if len(e) else np.zeros(1, PENALTY_DTYPE), dev)
+            self.keep_alive += [rp, en]
+            a.penalty_row_ptr = rp.data_ptr()
+            a.penalty_entries = en.data_ptr()
+            if penalty_row_len is not None:
+                rl = dev_tensor(penalty_row_len, np.int32)
+                self.keep_alive.append(rl)
+                a.penalty_row_len = rl.data_ptr()
+            if penalty_drafts is not None:
+                pd = dev_tensor(penalty_drafts, np.int32)
+                self.keep_alive.append(pd)
+                a.penalty_drafts = pd.data_ptr()
+                a.penalty_drafts_stride = pd.shape[-1]
+                a.penalty_column_offset = int(column_offset)
+            if n_max is None and not scratch_cap:
+                raise ValueError("device penalty_entries need an explicit scratch_cap")
+            cap = int(scratch_cap) or (n_max + int(column_offset) + W)
+            self.scratch = torch.empty(S * W * cap * 16, dtype=torch.uint8, device=dev)
+            a.penalty_scratch = self.scratch.data_ptr()
+            a.penalty_scratch_cap = cap
         self.args = a
         self._byref = ctypes.byref(a)
 

@@ -745,7 +745,8 @@ int32_t lso_sample(const lso_sample_args* a) {
 /* One verify row: CBv2 transform (no penalties, no mask) and filter with the
  * sequence's params, then fixed-point weights (scale 1). */
 static void verify_row(const void* logits, int32_t dtype, int32_t V, const lsamp_row_params* p,
-                       scratch_t* s, uint64_t* w, uint64_t* W_out, float* y_out) {
+                       scratch_t* s, uint64_t* w, uint64_t* W_out, float* y_out,
+                       const int32_t* pen_rp, const lsamp_penalty_entry* pen_ent) {
   lso_sample_args a;
   memset(&a, 0, sizeof a);
   a.semantics = LSAMP_SEM_CBV2;
@@ -755,6 +756,8 @@ static void verify_row(const void* logits, int32_t dtype, int32_t V, const lsamp
   a.row_stride = V;
   a.logits = logits;
   a.params = p;
+  a.penalty_row_ptr = pen_rp;
+  a.penalty_entries = pen_ent;
   cbv2_transform(&a, 0, s);
   float* x = s->x;
   for (int32_t i = 0; i < V; ++i)
@@ -808,7 +811,9 @@ static void* verify_worker(void* arg) {
   uint64_t* wd = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
   uint64_t* res = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)V);
   float* yt = (float*)malloc(sizeof(float) * (size_t)V);
-  if (!scratch_init(&s, V) || !wt || !wd || !res || !yt) {
+  float* cnt = (float*)malloc(sizeof(float) * (size_t)V);
+  lsamp_penalty_entry* ent = (lsamp_penalty_entry*)malloc(sizeof(lsamp_penalty_entry) * (size_t)V);
+  if (!scratch_init(&s, V) || !wt || !wd || !res || !yt || !cnt || !ent) {
     vw->status = LSAMP_ERR_CAPACITY;
     goto done;
   }
@@ -827,8 +832,8 @@ static void* verify_worker(void* arg) {
         uint64_t Wt, Wd;
         const void* trow = (const char*)a->target_logits + ((size_t)sq * W + j) * (size_t)V * esz;
         const void* drow = (const char*)a->draft_logits + ((size_t)sq * D + j) * (size_t)V * esz;
-        verify_row(trow, a->dtype, V, p, &s, wt, &Wt, NULL);
-        verify_row(drow, a->dtype, V, p, &s, wd, &Wd, NULL);
+        verify_row(trow, a->dtype, V, p, &s, wt, &Wt, NULL, NULL, NULL);
+        verify_row(drow, a->dtype, V, p, &s, wd, &Wd, NULL, NULL, NULL);
         const int32_t x = drafts[j];
         const double pt = (x >= 0 && x < V && Wt) ? (double)wt[x] / (double)Wt : 0.0;
         const double pd = (x >= 0 && x < V && Wd) ? (double)wd[x] / (double)Wd : 0.0;
@@ -853,16 +858,44 @@ static void* verify_worker(void* arg) {
       if (j == D) {
         uint64_t Wt;
         const void* trow = (const char*)a->target_logits + ((size_t)sq * W + D) * (size_t)V * esz;
-        verify_row(trow, a->dtype, V, p, &s, wt, &Wt, NULL);
+        verify_row(trow, a->dtype, V, p, &s, wt, &Wt, NULL, NULL, NULL);
         tok[D] = draw_from_weights(V, wt, Wt, u[D]);
       }
       a->accepted[sq] = j;
     } else {
       int32_t prefix = 0, still = 1;
+      /* applyWindowPenalties (DefaultSamplerV2.swift:503-580) for rows with a
+       * frequency or presence penalty: counts = the confirmed output counts
+       * plus the one-hot of the drafts before the position, applied as
+       * x - f*c - p*(c > 0) (stage 2 of LogitsPipelineV2.process) */
+      const int pen = a->out_ptr && (p->frequency_penalty != 0.0f || p->presence_penalty != 0.0f);
+      if (pen) {
+        memset(cnt, 0, sizeof(float) * (size_t)V);
+        for (int32_t i = a->out_ptr[sq]; i < a->out_ptr[sq + 1]; ++i)
+          if (a->out_tokens[i] >= 0 && a->out_tokens[i] < V) cnt[a->out_tokens[i]] += 1.0f;
+      }
+      const int32_t* chain = a->pen_drafts ? a->pen_drafts + (size_t)sq * (size_t)a->pen_stride
+                                           : drafts;
+      const int32_t off = a->pen_drafts ? a->pen_offset : 0;
+      if (pen)
+        for (int32_t i = 0; i < off; ++i)
+          if (chain[i] >= 0 && chain[i] < V) cnt[chain[i]] += 1.0f;
       for (int32_t j = 0; j < W; ++j) {
         uint64_t Wt;
         const void* trow = (const char*)a->target_logits + ((size_t)sq * W + j) * (size_t)V * esz;
-        verify_row(trow, a->dtype, V, p, &s, wt, &Wt, yt);
+        int32_t rp[2] = {0, 0};
+        if (pen) {
+          if (j > 0 && chain[off + j - 1] >= 0 && chain[off + j - 1] < V) cnt[chain[off + j - 1]] += 1.0f;
+          for (int32_t i = 0; i < V; ++i)
+            if (cnt[i] > 0.0f) {
+              ent[rp[1]].token = i;
+              ent[rp[1]].count = (int32_t)cnt[i];
+              ent[rp[1]].flags = 0u;
+              ent[rp[1]].bias = 0.0f;
+              ++rp[1];
+            }
+        }
+        verify_row(trow, a->dtype, V, p, &s, wt, &Wt, yt, pen ? rp : NULL, pen ? ent : NULL);
         tok[j] = draw_from_weights(V, wt, Wt, u[j]);
         if (j >= D) continue;
         int accept;
@@ -905,6 +938,8 @@ done:
   free(wd);
   free(res);
   free(yt);
+  free(cnt);
+  free(ent);
   return NULL;
 }
 

@@ -72,6 +72,15 @@ typedef struct lso_verify_args {
   int32_t* tokens;
   uint8_t* accept_mask;
   double* typical_margin; /* [S, W-1] or NULL: p(draft) - floor (TYPICAL) */
+  /* penalty-aware windows (EXACT / TYPICAL), or NULL: each sequence's
+   * confirmed output tokens out_tokens[out_ptr[s] .. out_ptr[s+1]), and the
+   * round's draft chain pen_drafts [S, pen_stride] (NULL: draft_tokens) of
+   * which position j counts chain positions [0, pen_offset + j) */
+  const int32_t* out_ptr;
+  const int32_t* out_tokens;
+  const int32_t* pen_drafts;
+  int32_t pen_stride;
+  int32_t pen_offset;
 } lso_verify_args;
 
 /* MTP verification (RESIDUAL / EXACT / TYPICAL).  Returns 0 or < 0. */

@@ -43,6 +43,8 @@ class LsoVerifyArgs(Structure):
         ("draft_tokens", c_void_p), ("params", c_void_p), ("uniforms", c_void_p),
         ("typical_delta", c_float), ("threads", c_int32), ("accepted", c_void_p),
         ("tokens", c_void_p), ("accept_mask", c_void_p), ("typical_margin", c_void_p),
+        ("out_ptr", c_void_p), ("out_tokens", c_void_p), ("pen_drafts", c_void_p),
+        ("pen_stride", c_int32), ("pen_offset", c_int32),
     ]
 
 
@@ -208,8 +210,11 @@ def sample(*, semantics, logits, dtype, params, row_ptr=None, entries=None, bitm
 
 
 def verify(*, mode, target, draft, draft_tokens, dtype, params, uniforms, typical_delta=0.0,
-           threads=1):
-    """target [S, W, V], draft [S, W-1, V] (or None), draft_tokens [S, W-1]."""
+           threads=1, output_tokens=None, pen_drafts=None, column_offset=0):
+    """target [S, W, V], draft [S, W-1, V] (or None), draft_tokens [S, W-1].
+    output_tokens: per sequence, the confirmed output tokens (penalty-aware
+    windows); pen_drafts [S, n] the round's draft chain with the window's
+    first column at chain position column_offset."""
     target = np.ascontiguousarray(target)
     S, W, V = target.shape
     if draft is not None:
@@ -237,6 +242,21 @@ def verify(*, mode, target, draft, draft_tokens, dtype, params, uniforms, typica
     a.tokens = _ptr(out["tokens"])
     a.accept_mask = _ptr(out["accept_mask"])
     a.typical_margin = _ptr(out["typical_margin"])
+    keep = []
+    if output_tokens is not None:
+        optr = np.zeros(S + 1, np.int32)
+        optr[1:] = np.cumsum([len(t) for t in output_tokens])
+        otok = np.ascontiguousarray(np.concatenate([np.asarray(t, np.int32) for t in output_tokens])
+                                    if optr[-1] else np.zeros(1, np.int32), np.int32)
+        keep += [optr, otok]
+        a.out_ptr = _ptr(optr)
+        a.out_tokens = _ptr(otok)
+        if pen_drafts is not None:
+            pdr = np.ascontiguousarray(pen_drafts, np.int32)
+            keep.append(pdr)
+            a.pen_drafts = _ptr(pdr)
+            a.pen_stride = pdr.shape[1]
+            a.pen_offset = int(column_offset)
     st = lib().lso_verify(ctypes.byref(a))
     if st != 0:
         raise RuntimeError(f"lso_verify failed: {st}")

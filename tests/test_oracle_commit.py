@@ -84,3 +84,41 @@ def test_tokens_outside_the_vocabulary_commit_nothing():
     st.commit(V)
     assert np.array_equal(st.counts, before[0]) and np.array_equal(st.window_counts, before[1])
     assert np.array_equal(st.window, before[2]) and st.ring_pos == before[3]
+
+
+# ------------------------------------------------- penalty-aware verify windows
+@pytest.mark.parametrize("offset", [0, 2])
+def test_verify_window_counts_follow_the_drafts_before_each_position(offset):
+    """CBv2MTPPenaltyLongRunTests.swift:185-196: at window position j the
+    applied counts are a recount of the confirmed output plus a recount of the
+    draft chain's first column_offset + j tokens.  The oracle's penalty-aware
+    verify must equal an unpenalized verify of logits penalized with exactly
+    those counts (recounted here with Counter)."""
+    from collections import Counter
+    from lsamp import workloads as W
+    rng = np.random.default_rng(40 + offset)
+    S, Wn, V = 3, 4, 40
+    x = rng.normal(0, 2, (S, Wn, V)).astype(np.float32)
+    outs = [rng.integers(0, 12, rng.integers(0, 20)).tolist() for _ in range(S)]
+    chain = rng.integers(0, 12, (S, offset + Wn - 1)).astype(np.int32)
+    drafts = chain[:, offset:offset + Wn - 1]
+    u = rng.random((S, Wn), dtype=np.float32)
+    p = W.resolve_cbv2(temperature=0.9, top_k=20, presence_penalty=0.7, frequency_penalty=0.4,
+                       vocab=V)
+    params = W._params([p] * S)
+    got = O.verify(mode=_ffi.VERIFY_EXACT, target=x, draft=None, draft_tokens=drafts,
+                   dtype=_ffi.DTYPE_F32, params=params, uniforms=u, output_tokens=outs,
+                   pen_drafts=chain, column_offset=offset)
+    xp = x.copy()
+    f, pr = np.float32(0.4), np.float32(0.7)
+    for s in range(S):
+        for j in range(Wn):
+            c = Counter(outs[s]) + Counter(chain[s, :offset + j].tolist())
+            cnt = np.zeros(V, np.float32)
+            for t, n in c.items():
+                cnt[t] = n
+            xp[s, j] = (xp[s, j] - f * cnt) - pr * (cnt > 0).astype(np.float32)
+    ref = O.verify(mode=_ffi.VERIFY_EXACT, target=xp, draft=None, draft_tokens=drafts,
+                   dtype=_ffi.DTYPE_F32, params=params, uniforms=u)
+    assert np.array_equal(got["tokens"], ref["tokens"])
+    assert np.array_equal(got["accepted"], ref["accepted"])
