@@ -28,7 +28,10 @@ headline line is the default `--path sample`):
 * top2: lsamp_top2 over the 64 x 151,936 bf16 logits;
 * logprobs: lsamp_logprobs of the sampled tokens and the top 20;
 * commit: lsamp_commit of one token per row into the device penalty table
-  built from the workload's histories (repetition window 64 on, counts on).
+  built from the workload's histories (repetition window 64 on, counts on);
+* verify: lsamp_verify (EXACT mode) of 32 sequences x 4 positions of 151,936
+  bf16 target logits, T=0.8, top-p 0.95; with --penalties, presence 0.5 and
+  frequency 0.3 over 2,048-token confirmed outputs and the window's drafts.
 """
 from __future__ import annotations
 
@@ -61,7 +64,10 @@ def parse():
                          "(the calibration), then --probe-steps eager steps; no timing")
     ap.add_argument("--probe-copy-mib", type=int, default=256)
     ap.add_argument("--probe-steps", type=int, default=32)
-    ap.add_argument("--path", default="sample", choices=["sample", "top2", "logprobs", "commit"])
+    ap.add_argument("--path", default="sample",
+                    choices=["sample", "top2", "logprobs", "commit", "verify"])
+    ap.add_argument("--penalties", action="store_true",
+                    help="--path verify: penalty-aware windows")
     ap.add_argument("--top-k", type=int, default=20, help="--path logprobs: top_k")
     return ap.parse_args()
 
@@ -78,6 +84,8 @@ def bench_aux(args):
     from lsamp.api import Context, PenaltyTable
     from lsamp.history import Cbv2RowState
 
+    if args.path == "verify":
+        return bench_verify(args)
     cfg = W.config2()
     B, V, R = cfg["rows"], cfg["vocab"], args.copies
     steps = max(R, (args.steps + R - 1) // R * R)
@@ -214,6 +222,90 @@ def cpu_baseline(cfg, seconds):
     return {"value": n / el, "unit": "steps/s", "cores": threads, "kind": "port",
             "sample": f"{n} whole steps of the same workload ({cfg['rows']} rows) in {el:.1f} s, "
                       f"rows over {threads} threads; host {model}; ms/step {1e3 * el / n:.2f}"}
+
+
+def bench_verify(args):
+    """lsamp_verify on the MTP verify configuration, HIP-graph timed."""
+    import numpy as np
+    import torch
+
+    from lsamp import _ffi, workloads as W
+    from lsamp.api import Context
+    from lsamp.history import Cbv2RowState, csr
+
+    cfg = W.config5()
+    S, Wn, V = cfg["sequences"], cfg["window"], cfg["vocab"]
+    R = 4
+    steps = max(R, (args.steps + R - 1) // R * R)
+    warm = max(R, (args.warmup + R - 1) // R * R)
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(13)
+    ctx = Context(0, max_rows=S * (2 * Wn - 1), max_vocab=V)
+    base = torch.from_numpy(cfg["target"].view(np.int16)).view(torch.bfloat16)
+    copies = torch.empty((R, S, Wn, V), dtype=torch.bfloat16, device=dev)
+    for i in range(R):
+        copies[i].copy_(base)
+    drafts = rng.integers(0, V, (S, Wn - 1)).astype(np.int32)
+    params = cfg["params"]
+    kw = {}
+    alg = S * Wn * V * 2 + S * Wn * 12
+    if args.penalties:
+        p = W.resolve_cbv2(temperature=0.8, top_p=0.95, presence_penalty=0.5,
+                           frequency_penalty=0.3, vocab=V)
+        params = W._params([p] * S)
+        cdf = W._zipf_cdf(1.1, V)
+        ents = []
+        for s in range(S):
+            hist = rng.permutation(V)[W.zipf_ranks(rng, 1.1, V, 2048, cdf)]
+            ents.append(Cbv2RowState(prompt=[], output=hist, repetition_window=64,
+                                     repetition_on=False, counts_on=True, vocab=V).entries())
+        rp, en = csr(ents)
+        kw = dict(penalty_row_ptr=rp, penalty_entries=en)
+        alg += len(en) * 16 * (1 + Wn)
+    preps = [ctx.prepare_verify(copies[i], None, drafts, params, cfg["uniforms"],
+                                mode=_ffi.VERIFY_EXACT, **kw) for i in range(R)]
+    stream = torch.cuda.Stream(device=dev)
+    for p_ in preps:
+        p_.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for p_ in preps:
+            p_.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    for _ in range(warm // R):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    with torch.cuda.stream(stream):
+        for _ in range(steps // R):
+            graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall_s = time.perf_counter() - t0
+    us = 1e3 * e0.elapsed_time(e1) / steps
+    achieved = alg / (us * 1e-6) / 1e9
+    out = {
+        "metric": f"MTP verify windows/s at S={S} W={Wn} V={V} (lsamp_verify EXACT"
+                  + (", penalties)" if args.penalties else ")"),
+        "value": steps / wall_s, "unit": "verifies/s", "n_gpus": 1, "steps": steps,
+        "warmup": warm, "ms_per_step": 1e3 * wall_s / steps, "us_per_launch": us,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"] + (" pres0.5 freq0.3 2048-token outputs"
+                                                  if args.penalties else ""),
+                   "input_copies": R},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg,
+                     "kernel": "k_window_entries + k_fused + k_verify_finish" if args.penalties
+                     else "k_fused + k_verify_finish", "launch_us": us},
+        "cpu_baseline": None,
+    }
+    ctx.close()
+    print(json.dumps(out))
+    return 0
 
 
 def main():

@@ -197,12 +197,13 @@ __global__ __launch_bounds__(64) void k_commit(lsamp_commit_args a) {
 // of the drafts ([B, W, vocab] floats).  Here each window position gets a
 // sparse run of entries: the sequence's entries with their counts raised by
 // the drafts before the position, then the drafts that are not among them.
-// One wave per position; the drafts sit in LDS and every lane compares its
-// entries with all of them.
+// Four waves per position (a row's entry loads all in flight at once); the
+// drafts sit in LDS and every thread compares its entries with all of them.
 
 constexpr int kMaxWindowDrafts = 64;
+constexpr int kWindowThreads = 256;
 
-__global__ __launch_bounds__(64) void k_window_entries(WindowEntriesPlan P) {
+__global__ __launch_bounds__(kWindowThreads) void k_window_entries(WindowEntriesPlan P) {
   __shared__ int32_t drafts[kMaxWindowDrafts];
   __shared__ unsigned long long found;  // drafts some entry matched
   const int row = blockIdx.x, lane = threadIdx.x;
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(64) void k_window_entries(WindowEntriesPlan P) {
   lsamp_penalty_entry* out = P.out + (size_t)row * (size_t)P.cap;
   unsigned long long hit = 0ull;
 #pragma unroll 4
-  for (int k = lane; k < len; k += 64) {
+  for (int k = lane; k < len; k += kWindowThreads) {
     const lsamp_penalty_entry e = P.entries[e0 + k];
     int32_t add = 0;
     for (int i = 0; i < nd; ++i) {
@@ -261,8 +262,8 @@ __global__ __launch_bounds__(64) void k_window_entries(WindowEntriesPlan P) {
 }  // namespace
 
 int launch_window_entries(const WindowEntriesPlan& plan, void* stream) {
-  hipLaunchKernelGGL(k_window_entries, dim3((unsigned)(plan.sequences * plan.window)), dim3(64), 0,
-                     reinterpret_cast<hipStream_t>(stream), plan);
+  hipLaunchKernelGGL(k_window_entries, dim3((unsigned)(plan.sequences * plan.window)),
+                     dim3(kWindowThreads), 0, reinterpret_cast<hipStream_t>(stream), plan);
   return (int)hipGetLastError();
 }
 
