@@ -307,6 +307,32 @@ lsamp_status lsamp_context_last_launch(lsamp_context* ctx, lsamp_launch_info* ou
 /* Enqueue one MTP verification on `stream`. */
 lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* args, void* stream);
 
+/* ---- coupled MTP proposal ---------------------------------------------------
+ * CBv2DefaultSampler.mtpCoupledProposal (DefaultSamplerV2.swift:310-374): the
+ * draft position's token drawn with the randomness the verifier will draw
+ * that position with, so a draft distribution close to the target's proposes
+ * the token the target draws.  The reference races exponential noise over the
+ * draft's tempered probabilities and falls back to the mode when the winner
+ * is outside top-k / top-p / min-p; the verifier here draws by inverse CDF
+ * from one uniform (lsamp.h, draw rule), so the coupled proposal is the
+ * inverse-CDF draw from the draft's filtered distribution with the same
+ * uniform (greedy rows: the argmax).  Stateless transforms only, as in the
+ * reference: no penalties, no mask.  Any proposal leaves verification exact. */
+typedef struct lsamp_propose_args {
+  int32_t rows;       /* sequences                                              */
+  int32_t vocab;
+  int32_t dtype;      /* lsamp_dtype                                           */
+  int64_t row_stride; /* elements between rows (>= vocab)                       */
+  const void* logits; /* [rows, row_stride] draft logits of one chain position  */
+  const lsamp_row_params* params; /* [rows] CBv2-resolved                        */
+  const float* uniforms;          /* [rows] the uniforms the verifier draws this
+                                     position with, or NULL to use philox_keys */
+  const uint64_t* philox_keys;    /* [rows] lsamp_rng_key(seed, id, stepBase + j) */
+  int32_t* tokens;                /* [rows] out                                 */
+} lsamp_propose_args;
+
+lsamp_status lsamp_propose(lsamp_context* ctx, const lsamp_propose_args* args, void* stream);
+
 /* ---- ranking of raw logits: exact top-2 and log-probabilities -------------
  * Both calls read a row's logits once (one kernel) and order tokens as the
  * reference's shared top-2 reduction does (CBv2TopTwo.swift:29-47): value

@@ -153,6 +153,7 @@ int64_t lsamp_abi_sizeof(const char* name) {
   if (!strcmp(name, "lsamp_cbv2_params")) return (int64_t)sizeof(lsamp_cbv2_params);
   if (!strcmp(name, "lsamp_launch_info")) return (int64_t)sizeof(lsamp_launch_info);
   if (!strcmp(name, "lsamp_top2_args")) return (int64_t)sizeof(lsamp_top2_args);
+  if (!strcmp(name, "lsamp_propose_args")) return (int64_t)sizeof(lsamp_propose_args);
   if (!strcmp(name, "lsamp_penalty_table")) return (int64_t)sizeof(lsamp_penalty_table);
   if (!strcmp(name, "lsamp_commit_args")) return (int64_t)sizeof(lsamp_commit_args);
   if (!strcmp(name, "lsamp_logprobs_args")) return (int64_t)sizeof(lsamp_logprobs_args);
@@ -409,6 +410,24 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
   if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                             hipGetErrorString((hipError_t)err));
   return ok();
+}
+
+lsamp_status lsamp_propose(lsamp_context* ctx, const lsamp_propose_args* a, void* stream) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  // the draft row's own draw: one CBv2 sampling step, no penalties, no mask
+  lsamp_sample_args s{};
+  s.semantics = LSAMP_SEM_CBV2;
+  s.rows = a->rows;
+  s.vocab = a->vocab;
+  s.dtype = a->dtype;
+  s.row_stride = a->row_stride;
+  s.logits = a->logits;
+  s.params = a->params;
+  s.uniforms = a->uniforms;
+  s.philox_keys = a->philox_keys;
+  s.tokens = a->tokens;
+  return lsamp_sample(ctx, &s, stream);
 }
 
 lsamp_status lsamp_top2(lsamp_context* ctx, const lsamp_top2_args* a, void* stream) {

@@ -194,6 +194,20 @@ class LaunchInfo(Structure):
                 ("rows_per_round", c_int32), ("grid", c_int32)]
 
 
+class ProposeArgs(Structure):
+    _fields_ = [
+        ("rows", c_int32),
+        ("vocab", c_int32),
+        ("dtype", c_int32),
+        ("row_stride", c_int64),
+        ("logits", c_void_p),
+        ("params", c_void_p),
+        ("uniforms", c_void_p),
+        ("philox_keys", c_void_p),
+        ("tokens", c_void_p),
+    ]
+
+
 class Top2Args(Structure):
     _fields_ = [
         ("rows", c_int32),
@@ -259,6 +273,8 @@ def load_library(path: str | None = None):
     lib.lsamp_context_read_timing.restype = c_int32
     lib.lsamp_verify.argtypes = [c_void_p, POINTER(VerifyArgs), c_void_p]
     lib.lsamp_verify.restype = c_int32
+    lib.lsamp_propose.argtypes = [c_void_p, POINTER(ProposeArgs), c_void_p]
+    lib.lsamp_propose.restype = c_int32
     lib.lsamp_commit.argtypes = [c_void_p, POINTER(CommitArgs), c_void_p]
     lib.lsamp_commit.restype = c_int32
     lib.lsamp_top2.argtypes = [c_void_p, POINTER(Top2Args), c_void_p]

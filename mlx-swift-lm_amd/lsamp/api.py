@@ -140,6 +140,40 @@ class Context:
         return prep.outputs()
 
     # ----------------------------------------------------------------- verify
+    def propose(self, logits: torch.Tensor, params, *, uniforms=None, philox_keys=None,
+                stream: Optional[int] = None) -> torch.Tensor:
+        """Coupled MTP proposal (lsamp_propose; mtpCoupledProposal,
+        DefaultSamplerV2.swift:310-374): [rows, vocab] draft logits of one
+        chain position, drawn with the uniforms the verifier will use there."""
+        if logits.dim() != 2 or logits.stride(1) != 1:
+            raise ValueError("logits must be a [rows, vocab] view with contiguous rows")
+        rows, V = logits.shape
+        dev = logits.device
+        keep = [logits]
+        pr = params if isinstance(params, torch.Tensor) else to_device_bytes(params_array(params), dev)
+        keep.append(pr)
+        a = _ffi.ProposeArgs()
+        a.rows, a.vocab, a.dtype = rows, V, LSAMP_DTYPE[logits.dtype]
+        a.row_stride = logits.stride(0) if rows > 1 else V
+        a.logits, a.params = logits.data_ptr(), pr.data_ptr()
+        if uniforms is not None:
+            u = (uniforms.to(dev).contiguous() if isinstance(uniforms, torch.Tensor)
+                 else torch.from_numpy(np.ascontiguousarray(uniforms, np.float32)).to(dev))
+            keep.append(u)
+            a.uniforms = u.data_ptr()
+        if philox_keys is not None:
+            k = torch.from_numpy(np.asarray(philox_keys, np.uint64).view(np.int64)).to(dev)
+            keep.append(k)
+            a.philox_keys = k.data_ptr()
+        tokens = torch.empty(rows, dtype=torch.int32, device=dev)
+        a.tokens = tokens.data_ptr()
+        s = stream if stream is not None else current_stream_handle(dev)
+        st = self.lib.lsamp_propose(self.handle, ctypes.byref(a), ctypes.c_void_p(s))
+        if st != 0:
+            raise _ffi.LsampError(st, "lsamp_propose")
+        self._last_propose_keep = keep
+        return tokens
+
     def prepare_top2(self, logits: torch.Tensor) -> "PreparedRank":
         return PreparedRank(self, logits, top2=True)
 
