@@ -25,9 +25,10 @@
 // carries the value) and the chosen token's log-probability (its logit
 // travels in the record of the slice that holds it).
 //
-// Straight-line code that a work-group runs once is expensive here (cold
-// instruction cache), so the once-per-slice steps are loops over LDS rather
-// than unrolled passes over the registers.
+// Work that only the few waves holding the candidates would run (unrolled
+// passes over their registers) is a long dependent chain with nothing to
+// overlap it, so the once-per-slice steps spread their work over all the
+// threads through LDS.
 #include <hip/hip_runtime.h>
 
 #include "lsamp_device.h"
