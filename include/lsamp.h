@@ -420,6 +420,26 @@ typedef struct lsamp_commit_args {
  * row takes the slot). */
 lsamp_status lsamp_commit(lsamp_context* ctx, const lsamp_commit_args* args, void* stream);
 
+/* ---- one decode step ----------------------------------------------------------
+ * CBv2DefaultSampler.sample (DefaultSamplerV2.swift:84-181) as one call: the
+ * draw (lsamp_sample), then the penalty commit of the drawn tokens into the
+ * device table (lsamp_commit, :162), then the log-probabilities of the RAW
+ * logits for the drawn tokens and the top k (lsamp_logprobs, :167-176), all
+ * enqueued on `stream` in that order.  Graph-capturable like its parts. */
+typedef struct lsamp_step_args {
+  lsamp_sample_args sample;          /* the draw; its penalty arguments usually
+                                        point at `table` (row_ptr[r] = r * capacity,
+                                        entries, row_len)                        */
+  const lsamp_penalty_table* table;  /* or NULL: no commit                      */
+  uint32_t* commit_flags;            /* [rows] or NULL: LSAMP_ROW_OVERFLOW        */
+  int32_t logprobs_top_k;            /* -1: no log-probabilities; else 0 .. 32    */
+  float* chosen_logprob;             /* [rows] (logprobs_top_k >= 0)             */
+  float* top_logprobs;               /* [rows, logprobs_top_k]                   */
+  int32_t* top_ids;                  /* [rows, logprobs_top_k]                   */
+} lsamp_step_args;
+
+lsamp_status lsamp_step(lsamp_context* ctx, const lsamp_step_args* args, void* stream);
+
 /* ---- host-side parameter resolution (no device work) ---------------------- */
 
 /* GenerateParameters subset that drives the mlx-lm sampler/processor factory

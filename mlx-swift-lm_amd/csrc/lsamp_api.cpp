@@ -154,6 +154,7 @@ int64_t lsamp_abi_sizeof(const char* name) {
   if (!strcmp(name, "lsamp_launch_info")) return (int64_t)sizeof(lsamp_launch_info);
   if (!strcmp(name, "lsamp_top2_args")) return (int64_t)sizeof(lsamp_top2_args);
   if (!strcmp(name, "lsamp_propose_args")) return (int64_t)sizeof(lsamp_propose_args);
+  if (!strcmp(name, "lsamp_step_args")) return (int64_t)sizeof(lsamp_step_args);
   if (!strcmp(name, "lsamp_penalty_table")) return (int64_t)sizeof(lsamp_penalty_table);
   if (!strcmp(name, "lsamp_commit_args")) return (int64_t)sizeof(lsamp_commit_args);
   if (!strcmp(name, "lsamp_logprobs_args")) return (int64_t)sizeof(lsamp_logprobs_args);
@@ -409,6 +410,49 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
   const int err = launch_sample(ctx->ws, P, stream, ev);
   if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                             hipGetErrorString((hipError_t)err));
+  return ok();
+}
+
+lsamp_status lsamp_step(lsamp_context* ctx, const lsamp_step_args* a, void* stream) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  const lsamp_sample_args& sa = a->sample;
+  if (a->table && a->table->rows != sa.rows)
+    return fail(LSAMP_ERR_SHAPE, "table rows %d != sample rows %d", a->table->rows, sa.rows);
+  if (a->logprobs_top_k >= 0 && !a->chosen_logprob)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "log-probabilities need chosen_logprob");
+  // validate the later calls before enqueueing anything
+  lsamp_logprobs_args la{};
+  if (a->logprobs_top_k >= 0) {
+    la.rows = sa.rows;
+    la.vocab = sa.vocab;
+    la.dtype = sa.dtype;
+    la.row_stride = sa.row_stride;
+    la.col_stride = 1;
+    la.logits = sa.logits;
+    la.top_k = a->logprobs_top_k;
+    la.tokens = sa.tokens;
+    la.chosen = a->chosen_logprob;
+    la.top_values = a->top_logprobs;
+    la.top_ids = a->top_ids;
+    if (la.top_k > kRankMaxK || la.top_k > la.vocab)
+      return fail(LSAMP_ERR_SHAPE, "logprobs_top_k %d outside [0, min(%d, vocab)]", la.top_k,
+                  kRankMaxK);
+    if (la.top_k > 0 && (!la.top_values || !la.top_ids))
+      return fail(LSAMP_ERR_INVALID_ARGUMENT, "top_logprobs and top_ids are required");
+  }
+  lsamp_status st = lsamp_sample(ctx, &sa, stream);
+  if (st != LSAMP_OK) return st;
+  if (a->table) {
+    lsamp_commit_args c{};
+    c.table = *a->table;
+    c.vocab = sa.vocab;
+    c.tokens = sa.tokens;
+    c.row_flags = a->commit_flags;
+    st = lsamp_commit(ctx, &c, stream);
+    if (st != LSAMP_OK) return st;
+  }
+  if (a->logprobs_top_k >= 0) return lsamp_logprobs(ctx, &la, stream);
   return ok();
 }
 

@@ -194,6 +194,18 @@ class LaunchInfo(Structure):
                 ("rows_per_round", c_int32), ("grid", c_int32)]
 
 
+class StepArgs(Structure):
+    _fields_ = [
+        ("sample", SampleArgs),
+        ("table", c_void_p),
+        ("commit_flags", c_void_p),
+        ("logprobs_top_k", c_int32),
+        ("chosen_logprob", c_void_p),
+        ("top_logprobs", c_void_p),
+        ("top_ids", c_void_p),
+    ]
+
+
 class ProposeArgs(Structure):
     _fields_ = [
         ("rows", c_int32),
@@ -273,6 +285,8 @@ def load_library(path: str | None = None):
     lib.lsamp_context_read_timing.restype = c_int32
     lib.lsamp_verify.argtypes = [c_void_p, POINTER(VerifyArgs), c_void_p]
     lib.lsamp_verify.restype = c_int32
+    lib.lsamp_step.argtypes = [c_void_p, POINTER(StepArgs), c_void_p]
+    lib.lsamp_step.restype = c_int32
     lib.lsamp_propose.argtypes = [c_void_p, POINTER(ProposeArgs), c_void_p]
     lib.lsamp_propose.restype = c_int32
     lib.lsamp_commit.argtypes = [c_void_p, POINTER(CommitArgs), c_void_p]

@@ -140,6 +140,20 @@ class Context:
         return prep.outputs()
 
     # ----------------------------------------------------------------- verify
+    def prepare_step(self, logits: torch.Tensor, params, *, table: Optional["PenaltyTable"] = None,
+                     uniforms=None, philox_keys=None, logprobs_top_k: int = -1,
+                     **sample_kw) -> "PreparedStep":
+        """One decode step (lsamp_step; CBv2DefaultSampler.sample,
+        DefaultSamplerV2.swift:84-181): draw, commit into `table`, and the
+        raw log-probabilities of the drawn tokens and the top k."""
+        return PreparedStep(self, logits, params, table=table, uniforms=uniforms,
+                            philox_keys=philox_keys, logprobs_top_k=logprobs_top_k, **sample_kw)
+
+    def step(self, logits: torch.Tensor, params, **kw) -> dict:
+        prep = self.prepare_step(logits, params, **kw)
+        prep.launch()
+        return prep.outputs()
+
     def propose(self, logits: torch.Tensor, params, *, uniforms=None, philox_keys=None,
                 stream: Optional[int] = None) -> torch.Tensor:
         """Coupled MTP proposal (lsamp_propose; mtpCoupledProposal,
@@ -413,6 +427,50 @@ class PreparedVerify:
 
     def outputs(self) -> dict:
         return {"accepted": self.accepted, "tokens": self.tokens, "accept_mask": self.accept_mask}
+
+
+class PreparedStep:
+    """A fully bound lsamp_step call (draw -> commit -> log-probabilities)."""
+
+    def __init__(self, ctx: Context, logits, params, *, table, uniforms, philox_keys,
+                 logprobs_top_k, **sample_kw):
+        self.ctx = ctx
+        self.sample = ctx.prepare_sample(logits, params, semantics=_ffi.SEM_CBV2, table=table,
+                                         uniforms=uniforms, philox_keys=philox_keys, **sample_kw)
+        rows = logits.shape[0]
+        dev = logits.device
+        a = _ffi.StepArgs()
+        a.sample = self.sample.args
+        self.table = table
+        if table is not None:
+            a.table = ctypes.addressof(table._table)
+            a.commit_flags = table.row_flags.data_ptr()
+        a.logprobs_top_k = int(logprobs_top_k)
+        self.chosen = self.top_values = self.top_ids = None
+        if logprobs_top_k >= 0:
+            k = int(logprobs_top_k)
+            self.chosen = torch.empty(rows, dtype=torch.float32, device=dev)
+            self.top_values = torch.empty((rows, k), dtype=torch.float32, device=dev)
+            self.top_ids = torch.empty((rows, k), dtype=torch.int32, device=dev)
+            a.chosen_logprob = self.chosen.data_ptr()
+            a.top_logprobs = self.top_values.data_ptr() if k else None
+            a.top_ids = self.top_ids.data_ptr() if k else None
+        self.args = a
+        self._byref = ctypes.byref(a)
+
+    def launch(self, stream: Optional[int] = None) -> None:
+        s = stream if stream is not None else current_stream_handle(self.sample.tokens.device)
+        st = self.ctx.lib.lsamp_step(self.ctx.handle, self._byref, ctypes.c_void_p(s))
+        if st != 0:
+            raise _ffi.LsampError(st, "lsamp_step")
+
+    def outputs(self) -> dict:
+        out = self.sample.outputs()
+        if self.table is not None:
+            out["commit_flags"] = self.table.row_flags
+        if self.chosen is not None:
+            out.update(chosen=self.chosen, top_values=self.top_values, top_ids=self.top_ids)
+        return out
 
 
 class PenaltyTable:
