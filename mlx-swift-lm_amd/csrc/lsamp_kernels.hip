@@ -477,22 +477,6 @@ __device__ __forceinline__ int32_t key_id(uint64_t key) {
 }
 __device__ __forceinline__ float key_y(uint64_t key) { return key_to_float((uint32_t)(key >> 32)); }
 
-// Transformed value of one token read on its own (chunk scan, probe).
-template <int DT>
-__device__ __forceinline__ float token_value(const SamplePlan& P, const RowCtx& c, const lsamp_row_params& prm,
-                             int row, const char* rowp, const uint32_t* mrow, int64_t i,
-                             const float* patched, const uint8_t* has_patch) {
-  float x;
-  if (has_patch && has_patch[0]) {
-    x = patched[0];
-  } else {
-    x = load_scalar<DT>(rowp, i);
-    if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, i)) x = kNegInf;
-  }
-  if (x != x) x = kNegInf;
-  return x;
-}
-
 // Top-p bound on the mass ranked before a token, z the row's total mass (both
 // relative to the same e^q): CBv2 keeps exclusive mass <= top_p * z, a
 // non-positive top_p keeping the top token (LogitsPipelineV2.swift:199-206,
@@ -946,6 +930,14 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
         e0 = P.row_ptr[row];
         e1 = P.row_len ? e0 + P.row_len[row] : P.row_ptr[row + 1];
       }
+      // (the lane's kSlotsPerLane contiguous tokens, requested at once with
+      // the entries, ahead of the patches that need them)
+      constexpr int NV = kSlotsPerLane / Vec<DT>::N;
+      const int64_t i0 = cb + kSlotsPerLane * l;
+      uint4 lv[NV];
+#pragma unroll
+      for (int v = 0; v < NV; ++v) lv[v] = load_vec<DT>(rowp, i0 + v * Vec<DT>::N, ce, P.aligned != 0);
+#pragma unroll 4
       for (int32_t e = e0 + l; e < e1; e += 64) {
         const lsamp_penalty_entry ent = P.entries[e];
         if (ent.token < cb || ent.token >= ce) continue;
@@ -958,10 +950,16 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
       }
       __builtin_amdgcn_wave_barrier();
       const ClassRule rule = make_rule(info, c);
+      const uint32_t allow =
+          mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, (int32_t)i0, kSlotsPerLane);
+#pragma unroll
       for (int i = 0; i < kSlotsPerLane; ++i) {
         const int o = kSlotsPerLane * l + i;
-        if (cb + o >= ce) break;
-        const float x = token_value<DT>(P, c, prm, row, rowp, mrow, cb + o, &F.cx[o], &F.cent[o]);
+        if (cb + o >= ce) continue;
+        float x = F.cent[o] ? F.cx[o]
+                            : (((allow >> i) & 1u) ? vec_elem<DT>(lv[i / Vec<DT>::N], i % Vec<DT>::N)
+                                                   : kNegInf);
+        if (x != x) x = kNegInf;
         const int cls = classify(rule, x);
         if (cls == kKept || (cls == kCand && F.cflag[o]))
           F.dw[draw_slot(o)] = weight(to_filter(c, x), y_max, c.scale);
@@ -1060,9 +1058,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   const int l = tid & 63;
   const bool wave0 = tid < 64;
   const int G = P.slices;
-  const int64_t V = P.vocab;
   const int nch_row = P.nchunks;
-  const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
   const bool active = info.mode != kModeEmpty;
   uint64_t* rowchunks = ws.chunk_w + (size_t)row * (size_t)ws.max_chunks;
   Candidate* rc = ws.cands + (size_t)row * kCandCap;
