@@ -391,6 +391,7 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
   P.processed = a->processed;
   P.keep = a->keep;
   P.stats = a->stats;
+  P.stats_full = a->stats != nullptr;
   DeviceGuard guard(ctx->device);
   void* const* ev = nullptr;
   if (ctx->timing && ctx->timed < lsamp_context::kTimedCalls) {
@@ -735,6 +736,8 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   P.tokens = ctx->ws.vtokens;
   P.row_flags = ctx->ws.vflags;
   P.stats = ctx->ws.vstats;
+  // the outcome reads the kept weight and the probe's; TYPICAL also the entropy
+  P.stats_full = a->mode == LSAMP_VERIFY_TYPICAL;
   VerifyPlan Q{};
   Q.mode = a->mode;
   Q.sequences = a->sequences;

@@ -223,6 +223,7 @@ struct SamplePlan {
   int32_t mask_words;
   int32_t mask_bits;
   int32_t mask_tail;
+  int32_t stats_full;      // kept count, cut value and entropy wanted in stats
   const float* uniforms;
   const uint64_t* philox_keys;
   const int32_t* probe_tokens;

@@ -2277,13 +2277,17 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   // Kept tokens are listed (fast draw path) only when the whole row keeps at
   // most kKeptCap tokens above the cut bin; otherwise the draw scans a chunk.
   const bool list_on = info.count_above <= kKeptCap;
+  // the kept count, smallest kept value and entropy feed only the statistics
+  const bool want_stats = P.stats_full != 0;
   auto keep_token = [&](float x, int32_t id, uint64_t& part) {
     const float y = to_filter(c, x);
     const uint64_t wq = weight(y, y_max, c.scale);
     part += wq;
-    ent += (double)wq * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
-    min_kept = __builtin_fminf(min_kept, y);
-    ++n_kept;
+    if (want_stats) {
+      ent += (double)wq * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale);
+      min_kept = __builtin_fminf(min_kept, y);
+      ++n_kept;
+    }
     if (list_on) {
       const int ks = atomicAdd(&L.nlist, 1);
       if (ks < kKeptCap) {
@@ -2315,13 +2319,19 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
           kb |= (uint32_t)(cls == kKept) << e;
           cb |= (uint32_t)(cls == kCand) << e;
         }
-        for (uint32_t bits = kb | cb; bits != 0u; bits &= bits - 1u) {
-          const int e = __builtin_ctz(bits);
-          const float x = vec_elem_dyn<DT>(v, e);
-          if ((kb >> e) & 1u)
-            keep_token(x, i0 + e, part);
-          else
-            cand_token(x, i0 + e);
+        if (kb == FULL) {
+          // every element kept (wide nuclei): static element reads
+#pragma unroll
+          for (int e = 0; e < N; ++e) keep_token(vec_elem<DT>(v, e), i0 + e, part);
+        } else {
+          for (uint32_t bits = kb | cb; bits != 0u; bits &= bits - 1u) {
+            const int e = __builtin_ctz(bits);
+            const float x = vec_elem_dyn<DT>(v, e);
+            if ((kb >> e) & 1u)
+              keep_token(x, i0 + e, part);
+            else
+              cand_token(x, i0 + e);
+          }
         }
       }
       // chunk sums: a wave's quads lie in one 1024-token chunk
@@ -2369,7 +2379,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       }
     }
   }
-  {
+  if (want_stats) {
     // one exchange for the three work-group reductions
     ent = wave_sum(ent);
     min_kept = wave_min(min_kept);
@@ -2391,6 +2401,9 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       min_kept = __builtin_fminf(min_kept, L.redf[i]);
       n_kept += L.redi[i];
     }
+  } else {
+    // the chunk sums, candidates and kept list are complete past here
+    __syncthreads();
   }
 
   // publish chunk sums, candidates, kept list, partials
