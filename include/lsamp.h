@@ -440,6 +440,50 @@ typedef struct lsamp_step_args {
 
 lsamp_status lsamp_step(lsamp_context* ctx, const lsamp_step_args* args, void* stream);
 
+/* ---- grammar masks: cached rows and the step's bitmask ---------------------
+ * Replaces CBv2TokenConstraintSampler.mask (TokenConstraintSamplerV2.swift:
+ * 131-182) and its deviceMask / open rows (:187-199): the reference builds a
+ * [1, vocab] bool row per constrained request from its allowed ids (O(vocab)
+ * host work and upload), keeps up to 8 per request in an LRU, and concatenates
+ * the rows of a step.  Here a row's mask is a packed LSB-first bitmask row
+ * ((vocab + 31) / 32 words, the lsamp_sample bitmask layout) in a device pool
+ * the caller owns; one call assembles the step's [rows, words] bitmask:
+ *   row_source[r] = -1  an open row (every token allowed: all bits set);
+ *   row_source[r] = s   pool row s, built first from the row's allowed ids
+ *                       when row_build[r] != 0 (a cache miss), else as cached.
+ * A build with an id outside [0, vocab) yields an all-zero row (every logit
+ * -inf, deviceMask :189-191) and sets LSAMP_MASK_ID_RANGE in row_flags.  The
+ * impossible-state fallback (empty or out-of-range allowed ids -> the
+ * fallback id, :160-163) is the caller's rule, made before the call.
+ *
+ * The descriptors (row_source, row_build, ids_ptr, ids) are HOST arrays.  The
+ * call packs them into one of two pinned staging buffers the context owns,
+ * copies it to the device on `stream` and launches the assembly, so the host
+ * prepares step N+1's ids while step N's copy runs; it blocks only when the
+ * copied or read.  Unlike the other entry points it allocates: the staging
+ * pair on first use and again when the descriptors outgrow it (after waiting
+ * for both buffers).  Not capturable in a HIP graph (host staging).  A pool
+ * row built by a call must not be read by another row of the same call. */
+#define LSAMP_MASK_ID_RANGE 1u
+#define LSAMP_MASK_MAX_WORDS 16000 /* vocab <= 512,000 (the row sits in LDS) */
+
+typedef struct lsamp_mask_assemble_args {
+  int32_t rows;
+  int32_t vocab;
+  int32_t words;              /* (vocab + 31) / 32                               */
+  int32_t pool_rows;
+  uint32_t* pool;             /* [pool_rows, words] device, caller-owned cache     */
+  uint32_t* out;              /* [rows, words] device: the step's bitmask          */
+  uint32_t* row_flags;        /* [rows] device out or NULL                         */
+  const int32_t* row_source;  /* [rows] host: -1 open, else a pool row             */
+  const uint8_t* row_build;   /* [rows] host: 1 = build the pool row from ids      */
+  const int32_t* ids_ptr;     /* [rows + 1] host offsets into ids (build rows)     */
+  const int32_t* ids;         /* [ids_ptr[rows]] host: allowed ids, any order      */
+} lsamp_mask_assemble_args;
+
+lsamp_status lsamp_mask_assemble(lsamp_context* ctx, const lsamp_mask_assemble_args* args,
+                                 void* stream);
+
 /* ---- host-side parameter resolution (no device work) ---------------------- */
 
 /* GenerateParameters subset that drives the mlx-lm sampler/processor factory

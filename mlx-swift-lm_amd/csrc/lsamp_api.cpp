@@ -69,6 +69,16 @@ struct lsamp_context {
   int timed = 0;
   hipEvent_t* events = nullptr;  // [kTimedCalls * 3]
   lsamp_launch_info last{};      // shape of the last sample launch
+  // grammar mask descriptors: two pinned staging buffers and their device
+  // copies; done[i] follows the last assembly that read buffer i
+  struct MaskStage {
+    void* host[2] = {nullptr, nullptr};
+    void* dev[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool pending[2] = {false, false};
+    size_t cap = 0;
+    int next = 0;
+  } mstage;
 };
 
 namespace {
@@ -157,6 +167,7 @@ int64_t lsamp_abi_sizeof(const char* name) {
   if (!strcmp(name, "lsamp_step_args")) return (int64_t)sizeof(lsamp_step_args);
   if (!strcmp(name, "lsamp_penalty_table")) return (int64_t)sizeof(lsamp_penalty_table);
   if (!strcmp(name, "lsamp_commit_args")) return (int64_t)sizeof(lsamp_commit_args);
+  if (!strcmp(name, "lsamp_mask_assemble_args")) return (int64_t)sizeof(lsamp_mask_assemble_args);
   if (!strcmp(name, "lsamp_logprobs_args")) return (int64_t)sizeof(lsamp_logprobs_args);
   return -1;
 }
@@ -251,6 +262,11 @@ void lsamp_context_destroy(lsamp_context* ctx) {
     DeviceGuard guard(ctx->device);
     (void)hipDeviceSynchronize();
     (void)hipFree(ctx->block);
+    for (int i = 0; i < 2; ++i) {
+      if (ctx->mstage.host[i]) (void)hipHostFree(ctx->mstage.host[i]);
+      if (ctx->mstage.dev[i]) (void)hipFree(ctx->mstage.dev[i]);
+      if (ctx->mstage.done[i]) (void)hipEventDestroy(ctx->mstage.done[i]);
+    }
     if (ctx->events) {
       for (int i = 0; i < lsamp_context::kTimedCalls * 3; ++i) (void)hipEventDestroy(ctx->events[i]);
       delete[] ctx->events;
@@ -537,6 +553,96 @@ lsamp_status lsamp_commit(lsamp_context* ctx, const lsamp_commit_args* a, void* 
   const int err = launch_commit(*a, stream);
   if (err != 0)
     return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+  return ok();
+}
+
+// ------------------------------------------------------------- grammar masks
+
+lsamp_status lsamp_mask_assemble(lsamp_context* ctx, const lsamp_mask_assemble_args* a,
+                                 void* stream) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->rows <= 0 || a->vocab <= 0)
+    return fail(LSAMP_ERR_SHAPE, "rows %d / vocab %d must be positive", a->rows, a->vocab);
+  if (a->words != (a->vocab + 31) / 32 || a->words > LSAMP_MASK_MAX_WORDS)
+    return fail(LSAMP_ERR_SHAPE, "words %d must be (vocab + 31) / 32 = %d and at most %d",
+                a->words, (a->vocab + 31) / 32, LSAMP_MASK_MAX_WORDS);
+  if (!a->out || !a->row_source || !a->row_build || !a->ids_ptr)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "out, row_source, row_build and ids_ptr are required");
+  if (a->pool_rows < 0) return fail(LSAMP_ERR_SHAPE, "pool_rows %d is negative", a->pool_rows);
+  if (a->ids_ptr[0] != 0) return fail(LSAMP_ERR_SHAPE, "ids_ptr[0] must be 0");
+  for (int32_t r = 0; r < a->rows; ++r) {
+    const int32_t s = a->row_source[r];
+    if (s < -1 || s >= a->pool_rows)
+      return fail(LSAMP_ERR_SHAPE, "row %d: pool row %d outside [-1, %d)", r, s, a->pool_rows);
+    if (s >= 0 && !a->pool) return fail(LSAMP_ERR_INVALID_ARGUMENT, "pool is NULL");
+    if (a->row_build[r] && s < 0)
+      return fail(LSAMP_ERR_SHAPE, "row %d: a build needs a pool row", r);
+    if (a->ids_ptr[r + 1] < a->ids_ptr[r])
+      return fail(LSAMP_ERR_SHAPE, "ids_ptr decreases at row %d", r);
+  }
+  const int32_t nids = a->ids_ptr[a->rows];
+  if (nids > 0 && !a->ids) return fail(LSAMP_ERR_INVALID_ARGUMENT, "ids is NULL");
+  // staging layout: row_source | ids_ptr | ids | row_build, 16-byte aligned parts
+  const size_t b_src = align_up((size_t)a->rows * 4, 16);
+  const size_t b_ptr = align_up(((size_t)a->rows + 1) * 4, 16);
+  const size_t b_ids = align_up((size_t)nids * 4, 16);
+  const size_t bytes = b_src + b_ptr + b_ids + align_up((size_t)a->rows, 16);
+  DeviceGuard guard(ctx->device);
+  auto& m = ctx->mstage;
+  if (bytes > m.cap) {
+    // growth: wait for both buffers' readers, then reallocate
+    for (int i = 0; i < 2; ++i) {
+      if (m.pending[i]) (void)hipEventSynchronize(m.done[i]);
+      m.pending[i] = false;
+      if (m.host[i]) (void)hipHostFree(m.host[i]);
+      if (m.dev[i]) (void)hipFree(m.dev[i]);
+      m.host[i] = m.dev[i] = nullptr;
+    }
+    const size_t cap = align_up(bytes * 2 > 65536 ? bytes * 2 : 65536, 4096);
+    m.cap = 0;
+    for (int i = 0; i < 2; ++i) {
+      if (!m.done[i] && hipEventCreateWithFlags(&m.done[i], hipEventDisableTiming) != hipSuccess)
+        return fail(LSAMP_ERR_DEVICE, "hipEventCreateWithFlags failed");
+      if (hipHostMalloc(&m.host[i], cap, hipHostMallocDefault) != hipSuccess ||
+          hipMalloc(&m.dev[i], cap) != hipSuccess)
+        return fail(LSAMP_ERR_DEVICE, "mask staging allocation of %zu bytes failed", cap);
+    }
+    m.cap = cap;
+  }
+  const int slot = m.next;
+  m.next ^= 1;
+  // the buffer's previous copy and assembly (two calls ago) must be over
+  if (m.pending[slot] && hipEventSynchronize(m.done[slot]) != hipSuccess)
+    return fail(LSAMP_ERR_DEVICE, "waiting for the mask staging buffer failed");
+  char* h = static_cast<char*>(m.host[slot]);
+  memcpy(h, a->row_source, (size_t)a->rows * 4);
+  memcpy(h + b_src, a->ids_ptr, ((size_t)a->rows + 1) * 4);
+  if (nids > 0) memcpy(h + b_src + b_ptr, a->ids, (size_t)nids * 4);
+  memcpy(h + b_src + b_ptr + b_ids, a->row_build, (size_t)a->rows);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (hipMemcpyAsync(m.dev[slot], h, bytes, hipMemcpyHostToDevice, st) != hipSuccess)
+    return fail(LSAMP_ERR_DEVICE, "mask descriptor copy failed");
+  const char* d = static_cast<const char*>(m.dev[slot]);
+  MaskAssemblePlan P{};
+  P.rows = a->rows;
+  P.vocab = a->vocab;
+  P.words = a->words;
+  P.vec = (a->words % 4 == 0 && ((uintptr_t)a->out % 16) == 0 && ((uintptr_t)a->pool % 16) == 0)
+              ? 1 : 0;
+  P.pool = a->pool;
+  P.out = a->out;
+  P.row_flags = a->row_flags;
+  P.row_source = reinterpret_cast<const int32_t*>(d);
+  P.ids_ptr = reinterpret_cast<const int32_t*>(d + b_src);
+  P.ids = reinterpret_cast<const int32_t*>(d + b_src + b_ptr);
+  P.row_build = reinterpret_cast<const uint8_t*>(d + b_src + b_ptr + b_ids);
+  const int err = launch_mask_assemble(P, stream);
+  if (err != 0)
+    return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+  if (hipEventRecord(m.done[slot], st) != hipSuccess)
+    return fail(LSAMP_ERR_DEVICE, "hipEventRecord failed");
+  m.pending[slot] = true;
   return ok();
 }
 

@@ -288,4 +288,22 @@ struct WindowEntriesPlan {
 };
 int launch_window_entries(const WindowEntriesPlan& plan, void* stream);
 
+// Grammar bitmask assembly (lsamp_mask_assemble).  The descriptor arrays are
+// device copies of the caller's host arrays; vec: words % 4 == 0 and the pool
+// and output 16-byte aligned (cached and open rows copy whole vectors).
+struct MaskAssemblePlan {
+  int32_t rows;
+  int32_t vocab;
+  int32_t words;
+  int32_t vec;
+  uint32_t* pool;
+  uint32_t* out;
+  uint32_t* row_flags;
+  const int32_t* row_source;
+  const uint8_t* row_build;
+  const int32_t* ids_ptr;
+  const int32_t* ids;
+};
+int launch_mask_assemble(const MaskAssemblePlan& plan, void* stream);
+
 }  // namespace lsamp

@@ -35,6 +35,8 @@ MODE_AUTO, MODE_FUSED, MODE_SPLIT = 0, 1, 2
 STATE_COUNTS, STATE_REPETITION = 1, 2
 STATUS_SPIN_TIMEOUT = 1
 STATUS_PENALTY_CAPACITY = 2
+MASK_ID_RANGE = 1
+MASK_MAX_WORDS = 16000
 
 
 class RowParams(Structure):
@@ -122,6 +124,22 @@ class CommitArgs(Structure):
         ("vocab", c_int32),
         ("tokens", c_void_p),
         ("row_flags", c_void_p),
+    ]
+
+
+class MaskAssembleArgs(Structure):
+    _fields_ = [
+        ("rows", c_int32),
+        ("vocab", c_int32),
+        ("words", c_int32),
+        ("pool_rows", c_int32),
+        ("pool", c_void_p),
+        ("out", c_void_p),
+        ("row_flags", c_void_p),
+        ("row_source", c_void_p),
+        ("row_build", c_void_p),
+        ("ids_ptr", c_void_p),
+        ("ids", c_void_p),
     ]
 
 
@@ -291,6 +309,8 @@ def load_library(path: str | None = None):
     lib.lsamp_propose.restype = c_int32
     lib.lsamp_commit.argtypes = [c_void_p, POINTER(CommitArgs), c_void_p]
     lib.lsamp_commit.restype = c_int32
+    lib.lsamp_mask_assemble.argtypes = [c_void_p, POINTER(MaskAssembleArgs), c_void_p]
+    lib.lsamp_mask_assemble.restype = c_int32
     lib.lsamp_top2.argtypes = [c_void_p, POINTER(Top2Args), c_void_p]
     lib.lsamp_top2.restype = c_int32
     lib.lsamp_logprobs.argtypes = [c_void_p, POINTER(LogprobsArgs), c_void_p]

@@ -188,6 +188,39 @@ class Context:
         self._last_propose_keep = keep
         return tokens
 
+    def mask_pool(self, masks) -> torch.Tensor:
+        """The device pool [pool_rows, words] (int32 view of the uint32
+        words) of a lsamp.constraint.ConstraintMasks."""
+        return torch.zeros((masks.pool_rows, masks.words), dtype=torch.int32,
+                           device=f"cuda:{self.device}")
+
+    def assemble_masks(self, plan, pool: torch.Tensor, vocab: int, out: Optional[torch.Tensor] = None,
+                       row_flags: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+        """lsamp_mask_assemble (CBv2TokenConstraintSampler.mask,
+        TokenConstraintSamplerV2.swift:131-182): the step's [rows, words]
+        bitmask for lsamp_sample from a lsamp.constraint.MaskPlan."""
+        words = (vocab + 31) // 32
+        rows = plan.rows
+        if pool.dim() != 2 or pool.shape[1] != words or pool.dtype != torch.int32:
+            raise ValueError(f"pool must be int32 [pool_rows, {words}]")
+        if out is None:
+            out = torch.empty((rows, words), dtype=torch.int32, device=pool.device)
+        src = np.ascontiguousarray(plan.row_source, np.int32)
+        build = np.ascontiguousarray(plan.row_build, np.uint8)
+        ptr = np.ascontiguousarray(plan.ids_ptr, np.int32)
+        ids = np.ascontiguousarray(plan.ids, np.int32)
+        a = _ffi.MaskAssembleArgs()
+        a.rows, a.vocab, a.words, a.pool_rows = rows, vocab, words, pool.shape[0]
+        a.pool, a.out = pool.data_ptr(), out.data_ptr()
+        a.row_flags = _ptr(row_flags)
+        a.row_source, a.row_build = src.ctypes.data, build.ctypes.data
+        a.ids_ptr = ptr.ctypes.data
+        a.ids = ids.ctypes.data if len(ids) else None
+        s = stream if stream is not None else current_stream_handle(pool.device)
+        _ffi.check(self.lib.lsamp_mask_assemble(self.handle, ctypes.byref(a), s),
+                   "lsamp_mask_assemble")
+        return out
+
     def prepare_top2(self, logits: torch.Tensor) -> "PreparedRank":
         return PreparedRank(self, logits, top2=True)
 

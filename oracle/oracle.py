@@ -355,3 +355,39 @@ def rng_key(seed, rid, step):
 
 def rng_uniform(key, purpose=0):
     return lib().lso_rng_uniform(key, purpose)
+
+
+# ------------------------------------------------------------- grammar masks
+def device_mask_words(allowed, vocab):
+    """deviceMask(allowed:vocab:) (TokenConstraintSamplerV2.swift:187-193) as
+    packed LSB-first uint32 words: bit t of word t // 32 set exactly for the
+    allowed ids; an id outside [0, vocab) leaves the whole row false."""
+    words = np.zeros((vocab + 31) // 32, np.uint32)
+    allowed = [int(t) for t in allowed]
+    if all(0 <= t < vocab for t in allowed):
+        for t in allowed:
+            words[t >> 5] |= np.uint32(1 << (t & 31))
+    return words
+
+
+def assemble_masks(plan, pool, vocab):
+    """The step's bitmask from a lsamp.constraint.MaskPlan (the device
+    assembly's rule): an open row (-1) is all ones (open, :195-200); a build
+    row first stores device_mask_words of its ids in its pool row; every other
+    row copies its pool row.  Returns (out [rows, words], flags [rows]) and
+    updates `pool` [pool_rows, words] in place."""
+    words = (vocab + 31) // 32
+    out = np.zeros((plan.rows, words), np.uint32)
+    flags = np.zeros(plan.rows, np.uint32)
+    for r in range(plan.rows):
+        s = int(plan.row_source[r])
+        if s < 0:
+            out[r] = np.uint32(0xFFFFFFFF)
+            continue
+        if plan.row_build[r]:
+            ids = plan.ids[plan.ids_ptr[r]:plan.ids_ptr[r + 1]]
+            pool[s] = device_mask_words(ids, vocab)
+            if any(t < 0 or t >= vocab for t in ids):
+                flags[r] = _ffi.MASK_ID_RANGE
+        out[r] = pool[s]
+    return out, flags

@@ -47,7 +47,7 @@ def test_library_exports_every_declared_function(lib):
 @pytest.mark.parametrize("name,struct", [
     ("lsamp_row_params", _ffi.RowParams), ("lsamp_penalty_entry", _ffi.PenaltyEntry),
     ("lsamp_row_stats", _ffi.RowStats), ("lsamp_sample_args", _ffi.SampleArgs),
-    ("lsamp_verify_args", _ffi.VerifyArgs),
+    ("lsamp_verify_args", _ffi.VerifyArgs), ("lsamp_mask_assemble_args", _ffi.MaskAssembleArgs),
     ("lsamp_generate_parameters", _ffi.GenerateParameters),
     ("lsamp_cbv2_params", _ffi.Cbv2Params), ("lsamp_launch_info", _ffi.LaunchInfo)])
 def test_struct_layouts_agree(lib, name, struct):
