@@ -29,6 +29,11 @@ headline line is the default `--path sample`):
 * logprobs: lsamp_logprobs of the sampled tokens and the top 20;
 * commit: lsamp_commit of one token per row into the device penalty table
   built from the workload's histories (repetition window 64 on, counts on);
+* masks: lsamp_mask_assemble of the grammar-constrained batch (64 rows of
+  151,936 tokens; allowed sets of density 0.1%, 2%, 30%, 100% and one EOS-only
+  row): the steady state where every row's mask is cached (value), and every
+  row built from its allowed ids (the `miss` field); eager calls, since the
+  host staging cannot be captured;
 * verify: lsamp_verify (EXACT mode) of 32 sequences x 4 positions of 151,936
   bf16 target logits, T=0.8, top-p 0.95; with --penalties, presence 0.5 and
   frequency 0.3 over 2,048-token confirmed outputs and the window's drafts.
@@ -65,7 +70,7 @@ def parse():
     ap.add_argument("--probe-copy-mib", type=int, default=256)
     ap.add_argument("--probe-steps", type=int, default=32)
     ap.add_argument("--path", default="sample",
-                    choices=["sample", "top2", "logprobs", "commit", "verify"])
+                    choices=["sample", "top2", "logprobs", "commit", "verify", "masks"])
     ap.add_argument("--penalties", action="store_true",
                     help="--path verify: penalty-aware windows")
     ap.add_argument("--top-k", type=int, default=20, help="--path logprobs: top_k")
@@ -86,6 +91,8 @@ def bench_aux(args):
 
     if args.path == "verify":
         return bench_verify(args)
+    if args.path == "masks":
+        return bench_masks(args)
     cfg = W.config2()
     B, V, R = cfg["rows"], cfg["vocab"], args.copies
     steps = max(R, (args.steps + R - 1) // R * R)
@@ -189,6 +196,90 @@ def bench_aux(args):
                 break
         out["cpu_baseline"] = {"value": B * n / el, "unit": "rows/s", "cores": 1, "kind": "port",
                                "sample": f"{n} whole batches of {B} rows in {el:.1f} s, one thread"}
+    ctx.close()
+    print(json.dumps(out))
+    return 0
+
+
+def bench_masks(args):
+    """lsamp_mask_assemble on the grammar-constrained batch: per-call duration
+    from HIP events on the launch stream (descriptor copy + assembly) and
+    calls per second by the host clock, for the all-cached and all-built
+    steps; the oracle's assembly timed on the host as the baseline."""
+    import numpy as np
+    import torch
+
+    from lsamp.api import Context
+    from lsamp.constraint import ConstraintMasks, MaskPlan
+
+    B, V = 64, 151936
+    rng = np.random.default_rng(4)
+    cm = ConstraintMasks(B, V)
+    words = cm.words
+    dens = [0.001, 0.02, 0.3, 1.0]
+    sets = [np.sort(rng.choice(V, max(1, int(V * dens[r % 4])), replace=False)).astype(np.int32)
+            for r in range(B - 1)] + [np.array([151645], np.int32)]
+    ptr = np.concatenate([[0], np.cumsum([len(x) for x in sets])]).astype(np.int32)
+    ids = np.concatenate(sets)
+    src = np.arange(B, dtype=np.int32)
+    miss = MaskPlan(src, np.ones(B, np.uint8), ptr, ids)
+    hit = MaskPlan(src, np.zeros(B, np.uint8), np.zeros(B + 1, np.int32), np.zeros(0, np.int32))
+    ctx = Context(0, max_rows=B, max_vocab=V)
+    dev = torch.device("cuda", 0)
+    pool = torch.zeros((cm.pool_rows, words), dtype=torch.int32, device=dev)
+    outs = [torch.empty((B, words), dtype=torch.int32, device=dev) for _ in range(2)]
+    stream = torch.cuda.Stream(device=dev)
+    res = {}
+    for name, plan in (("miss", miss), ("hit", hit)):
+        for i in range(max(8, args.warmup // 8)):
+            ctx.assemble_masks(plan, pool, V, out=outs[i & 1], stream=stream.cuda_stream)
+        torch.cuda.synchronize()
+        n = max(16, args.steps // 4)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(n):
+            ctx.assemble_masks(plan, pool, V, out=outs[i & 1], stream=stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        res[name] = (n, wall, 1e3 * e0.elapsed_time(e1) / n)
+    row_bytes = words * 4
+    alg_hit = B * 2 * row_bytes + B * 5
+    alg_miss = 4 * len(ids) + B * 2 * row_bytes + B * 9
+    n, wall, us = res["hit"]
+    achieved = alg_hit / (us * 1e-6) / 1e9
+    nm, wallm, usm = res["miss"]
+    out = {
+        "metric": f"grammar bitmask steps/s at B={B} V={V} (lsamp_mask_assemble)",
+        "value": n / wall, "unit": "steps/s", "n_gpus": 1, "steps": n, "warmup": max(8, args.warmup // 8),
+        "ms_per_step": 1e3 * wall / n, "us_per_launch": us, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u32", "data": "synthetic",
+        "config": {"workload": f"grammar masks B={B} V={V} densities 0.1/2/30/100% + EOS-only, "
+                               "every row cached"},
+        "miss": {"steps_per_s": nm / wallm, "us_per_launch": usm, "ids": int(len(ids)),
+                 "algorithmic_bytes": alg_miss,
+                 "achieved_GBps": alg_miss / (usm * 1e-6) / 1e9},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg_hit,
+                     "kernel": "k_mask_assemble (+ descriptor copy)", "launch_us": us},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+        opool = np.zeros((cm.pool_rows, words), np.uint32)
+        O.assemble_masks(miss, opool, V)   # fills the cache rows (untimed)
+        k, t0 = 0, time.perf_counter()
+        while True:
+            O.assemble_masks(hit, opool, V)
+            k += 1
+            el = time.perf_counter() - t0
+            if el >= min(args.cpu_seconds, 5.0) and k >= 3:
+                break
+        out["cpu_baseline"] = {"value": k / el, "unit": "steps/s", "cores": 1, "kind": "port",
+                               "sample": f"{k} all-cached assemblies of the same batch in "
+                                         f"{el:.1f} s, one thread"}
     ctx.close()
     print(json.dumps(out))
     return 0

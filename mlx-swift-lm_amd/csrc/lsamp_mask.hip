@@ -5,11 +5,11 @@
 // The reference keeps a [1, vocab] bool row per cached mask and builds a miss
 // on the host (O(vocab) flags, then an upload).  Here a mask row is the packed
 // LSB-first bitmask lsamp_sample consumes, a miss uploads only the allowed
-// ids, and one work-group per output row either
-//   * sets the allowed ids' bits in an LDS copy of the row and writes the row
-//     to its pool slot and to the output (a build),
-//   * copies its pool row to the output (a cached row), or
-//   * writes all ones (an open row).
+// ids, and the work-groups of an output row either
+//   * set the allowed ids' bits in an LDS copy of the row and write the row
+//     to its pool slot and to the output (a build: one work-group),
+//   * copy its pool row to the output, four work-groups a row (a cached row), or
+//   * write all ones (an open row).
 #include <hip/hip_runtime.h>
 
 #include "lsamp_device.h"
@@ -18,40 +18,77 @@
 namespace lsamp {
 namespace {
 
-constexpr int kMaskThreads = 256;
+constexpr int kMaskThreads = 1024;
+constexpr int kMaskParts = 4;  // work-groups per row (cached and open rows split the copy)
 
 __global__ __launch_bounds__(kMaskThreads) void k_mask_assemble(MaskAssemblePlan P) {
   extern __shared__ uint32_t bits[];  // [words]: the row being built
   __shared__ int bad;
-  const int r = blockIdx.x, tid = threadIdx.x;
+  const int r = blockIdx.x / kMaskParts, part = blockIdx.x % kMaskParts;
+  const int tid = threadIdx.x;
   const int32_t src = P.row_source[r];
   const int W = P.words;
   uint32_t* out = P.out + (size_t)r * (size_t)W;
   if (src < 0 || !P.row_build[r]) {
+    // this work-group's quarter of the row
     const uint32_t* prow = src < 0 ? nullptr : P.pool + (size_t)src * (size_t)W;
     if (P.vec) {
+      const int n4 = W / 4, q0 = part * n4 / kMaskParts, q1 = (part + 1) * n4 / kMaskParts;
       uint4* o4 = reinterpret_cast<uint4*>(out);
       const uint4* p4 = reinterpret_cast<const uint4*>(prow);
       const uint4 ones = make_uint4(~0u, ~0u, ~0u, ~0u);
-      for (int i = tid; i < W / 4; i += kMaskThreads) o4[i] = prow ? p4[i] : ones;
+      for (int i = q0 + tid; i < q1; i += kMaskThreads) o4[i] = prow ? p4[i] : ones;
     } else {
-      for (int i = tid; i < W; i += kMaskThreads) out[i] = prow ? prow[i] : ~0u;
+      const int q0 = part * W / kMaskParts, q1 = (part + 1) * W / kMaskParts;
+      for (int i = q0 + tid; i < q1; i += kMaskThreads) out[i] = prow ? prow[i] : ~0u;
     }
-    if (tid == 0 && P.row_flags) P.row_flags[r] = 0u;
+    if (part == 0 && tid == 0 && P.row_flags) P.row_flags[r] = 0u;
     return;
   }
+  if (part != 0) return;  // a build is one work-group's (the row sits in its LDS)
   for (int i = tid; i < W; i += kMaskThreads) bits[i] = 0u;
   if (tid == 0) bad = 0;
   __syncthreads();
   const int32_t a = P.ids_ptr[r], b = P.ids_ptr[r + 1];
+  const int lane = tid & 63;
   bool mybad = false;
-  for (int32_t k = a + tid; k < b; k += kMaskThreads) {
-    const int32_t id = P.ids[k];
-    if (id < 0 || id >= P.vocab) {
-      mybad = true;
-      continue;
+  // 64 ids per wave and pass; lanes whose ids share a word OR their bits
+  // together first (a segmented suffix OR over runs of equal words), so a
+  // sorted dense list costs a few LDS atomics per wave instead of 64
+  constexpr int kAhead = 4;  // passes whose ids are loaded before the first is combined
+  for (int32_t k00 = a + (tid & ~63); k00 < b; k00 += kAhead * kMaskThreads) {
+    int32_t idv[kAhead];
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int32_t k = k00 + u * kMaskThreads + lane;
+      idv[u] = k < b ? P.ids[k] : 0;
     }
-    atomicOr(&bits[id >> 5], 1u << (id & 31));
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const int32_t k0 = k00 + u * kMaskThreads;  // wave-uniform
+      if (k0 >= b) break;
+      const int32_t k = k0 + lane;
+      const bool in = k < b;
+      const int32_t id = idv[u];
+      const bool ok = in && id >= 0 && id < P.vocab;
+      mybad |= in && !ok;
+      const int32_t w = ok ? (id >> 5) : -1 - lane;  // a lane without an id is a run of its own
+      uint32_t v = ok ? 1u << (id & 31) : 0u;
+      // every lane shuffles (a lane outside the exec mask would read as 0)
+      const int32_t wn = __shfl_down(w, 1, 64);
+      bool end = lane == 63 || wn != w;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t v2 = __shfl_down(v, d, 64);
+        const int e2 = __shfl_down((int)end, d, 64);
+        if (!end) {
+          v |= v2;
+          end = e2 != 0;
+        }
+      }
+      const int32_t wp = __shfl_up(w, 1, 64);
+      if (ok && (lane == 0 || wp != w)) atomicOr(&bits[w], v);
+    }
   }
   if (mybad) bad = 1;  // every writer stores the same value
   __syncthreads();
@@ -59,9 +96,9 @@ __global__ __launch_bounds__(kMaskThreads) void k_mask_assemble(MaskAssemblePlan
   const bool zero = bad != 0;
   uint32_t* prow = P.pool + (size_t)src * (size_t)W;
   for (int i = tid; i < W; i += kMaskThreads) {
-    const uint32_t w = zero ? 0u : bits[i];
-    prow[i] = w;
-    out[i] = w;
+    const uint32_t x = zero ? 0u : bits[i];
+    prow[i] = x;
+    out[i] = x;
   }
   if (tid == 0 && P.row_flags) P.row_flags[r] = zero ? LSAMP_MASK_ID_RANGE : 0u;
 }
@@ -69,7 +106,7 @@ __global__ __launch_bounds__(kMaskThreads) void k_mask_assemble(MaskAssemblePlan
 }  // namespace
 
 int launch_mask_assemble(const MaskAssemblePlan& plan, void* stream) {
-  hipLaunchKernelGGL(k_mask_assemble, dim3((unsigned)plan.rows), dim3(kMaskThreads),
+  hipLaunchKernelGGL(k_mask_assemble, dim3((unsigned)(plan.rows * kMaskParts)), dim3(kMaskThreads),
                      (size_t)plan.words * sizeof(uint32_t), reinterpret_cast<hipStream_t>(stream),
                      plan);
   return (int)hipGetLastError();
