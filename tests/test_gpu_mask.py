@@ -204,3 +204,81 @@ def test_constrained_step_matches_the_oracle(ctx):
     tok = got.cpu().numpy()
     assert np.array_equal(tok, ref)
     assert tok[-1] == 151645
+
+
+def test_chained_decode_with_redraw_equals_the_unchained_stream(ctx):
+    """DefaultSamplerV2.swift:114-127, 206-240 (redrawChainedSuccessor): step
+    N+1 is sampled before step N's token is confirmed, under masks from the
+    confirmed state with N+1's budget; rows the confirmation invalidates are
+    redrawn from the same logits and the same keys (a pure function of seed,
+    request and step) with masks from the confirmed state.  The chained
+    stream must equal the unchained one token for token.  Path constraints
+    are invalidated every step; one-state constraints stay valid."""
+    import torch
+    rows, steps, Vs = 8, 6, 151936
+    rng = np.random.default_rng(21)
+    logits = [torch.from_numpy(rng.normal(0, 3, (rows, Vs)).astype(np.float32)).cuda()
+              for _ in range(steps)]
+    params = W._params([W.resolve_cbv2(temperature=0.8, top_k=50, top_p=0.95, vocab=Vs)] * rows)
+    ids = list(range(300, 300 + rows))
+    lib = _ffi.load_library()
+
+    def keys(step):
+        return np.array([lib.lsamp_rng_key(7, i, step) for i in ids], np.uint64)
+
+    def constraints():
+        cs = []
+        for r in range(rows):
+            if r % 4 == 0:
+                cs.append(FixedTokenConstraint([int(t) for t in rng.integers(0, Vs, steps + 2)]))
+            elif r % 4 == 1:
+                cs.append(CyclicKeyedConstraint(Vs, states=1, density=0.05, seed=r))  # self-loop
+            elif r % 4 == 2:
+                cs.append(CyclicKeyedConstraint(Vs, states=3, density=0.02, seed=r))
+            else:
+                cs.append(None)
+        return cs
+
+    cons = constraints()
+
+    def draw(cm, pool, step, plan):
+        kw = {}
+        if plan is not None:
+            kw.update(bitmask=ctx.assemble_masks(plan, pool, Vs), mask_bits=Vs)
+        out = ctx.sample(logits[step], params, semantics=_ffi.SEM_CBV2, philox_keys=keys(step), **kw)
+        torch.cuda.synchronize()
+        return out["tokens"].cpu().numpy().tolist()
+
+    # unchained: mask from the confirmed state, sample, confirm
+    cm = ConstraintMasks(rows, Vs)
+    pool = ctx.mask_pool(cm)
+    cm.configure([(i, c, []) for i, c in zip(ids, cons)])
+    plain = []
+    for step in range(steps):
+        t = draw(cm, pool, step, cm.plan(ids))
+        cm.confirm(t, ids)
+        plain.append(t)
+
+    # chained: step N+1 samples before step N is confirmed
+    cm2 = ConstraintMasks(rows, Vs)
+    pool2 = ctx.mask_pool(cm2)
+    cm2.configure([(i, c, []) for i, c in zip(ids, cons)])
+    chained = [draw(cm2, pool2, 0, cm2.plan(ids))]
+    redraws = valid = 0
+    for step in range(1, steps):
+        cm2.begin_speculation()
+        spec = draw(cm2, pool2, step, cm2.plan(ids, speculative=True))
+        cm2.confirm(chained[-1], ids)
+        bad = cm2.take_invalidated()
+        if bad:
+            redraws += 1
+            t = draw(cm2, pool2, step, cm2.plan(ids))
+            for r, i in enumerate(ids):
+                if i not in bad and cons[r] is not None:
+                    assert t[r] == spec[r], f"validated row {r} changed at step {step}"
+                    valid += 1
+        else:
+            t = spec
+        chained.append(t)
+    assert chained == plain
+    assert redraws == steps - 1 and valid > 0
