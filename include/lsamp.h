@@ -460,7 +460,9 @@ lsamp_status lsamp_step(lsamp_context* ctx, const lsamp_step_args* args, void* s
  * call packs them into one of two pinned staging buffers the context owns,
  * copies it to the device on `stream` and launches the assembly, so the host
  * prepares step N+1's ids while step N's copy runs; it blocks only when the
- * copied or read.  Unlike the other entry points it allocates: the staging
+ * copied or read.  A step with no builds and at most 256 rows skips the
+ * staging: its pool rows travel in the kernel arguments.  Unlike the other
+ * entry points it allocates: the staging
  * pair on first use and again when the descriptors outgrow it (after waiting
  * for both buffers).  Not capturable in a HIP graph (host staging).  A pool
  * row built by a call must not be read by another row of the same call. */

@@ -583,12 +583,32 @@ lsamp_status lsamp_mask_assemble(lsamp_context* ctx, const lsamp_mask_assemble_a
   }
   const int32_t nids = a->ids_ptr[a->rows];
   if (nids > 0 && !a->ids) return fail(LSAMP_ERR_INVALID_ARGUMENT, "ids is NULL");
+  DeviceGuard guard(ctx->device);
+  MaskAssemblePlan P{};
+  P.rows = a->rows;
+  P.vocab = a->vocab;
+  P.words = a->words;
+  P.vec = (a->words % 4 == 0 && ((uintptr_t)a->out % 16) == 0 && ((uintptr_t)a->pool % 16) == 0)
+              ? 1 : 0;
+  P.pool = a->pool;
+  P.out = a->out;
+  P.row_flags = a->row_flags;
+  bool any_build = false;
+  for (int32_t r = 0; r < a->rows; ++r) any_build |= a->row_build[r] != 0;
+  if (!any_build && a->rows <= kMaskInlineRows) {
+    // every row cached or open: the pool rows travel in the kernel arguments
+    P.inline_rows = a->rows;
+    memcpy(P.src_inline, a->row_source, (size_t)a->rows * 4);
+    const int err = launch_mask_assemble(P, stream);
+    if (err != 0)
+      return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+    return ok();
+  }
   // staging layout: row_source | ids_ptr | ids | row_build, 16-byte aligned parts
   const size_t b_src = align_up((size_t)a->rows * 4, 16);
   const size_t b_ptr = align_up(((size_t)a->rows + 1) * 4, 16);
   const size_t b_ids = align_up((size_t)nids * 4, 16);
   const size_t bytes = b_src + b_ptr + b_ids + align_up((size_t)a->rows, 16);
-  DeviceGuard guard(ctx->device);
   auto& m = ctx->mstage;
   if (bytes > m.cap) {
     // growth: wait for both buffers' readers, then reallocate
@@ -624,15 +644,6 @@ lsamp_status lsamp_mask_assemble(lsamp_context* ctx, const lsamp_mask_assemble_a
   if (hipMemcpyAsync(m.dev[slot], h, bytes, hipMemcpyHostToDevice, st) != hipSuccess)
     return fail(LSAMP_ERR_DEVICE, "mask descriptor copy failed");
   const char* d = static_cast<const char*>(m.dev[slot]);
-  MaskAssemblePlan P{};
-  P.rows = a->rows;
-  P.vocab = a->vocab;
-  P.words = a->words;
-  P.vec = (a->words % 4 == 0 && ((uintptr_t)a->out % 16) == 0 && ((uintptr_t)a->pool % 16) == 0)
-              ? 1 : 0;
-  P.pool = a->pool;
-  P.out = a->out;
-  P.row_flags = a->row_flags;
   P.row_source = reinterpret_cast<const int32_t*>(d);
   P.ids_ptr = reinterpret_cast<const int32_t*>(d + b_src);
   P.ids = reinterpret_cast<const int32_t*>(d + b_src + b_ptr);

@@ -288,6 +288,8 @@ struct WindowEntriesPlan {
 };
 int launch_window_entries(const WindowEntriesPlan& plan, void* stream);
 
+constexpr int kMaskInlineRows = 256;
+
 // Grammar bitmask assembly (lsamp_mask_assemble).  The descriptor arrays are
 // device copies of the caller's host arrays; vec: words % 4 == 0 and the pool
 // and output 16-byte aligned (cached and open rows copy whole vectors).
@@ -303,6 +305,10 @@ struct MaskAssemblePlan {
   const uint8_t* row_build;
   const int32_t* ids_ptr;
   const int32_t* ids;
+  // a step with no builds and at most kMaskInlineRows rows carries its pool
+  // rows here (no descriptor copy); inline_rows = 0 otherwise
+  int32_t inline_rows;
+  int32_t src_inline[kMaskInlineRows];
 };
 int launch_mask_assemble(const MaskAssemblePlan& plan, void* stream);
 

@@ -26,10 +26,10 @@ __global__ __launch_bounds__(kMaskThreads) void k_mask_assemble(MaskAssemblePlan
   __shared__ int bad;
   const int r = blockIdx.x / kMaskParts, part = blockIdx.x % kMaskParts;
   const int tid = threadIdx.x;
-  const int32_t src = P.row_source[r];
+  const int32_t src = P.inline_rows ? P.src_inline[r] : P.row_source[r];
   const int W = P.words;
   uint32_t* out = P.out + (size_t)r * (size_t)W;
-  if (src < 0 || !P.row_build[r]) {
+  if (src < 0 || P.inline_rows || !P.row_build[r]) {
     // this work-group's quarter of the row
     const uint32_t* prow = src < 0 ? nullptr : P.pool + (size_t)src * (size_t)W;
     if (P.vec) {
@@ -37,10 +37,16 @@ __global__ __launch_bounds__(kMaskThreads) void k_mask_assemble(MaskAssemblePlan
       uint4* o4 = reinterpret_cast<uint4*>(out);
       const uint4* p4 = reinterpret_cast<const uint4*>(prow);
       const uint4 ones = make_uint4(~0u, ~0u, ~0u, ~0u);
-      for (int i = q0 + tid; i < q1; i += kMaskThreads) o4[i] = prow ? p4[i] : ones;
+      if (prow)
+        for (int i = q0 + tid; i < q1; i += kMaskThreads) o4[i] = p4[i];
+      else
+        for (int i = q0 + tid; i < q1; i += kMaskThreads) o4[i] = ones;
     } else {
       const int q0 = part * W / kMaskParts, q1 = (part + 1) * W / kMaskParts;
-      for (int i = q0 + tid; i < q1; i += kMaskThreads) out[i] = prow ? prow[i] : ~0u;
+      if (prow)
+        for (int i = q0 + tid; i < q1; i += kMaskThreads) out[i] = prow[i];
+      else
+        for (int i = q0 + tid; i < q1; i += kMaskThreads) out[i] = ~0u;
     }
     if (part == 0 && tid == 0 && P.row_flags) P.row_flags[r] = 0u;
     return;
@@ -66,7 +72,7 @@ __global__ __launch_bounds__(kMaskThreads) void k_mask_assemble(MaskAssemblePlan
 #pragma unroll
     for (int u = 0; u < kAhead; ++u) {
       const int32_t k0 = k00 + u * kMaskThreads;  // wave-uniform
-      if (k0 >= b) break;
+      if (k0 >= b) continue;
       const int32_t k = k0 + lane;
       const bool in = k < b;
       const int32_t id = idv[u];

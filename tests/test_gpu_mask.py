@@ -282,3 +282,32 @@ def test_chained_decode_with_redraw_equals_the_unchained_stream(ctx):
         chained.append(t)
     assert chained == plain
     assert redraws == steps - 1 and valid > 0
+
+
+@pytest.mark.parametrize("rows", [64, 256, 300])
+def test_all_cached_steps_inline_and_staged(ctx, rows):
+    """A step with no builds and at most 256 rows passes its pool rows in the
+    kernel arguments; a larger one goes through the staging buffers.  Both
+    equal the oracle's assembly after a building step."""
+    import torch
+    rng = np.random.default_rng(rows)
+    Vs, P = 20000, rows + 8
+    words = (Vs + 31) // 32
+    pool = torch.zeros((P, words), dtype=torch.int32, device="cuda")
+    opool = np.zeros((P, words), np.uint32)
+    sizes = rng.integers(1, 3000, P)
+    ptr = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    ids = rng.integers(0, Vs, int(ptr[-1])).astype(np.int32)
+    build = MaskPlan(np.arange(P, dtype=np.int32), np.ones(P, np.uint8), ptr, ids)
+    ctx.assemble_masks(build, pool, Vs)
+    O.assemble_masks(build, opool, Vs)
+    src = rng.integers(0, P, rows).astype(np.int32)
+    src[rng.random(rows) < 0.2] = -1
+    cached = MaskPlan(src, np.zeros(rows, np.uint8), np.zeros(rows + 1, np.int32),
+                      np.zeros(0, np.int32))
+    flags = torch.full((rows,), 9, dtype=torch.int32, device="cuda")
+    got = ctx.assemble_masks(cached, pool, Vs, row_flags=flags)
+    want, _ = O.assemble_masks(cached, opool, Vs)
+    torch.cuda.synchronize()
+    assert np.array_equal(as_u32(got), want)
+    assert not flags.cpu().numpy().any()
