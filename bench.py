@@ -22,6 +22,20 @@ per row.  A "step" is one lsamp_sample call over that batch.
 
 Usage: python bench.py [--gpus 1] [--steps 1600] [--warmup 160]
 
+Exactly `--steps` steps are timed after exactly `--warmup` untimed ones: the
+graph of `--copies` steps is replayed as often as it fits, and a graph of
+the first `steps % copies` steps runs the rest.
+
+`--path c1 | c3 | c4 | c5` measures the other configurations of the metric
+(one JSON line each, same shape, with roofline and cpu_baseline):
+* c1: one mlx-lm row of 151,936 fp32 logits, repetition 1.1 over 20, T=0.7,
+  top-p 0.9 (latency-bound: also the synchronized single-launch latency);
+* c3: the continuous-batching mixed step, 256 rows of 262,144 bf16 logits;
+* c4: the grammar-constrained step, 64 rows of 151,936 fp32 logits with
+  bitmasks (0.1% .. 100% and an EOS-only row), repetition 1.1 over 20;
+* c5: textbook speculative verification (RESIDUAL) of 32 sequences x 4
+  positions, target [32,4,V] and draft [32,3,V] bf16, T=0.8, top-p 0.95.
+
 `--path top2 | logprobs | commit` measures one of the stage's other entry
 points on the same batch instead (one JSON line of the same shape; the
 headline line is the default `--path sample`):
@@ -60,7 +74,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=160)
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--kernel-steps", type=int, default=512)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="time budget of each CPU baseline figure (all threads, one thread)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic", default=os.path.join(REPO, "profiles", "traffic_c2.json"),
                     help="measured HBM traffic per launch (rocprofv3 --pmc summary)")
@@ -70,11 +85,116 @@ def parse():
     ap.add_argument("--probe-copy-mib", type=int, default=256)
     ap.add_argument("--probe-steps", type=int, default=32)
     ap.add_argument("--path", default="sample",
-                    choices=["sample", "top2", "logprobs", "commit", "verify", "masks"])
+                    choices=["sample", "c1", "c3", "c4", "c5", "top2", "logprobs", "commit",
+                             "verify", "masks"])
     ap.add_argument("--penalties", action="store_true",
                     help="--path verify: penalty-aware windows")
     ap.add_argument("--top-k", type=int, default=20, help="--path logprobs: top_k")
     return ap.parse_args()
+
+
+def graph_runner(launches, stream):
+    """`launches`: callables, each enqueueing one step on `stream`.  Returns
+    run(n), which enqueues exactly n steps: a graph of all of them replayed
+    n // len(launches) times, then a graph of the first n % len(launches)."""
+    import torch
+    R = len(launches)
+    graphs = {}
+
+    def graph_of(k):
+        if k not in graphs:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for f in launches[:k]:
+                    f()
+            torch.cuda.synchronize()
+            graphs[k] = g
+        return graphs[k]
+
+    def prepare(*counts):
+        for n in counts:
+            if n >= R:
+                graph_of(R)
+            if n % R:
+                graph_of(n % R)
+
+    def run(n):
+        full, rem = divmod(n, R)
+        with torch.cuda.stream(stream):
+            for _ in range(full):
+                graph_of(R).replay()
+            if rem:
+                graph_of(rem).replay()
+
+    run.prepare = prepare
+    return run
+
+
+def time_steps(run, stream, steps, warmup):
+    """Warm-up, then exactly `steps` steps bracketed by synchronizations;
+    (wall seconds, HIP-event milliseconds on `stream`)."""
+    import torch
+    run.prepare(steps, warmup)
+    run(warmup)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    run(steps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, e0.elapsed_time(e1)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_baseline_of(step, rows, seconds, unit="steps/s", per_step=1.0):
+    """The oracle as the CPU baseline: step(threads, nrows) runs one whole step
+    on the first nrows rows.  Median of up to 20 timed runs after up to 3
+    warm-ups, each figure bounded by `seconds`: with every thread of the box's
+    share (min(16, nproc)) over all rows, and with one thread over as many
+    rows as fit the budget (scaled to the whole step).  value = per_step /
+    median seconds of a whole step."""
+    nproc = os.cpu_count() or 1
+    threads = max(1, min(16, nproc))
+
+    def figure(th, nrows):
+        t0 = time.perf_counter()
+        step(th, nrows)
+        first = time.perf_counter() - t0
+        warm = 0 if first * 4 > seconds else 2
+        for _ in range(warm):
+            step(th, nrows)
+        ts, t_all = [], time.perf_counter()
+        while len(ts) < 20 and (time.perf_counter() - t_all) < seconds or len(ts) < 3:
+            t0 = time.perf_counter()
+            step(th, nrows)
+            ts.append(time.perf_counter() - t0)
+        med = sorted(ts)[len(ts) // 2]
+        return med * rows / nrows, len(ts), warm + 1
+
+    t_all, n_all, w_all = figure(threads, rows)
+    # one thread: enough rows for about a second per run
+    per_row = t_all * threads / rows
+    n1 = int(max(1, min(rows, 1.0 / max(per_row, 1e-6))))
+    t_one, n_one, w_one = figure(1, n1)
+    return {"value": per_step / t_all, "unit": unit, "cores": threads, "kind": "port",
+            "nproc": nproc, "host": cpu_model(),
+            "sample": f"median of {n_all} whole steps ({rows} rows) after {w_all} warm-up(s), "
+                      f"rows over {threads} threads; ms/step {1e3 * t_all:.2f}",
+            "one_thread": {"value": per_step / t_one, "unit": unit,
+                           "sample": f"median of {n_one} runs over {n1} of {rows} rows after "
+                                     f"{w_one} warm-up(s), scaled to the step; "
+                                     f"ms/step {1e3 * t_one:.2f}"}}
 
 
 def bench_aux(args):
@@ -93,10 +213,13 @@ def bench_aux(args):
         return bench_verify(args)
     if args.path == "masks":
         return bench_masks(args)
+    if args.path in ("c1", "c3", "c4"):
+        return bench_config(args, int(args.path[1]))
+    if args.path == "c5":
+        return bench_c5(args)
     cfg = W.config2()
     B, V, R = cfg["rows"], cfg["vocab"], args.copies
-    steps = max(R, (args.steps + R - 1) // R * R)
-    warm = max(R, (args.warmup + R - 1) // R * R)
+    steps, warm = args.steps, args.warmup
     dev = torch.device("cuda", 0)
     rng = np.random.default_rng(11)
     ctx = Context(0, max_rows=B, max_vocab=V)
@@ -148,24 +271,9 @@ def bench_aux(args):
         for p in preps:
             p.launch(stream.cuda_stream)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for p in preps:
-            p.launch(stream.cuda_stream)
-    torch.cuda.synchronize()
-    for _ in range(warm // R):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    with torch.cuda.stream(stream):
-        for _ in range(steps // R):
-            graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall_s = time.perf_counter() - t0
-    launch_us = 1e3 * e0.elapsed_time(e1) / steps
+    run = graph_runner([(lambda p=p: p.launch(stream.cuda_stream)) for p in preps], stream)
+    wall_s, ev_ms = time_steps(run, stream, steps, warm)
+    launch_us = 1e3 * ev_ms / steps
     achieved = alg / (launch_us * 1e-6) / 1e9
     out = {
         "metric": f"{unit_name} at B={B} V={V} (lsamp_{args.path})",
@@ -231,10 +339,10 @@ def bench_masks(args):
     stream = torch.cuda.Stream(device=dev)
     res = {}
     for name, plan in (("miss", miss), ("hit", hit)):
-        for i in range(max(8, args.warmup // 8)):
+        for i in range(args.warmup):
             ctx.assemble_masks(plan, pool, V, out=outs[i & 1], stream=stream.cuda_stream)
         torch.cuda.synchronize()
-        n = max(16, args.steps // 4)
+        n = args.steps
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         e0.record(stream)
@@ -252,7 +360,7 @@ def bench_masks(args):
     nm, wallm, usm = res["miss"]
     out = {
         "metric": f"grammar bitmask steps/s at B={B} V={V} (lsamp_mask_assemble)",
-        "value": n / wall, "unit": "steps/s", "n_gpus": 1, "steps": n, "warmup": max(8, args.warmup // 8),
+        "value": n / wall, "unit": "steps/s", "n_gpus": 1, "steps": n, "warmup": args.warmup,
         "ms_per_step": 1e3 * wall / n, "us_per_launch": us, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "u32", "data": "synthetic",
         "config": {"workload": f"grammar masks B={B} V={V} densities 0.1/2/30/100% + EOS-only, "

@@ -108,6 +108,9 @@ typedef enum lsamp_mask_tail {
                                   context's candidate capacity; token = -1   */
 #define LSAMP_ROW_TOKEN_RANGE 8u /* lsamp_logprobs: the row's token lies outside
                                     [0, vocab); its log-probability is NaN  */
+#define LSAMP_ROW_TIMEOUT 16u    /* a fused step's bounded wait for the row's other
+                                    slices gave up (another workload held the
+                                    CUs); token = -1 (fail closed)           */
 
 /* ---- per-row inputs ------------------------------------------------------- */
 
@@ -190,7 +193,19 @@ typedef struct lsamp_sample_args {
    * penalty_row_ptr[r] + penalty_row_len[r]) instead of .. penalty_row_ptr[r+1]
    * (a fixed-capacity table that lsamp_commit keeps up to date)             */
   const int32_t* penalty_row_len;
+
+  /* [n_suppress] or NULL: token ids masked to -inf in every row, after the
+   * penalties and the bitmask (SuppressTokensProcessor.process,
+   * Libraries/MLXLMCommon/SuppressTokens.swift:67-81, chained last by
+   * GenerationComponents.swift:126-141).  Any order; negative ids and ids >=
+   * vocab are ignored, as the reference drops them.  Applied at the bitmask's
+   * position in both semantics (both write -inf, so the order between them
+   * does not change a value).                                               */
+  const int32_t* suppress_ids;
+  int32_t n_suppress; /* 0 .. LSAMP_MAX_SUPPRESS                             */
 } lsamp_sample_args;
+
+#define LSAMP_MAX_SUPPRESS 65536
 
 /* ---- MTP verification ----------------------------------------------------- */
 typedef enum lsamp_verify_mode {
@@ -252,7 +267,14 @@ typedef struct lsamp_context lsamp_context;
 
 /* Allocates the device workspace for up to `max_rows` rows of up to
  * `max_vocab` logits on `device` (and for MTP verification of up to
- * max_rows target+draft rows).  The step functions allocate nothing. */
+ * max_rows target+draft rows).  The step functions allocate nothing.
+ *
+ * Every entry point that takes a context uses its workspace (arrival
+ * counters, candidate lists, slice summaries, the suppress bitmask, the mask
+ * staging pair), so calls on one context must be ordered on ONE stream: two
+ * calls in flight on different streams with the same context race.  Use one
+ * context per concurrent stream.  The reference's caller is single-threaded
+ * for the same reason (one engine queue). */
 lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_vocab,
                                   lsamp_context** out);
 void lsamp_context_destroy(lsamp_context* ctx);
@@ -284,13 +306,20 @@ lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode);
 
 /* Sticky device-side status bits raised since the last read (waits for the
  * device); clears them.  LSAMP_STATUS_SPIN_TIMEOUT: a fused step could not
- * gather all slices of a row (another workload held the CUs); that step's
- * outputs are unreliable. */
+ * gather all slices of a row (another workload held the CUs); the affected
+ * rows carry LSAMP_ROW_TIMEOUT and token -1 in the same step's outputs. */
 #define LSAMP_STATUS_SPIN_TIMEOUT 1u
 /* a penalty-aware verify position had more entries than penalty_scratch_cap
  * (its outputs are unreliable) */
 #define LSAMP_STATUS_PENALTY_CAPACITY 2u
 lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
+
+/* Test hook of the fused arrangement's bounded waits, process-wide on
+ * `device`: polls > 0 makes every wait's target unreachable and gives it up
+ * after `polls` polls, so the fail-closed path (LSAMP_ROW_TIMEOUT) runs while
+ * every kernel exits normally; 0 restores normal waits.  Synchronous; not for
+ * use while other calls are in flight. */
+lsamp_status lsamp_set_spin_test(int32_t device, int32_t polls);
 
 /* Launch shape of the context's last lsamp_sample call (diagnostics; no
  * device work): fused (1) or split (0), slices per row, tokens per slice,

@@ -61,6 +61,8 @@ struct lsamp_context {
   uint32_t* arrive_rank; // [max_rows] (in `block`)
   int32_t* vrow_ptr;     // [max_rows] penalty-aware verify: per-position runs (in `block`)
   int32_t* vrow_len;     // [max_rows] (in `block`)
+  uint32_t* smask;       // [max_rows][smask_words] bitmask with suppressed ids (in `block`)
+  int32_t smask_words;
   void* block;  // single device allocation backing the workspace
   size_t bytes;
   // timing hook
@@ -213,6 +215,8 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   const size_t o_arank = take(R * sizeof(uint32_t));
   const size_t o_vrp = take(R * sizeof(int32_t));
   const size_t o_vrl = take(R * sizeof(int32_t));
+  const size_t smask_words = (size_t)((max_vocab + 31) / 32);
+  const size_t o_smask = take(R * smask_words * sizeof(uint32_t));
   const size_t total = off;
 
   void* block = nullptr;
@@ -252,6 +256,8 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   ctx->arrive_rank = reinterpret_cast<uint32_t*>(b + o_arank);
   ctx->vrow_ptr = reinterpret_cast<int32_t*>(b + o_vrp);
   ctx->vrow_len = reinterpret_cast<int32_t*>(b + o_vrl);
+  ctx->smask = reinterpret_cast<uint32_t*>(b + o_smask);
+  ctx->smask_words = (int32_t)smask_words;
   *out = ctx;
   return ok();
 }
@@ -292,6 +298,17 @@ lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits) {
       hipMemcpy(ctx->ws.status, &zero, sizeof zero, hipMemcpyHostToDevice) != hipSuccess)
     return fail(LSAMP_ERR_DEVICE, "reading the device status failed");
   *bits = v;
+  return ok();
+}
+
+lsamp_status lsamp_set_spin_test(int32_t device, int32_t polls) {
+  if (polls < 0) return fail(LSAMP_ERR_INVALID_ARGUMENT, "polls %d is negative", polls);
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
+    return fail(LSAMP_ERR_DEVICE, "device %d not available (%d devices)", device, ndev);
+  DeviceGuard guard(device);
+  if (set_spin_test(polls) != 0 || hipDeviceSynchronize() != hipSuccess)
+    return fail(LSAMP_ERR_DEVICE, "setting the wait test hook failed");
   return ok();
 }
 
@@ -375,6 +392,11 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
     if (a->mask_tail != LSAMP_MASK_TAIL_KEEP && a->mask_tail != LSAMP_MASK_TAIL_FORBID)
       return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown mask_tail %d", a->mask_tail);
   }
+  if (a->n_suppress < 0 || a->n_suppress > LSAMP_MAX_SUPPRESS)
+    return fail(LSAMP_ERR_SHAPE, "n_suppress %d outside [0, %d]", a->n_suppress,
+                LSAMP_MAX_SUPPRESS);
+  if (a->n_suppress > 0 && !a->suppress_ids)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "suppress_ids is NULL");
   SamplePlan P{};
   P.semantics = a->semantics;
   P.rows = a->rows;
@@ -409,6 +431,28 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
   P.stats = a->stats;
   P.stats_full = a->stats != nullptr;
   DeviceGuard guard(ctx->device);
+  if (a->n_suppress > 0) {
+    // the suppressed ids and the caller's bitmask become one bitmask over
+    // the whole vocabulary, which the sampling kernels apply as any other
+    SuppressPlan S{};
+    S.rows = a->rows;
+    S.vocab = a->vocab;
+    S.words = (a->vocab + 31) / 32;
+    S.bitmask = a->bitmask;
+    S.mask_words = a->mask_words;
+    S.mask_bits = a->mask_bits;
+    S.mask_tail = a->mask_tail;
+    S.ids = a->suppress_ids;
+    S.n = a->n_suppress;
+    S.out = ctx->smask;
+    const int err = launch_suppress_mask(S, stream);
+    if (err != 0)
+      return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+    P.bitmask = ctx->smask;
+    P.mask_words = S.words;
+    P.mask_bits = a->vocab;
+    P.mask_tail = LSAMP_MASK_TAIL_KEEP;
+  }
   void* const* ev = nullptr;
   if (ctx->timing && ctx->timed < lsamp_context::kTimedCalls) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;

@@ -105,7 +105,7 @@ struct SelectPartial {
   int32_t n_cand;    // candidates this slice produced
   int32_t n_list;    // kept tokens listed (> kKeptCap: list incomplete)
   int32_t overflow;  // entry-table overflow in this slice
-  int32_t pad;
+  int32_t timeout;   // this slice's bounded wait for the row's other slices gave up
 };
 
 struct Candidate {
@@ -191,6 +191,10 @@ struct RankPlan {
 
 // Sticky device status bits.
 constexpr uint32_t kStatusSpinTimeout = 1u;  // a fused-kernel barrier wait timed out
+// Test hook of the fused kernel's bounded waits (set by lsamp_set_spin_test):
+// 0 = normal; n > 0 = every wait's target is unreachable and it gives up after
+// n polls, so the fail-closed path runs while every kernel still exits.
+int set_spin_test(int32_t polls);
 constexpr uint32_t kStatusPenaltyCapacity = 2u;  // a verify position's entries did not fit
 
 // Launch description resolved on the host.
@@ -311,5 +315,22 @@ struct MaskAssemblePlan {
   int32_t src_inline[kMaskInlineRows];
 };
 int launch_mask_assemble(const MaskAssemblePlan& plan, void* stream);
+
+// Suppressed ids folded into a step's bitmask: out[r] = the caller's row r
+// (its tail policy resolved; all ones without a bitmask) with the bits of the
+// suppressed ids cleared, over (vocab + 31) / 32 words per row.
+struct SuppressPlan {
+  int32_t rows;
+  int32_t vocab;
+  int32_t words;            // (vocab + 31) / 32
+  const uint32_t* bitmask;  // caller's [rows, mask_words] or NULL
+  int32_t mask_words;
+  int32_t mask_bits;
+  int32_t mask_tail;
+  const int32_t* ids;       // [n]
+  int32_t n;
+  uint32_t* out;            // [rows, words]
+};
+int launch_suppress_mask(const SuppressPlan& plan, void* stream);
 
 }  // namespace lsamp

@@ -38,6 +38,27 @@ using namespace dev;
 
 constexpr int kSliceWords = kMaxSliceLen / 32;       // penalty bitmap words
 constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
+// lsamp_set_spin_test: > 0 makes every bounded wait's target unreachable and
+// its limit this many polls (the waits' fail-closed path, under test)
+__device__ int32_t g_spin_test = 0;
+
+// A bounded wait of the fused kernel (thread 0): until `*counter` reaches
+// `target`; false when it gave up (the sticky status bit is raised).
+__device__ __forceinline__ bool spin_until(const Workspace& ws, const uint32_t* counter,
+                                           uint32_t target) {
+  const int32_t test = __hip_atomic_load(&g_spin_test, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t tgt = test > 0 ? 0xffffffffu : target;
+  const int lim = test > 0 ? test : kSpinLimit;
+  int it = 0;
+  while (ld_coherent(counter) < tgt) {
+    if (++it >= lim) {
+      atomicOr(ws.status, kStatusSpinTimeout);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return true;
+}
 // Buckets of the short-list finalize's counting sort (by a key's high word);
 // their counts and starts live in the thread-maximum histogram.
 constexpr int kRankBuckets = 512;
@@ -468,6 +489,7 @@ struct TaskLds {
   int32_t nlist;
   int32_t nitems;
   int32_t last;
+  int32_t tmo;  // this task's bounded wait gave up
   uint32_t flags;
 };
 
@@ -741,6 +763,7 @@ __device__ __forceinline__ uint64_t cand_key(float y, int32_t id) {
 struct TailIn {
   int nc;           // candidates in F.keys, sorted by cand_key descending
   bool overflow;    // the row's keep set could not be resolved
+  bool timeout;     // a slice's wait for the others gave up (fail closed)
   double ent_all;   // kept tokens outside the candidates: entropy numerator,
   float min_all;    //   smallest kept value,
   int32_t kept_all; //   count
@@ -1016,7 +1039,10 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
 
   if (l == 0) {
     uint32_t flags = info.flags;
-    if (overflow) flags |= LSAMP_ROW_OVERFLOW;
+    if (t.timeout)
+      flags |= LSAMP_ROW_TIMEOUT;
+    else if (overflow)
+      flags |= LSAMP_ROW_OVERFLOW;
     if (!overflow && (token < 0 || W == 0ull)) flags |= LSAMP_ROW_EMPTY;
     const int tok = overflow ? -1 : token;
     P.tokens[row] = tok;
@@ -1079,6 +1105,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
       part.n_cand = ld_coherent(&sp->n_cand);
       part.n_list = ld_coherent(&sp->n_list);
       part.overflow = ld_coherent(&sp->overflow);
+      part.timeout = ld_coherent(&sp->timeout);
     }
 #pragma unroll
     for (int i = 0; i < kChunksPerLane; ++i) {
@@ -1109,7 +1136,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   double ent_all = 0.0;
   float min_all = kPosInf;
   int32_t kept_all = 0;
-  bool overflow = false;
+  bool overflow = false, timeout = false;
   int nc = 0;
   if (wave0) {
     const bool in = l < G;
@@ -1117,8 +1144,9 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
     min_all = wave_min(in ? part.min_kept : kPosInf);
     kept_all = wave_sum(in ? part.n_kept : 0);
     const int32_t ov = wave_max(in && (part.n_cand > kWgCandCap || part.overflow) ? 1 : 0);
+    timeout = __ballot(in && part.timeout != 0) != 0ull;
     overflow = (info.flags & LSAMP_ROW_OVERFLOW) != 0 || ov != 0 || total_cand > kCandCap;
-    nc = (overflow || !active) ? 0 : total_cand;
+    nc = (overflow || timeout || !active) ? 0 : total_cand;
     if (l == 0) L.misc[1] = nc;
   }
   __syncthreads();
@@ -1169,7 +1197,8 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
 
   TailIn t;
   t.nc = nc;
-  t.overflow = overflow;
+  t.overflow = overflow || timeout;
+  t.timeout = timeout;
   t.ent_all = ent_all;
   t.min_all = min_all;
   t.kept_all = kept_all;
@@ -1593,6 +1622,7 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   TailIn t;
   t.nc = nc;
   t.overflow = false;
+  t.timeout = false;
   t.ent_all = 0.0;
   t.min_all = kPosInf;
   t.kept_all = 0;
@@ -1756,6 +1786,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   if (tid == 0) {
     L.flags = 0u;
     L.ncand = 0;
+    L.tmo = 0;
   }
   SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
   EntryMarks em;
@@ -2115,16 +2146,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
           const uint32_t prev = __hip_atomic_fetch_add(&ws.arrive_stats[row], 1u, __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT);
           const bool last = prev + 1u == (uint32_t)G;
-          if (!last) {
-            int it = 0;
-            while (ld_coherent(&ws.arrive_stats[row]) < (uint32_t)G) {
-              if (++it >= kSpinLimit) {
-                atomicOr(ws.status, kStatusSpinTimeout);
-                break;
-              }
-              __builtin_amdgcn_s_sleep(2);
-            }
-          }
+          L.tmo = (!last && !spin_until(ws, &ws.arrive_stats[row], (uint32_t)G)) ? 1 : 0;
           L.last = last ? 1 : 0;
         }
         __syncthreads();
@@ -2133,7 +2155,10 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
             short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K);
             return;
           }
-        } else if (!short_fallback(ws, row, G, L)) {
+        } else if (L.tmo || !short_fallback(ws, row, G, L)) {
+          // (a slice that gave up waiting cannot trust the fallback flags; it
+          // leaves, and a row that did fall back then fails closed in its
+          // histogram wait)
           if (tid == 0) short_depart(ws, row, G);
           return;
         }
@@ -2224,17 +2249,9 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       if (tid == 0) {
         const uint32_t prev = __hip_atomic_fetch_add(&ws.arrive_stats[row], 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
-        if (prev + 1u < target) {
-          // bounded: a wait that runs out sets a status bit, so the grid drains
-          int it = 0;
-          while (ld_coherent(&ws.arrive_stats[row]) < target) {
-            if (++it >= kSpinLimit) {
-              atomicOr(ws.status, kStatusSpinTimeout);
-              break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-          }
-        }
+        // bounded: a wait that runs out sets a status bit and this slice's
+        // timeout mark, so the grid drains and the row fails closed
+        if (prev + 1u < target && !spin_until(ws, &ws.arrive_stats[row], target)) L.tmo = 1;
       }
       __syncthreads();
       merge_row(ws, P, row, c, prm, L);
@@ -2439,6 +2456,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     st_coherent(&sp->n_cand, ncand);
     st_coherent(&sp->n_list, nlist);
     st_coherent(&sp->overflow, ent_overflow ? 1 : 0);
+    st_coherent(&sp->timeout, L.tmo);
   }
   if (!arrive_last(&ws.arrive_select[row], (uint32_t)G, &L.last)) return;
   finalize_row<DT>(ws, P, row, c, prm, info, L, rowp, mrow, MODE == kFused);
@@ -2570,9 +2588,9 @@ __global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, Verify
     bool failed = false;  // a row whose keep set could not be resolved
     for (int j = 0; j < W; ++j) {
       tok[j] = -1;
-      if (ws.vflags[s * W + j] & LSAMP_ROW_OVERFLOW) failed = true;
+      if (ws.vflags[s * W + j] & (LSAMP_ROW_OVERFLOW | LSAMP_ROW_TIMEOUT)) failed = true;
       if (Q.mode == LSAMP_VERIFY_RESIDUAL && j < D &&
-          (ws.vflags[S * W + s * D + j] & LSAMP_ROW_OVERFLOW))
+          (ws.vflags[S * W + s * D + j] & (LSAMP_ROW_OVERFLOW | LSAMP_ROW_TIMEOUT)))
         failed = true;
     }
     if (am)
@@ -2707,21 +2725,29 @@ int launch_sample(const Workspace& ws, const SamplePlan& P, void* stream, void* 
   }
 }
 
+int set_spin_test(int32_t polls) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_spin_test), &polls, sizeof polls, 0,
+                                hipMemcpyHostToDevice);
+}
+
+// Work-groups per CU of the fused kernel: the smaller occupancy of its two
+// instantiations (one round / several rounds), since a launch may use either
+// and the grid is sized from this value.
+template <int DT>
+int fused_blocks_dt() {
+  int a = 0, b = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_fused<DT, true>, kThreads, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_fused<DT, false>, kThreads, 0) != hipSuccess)
+    return 0;
+  return a < b ? a : b;
+}
+
 int fused_blocks_per_cu(int dtype) {
-  int n = 0;
-  hipError_t e;
   switch (dtype) {
-    case LSAMP_DTYPE_F32:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_F32, false>, kThreads, 0);
-      break;
-    case LSAMP_DTYPE_BF16:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_BF16, false>, kThreads, 0);
-      break;
-    default:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_fused<LSAMP_DTYPE_F16, false>, kThreads, 0);
-      break;
+    case LSAMP_DTYPE_F32: return fused_blocks_dt<LSAMP_DTYPE_F32>();
+    case LSAMP_DTYPE_BF16: return fused_blocks_dt<LSAMP_DTYPE_BF16>();
+    default: return fused_blocks_dt<LSAMP_DTYPE_F16>();
   }
-  return e == hipSuccess ? n : 0;
 }
 
 }  // namespace lsamp

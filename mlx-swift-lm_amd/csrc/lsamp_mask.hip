@@ -109,7 +109,62 @@ __global__ __launch_bounds__(kMaskThreads) void k_mask_assemble(MaskAssemblePlan
   if (tid == 0 && P.row_flags) P.row_flags[r] = zero ? LSAMP_MASK_ID_RANGE : 0u;
 }
 
+// Suppressed ids (SuppressTokensProcessor, SuppressTokens.swift:67-81) folded
+// into the step's bitmask.  A work-group owns kSupWords consecutive words of
+// every row in its slice of rows: it clears the suppressed bits of its words
+// in LDS (the whole id list is read by every work-group; lists are short),
+// then writes caller word & LDS word for each row.
+constexpr int kSupThreads = 256;
+constexpr int kSupWords = 256;
+constexpr int kSupRowsPerGroup = 16;
+static_assert(kSupWords == kSupThreads, "one word per thread");
+
+__global__ __launch_bounds__(kSupThreads) void k_suppress_mask(SuppressPlan P) {
+  __shared__ uint32_t sup[kSupWords];
+  const int tid = threadIdx.x;
+  const int w0 = blockIdx.x * kSupWords;
+  sup[tid] = ~0u;
+  __syncthreads();
+  for (int j = tid; j < P.n; j += kSupThreads) {
+    const int32_t id = P.ids[j];
+    if (id < 0 || id >= P.vocab) continue;
+    const int w = (id >> 5) - w0;
+    if (w >= 0 && w < kSupWords) atomicAnd(&sup[w], ~(1u << (id & 31)));
+  }
+  __syncthreads();
+  const int w = w0 + tid;
+  if (w >= P.words) return;
+  // bits of this word that name tokens inside the vocabulary
+  const int32_t nv = P.vocab - 32 * w;
+  const uint32_t in_vocab = nv >= 32 ? ~0u : ((1u << nv) - 1u);
+  // caller's bits: a word past mask_words, or a bit at or past mask_bits,
+  // follows the tail policy
+  int32_t nin = w < P.mask_words ? P.mask_bits - 32 * w : 0;
+  nin = nin < 0 ? 0 : (nin > 32 ? 32 : nin);
+  const uint32_t in_mask = nin >= 32 ? ~0u : ((1u << nin) - 1u);
+  const uint32_t tail = P.mask_tail == LSAMP_MASK_TAIL_KEEP ? ~in_mask : 0u;
+  const uint32_t keep = sup[tid] & in_vocab;
+  const int r0 = blockIdx.y * kSupRowsPerGroup;
+  const int r1 = r0 + kSupRowsPerGroup < P.rows ? r0 + kSupRowsPerGroup : P.rows;
+  for (int r = r0; r < r1; ++r) {
+    uint32_t allow = ~0u;
+    if (P.bitmask) {
+      const uint32_t word = w < P.mask_words ? P.bitmask[(size_t)r * P.mask_words + w] : 0u;
+      allow = (word & in_mask) | tail;
+    }
+    P.out[(size_t)r * P.words + w] = allow & keep;
+  }
+}
+
 }  // namespace
+
+int launch_suppress_mask(const SuppressPlan& plan, void* stream) {
+  const unsigned gx = (unsigned)((plan.words + kSupWords - 1) / kSupWords);
+  const unsigned gy = (unsigned)((plan.rows + kSupRowsPerGroup - 1) / kSupRowsPerGroup);
+  hipLaunchKernelGGL(k_suppress_mask, dim3(gx, gy), dim3(kSupThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), plan);
+  return (int)hipGetLastError();
+}
 
 int launch_mask_assemble(const MaskAssemblePlan& plan, void* stream) {
   hipLaunchKernelGGL(k_mask_assemble, dim3((unsigned)(plan.rows * kMaskParts)), dim3(kMaskThreads),

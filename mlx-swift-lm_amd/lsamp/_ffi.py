@@ -28,7 +28,9 @@ SEM_MLXLM, SEM_CBV2 = 0, 1
 KIND_ARGMAX, KIND_FILTERED, KIND_CATEGORICAL = 0, 1, 2
 MASK_TAIL_KEEP, MASK_TAIL_FORBID = 0, 1
 PEN_REPETITION, PEN_PRESENCE = 1, 2
-ROW_NONFINITE, ROW_EMPTY, ROW_OVERFLOW, ROW_TOKEN_RANGE = 1, 2, 4, 8
+ROW_NONFINITE, ROW_EMPTY, ROW_OVERFLOW, ROW_TOKEN_RANGE, ROW_TIMEOUT = 1, 2, 4, 8, 16
+STATUS_SPIN_TIMEOUT = 1
+MAX_SUPPRESS = 65536
 RANK_MAX_K = 32
 VERIFY_RESIDUAL, VERIFY_EXACT, VERIFY_TYPICAL = 0, 1, 2
 MODE_AUTO, MODE_FUSED, MODE_SPLIT = 0, 1, 2
@@ -100,6 +102,8 @@ class SampleArgs(Structure):
         ("keep", c_void_p),
         ("stats", c_void_p),
         ("penalty_row_len", c_void_p),
+        ("suppress_ids", c_void_p),
+        ("n_suppress", c_int32),
     ]
 
 
@@ -294,6 +298,8 @@ def load_library(path: str | None = None):
     lib.lsamp_context_set_mode.restype = c_int32
     lib.lsamp_context_read_status.argtypes = [c_void_p, POINTER(c_uint32)]
     lib.lsamp_context_read_status.restype = c_int32
+    lib.lsamp_set_spin_test.argtypes = [c_int32, c_int32]
+    lib.lsamp_set_spin_test.restype = c_int32
     lib.lsamp_context_last_launch.argtypes = [c_void_p, POINTER(LaunchInfo)]
     lib.lsamp_context_last_launch.restype = c_int32
     lib.lsamp_context_set_timing.argtypes = [c_void_p, c_int32]

@@ -120,10 +120,11 @@ class Context:
                        row_ptr=None, entries=None, bitmask=None, mask_bits: Optional[int] = None,
                        mask_tail: int = _ffi.MASK_TAIL_KEEP, uniforms=None, philox_keys=None,
                        probe_tokens=None, want_processed: bool = False, want_keep: bool = False,
-                       want_stats: bool = False, table: Optional["PenaltyTable"] = None
-                       ) -> "PreparedSample":
+                       want_stats: bool = False, table: Optional["PenaltyTable"] = None,
+                       suppress_ids=None) -> "PreparedSample":
         """`table`: read the penalty entries from a device PenaltyTable
-        (instead of row_ptr / entries)."""
+        (instead of row_ptr / entries).  `suppress_ids`: token ids masked to
+        -inf in every row (SuppressTokensProcessor, SuppressTokens.swift:67-81)."""
         row_len = None
         if table is not None:
             row_ptr, entries, row_len = table.row_ptr, table.entries, table.row_len
@@ -132,7 +133,7 @@ class Context:
                               mask_bits=mask_bits, mask_tail=mask_tail, uniforms=uniforms,
                               philox_keys=philox_keys, probe_tokens=probe_tokens,
                               want_processed=want_processed, want_keep=want_keep,
-                              want_stats=want_stats)
+                              want_stats=want_stats, suppress_ids=suppress_ids)
 
     def sample(self, logits: torch.Tensor, params, **kw) -> dict:
         prep = self.prepare_sample(logits, params, **kw)
@@ -273,7 +274,7 @@ class PreparedSample:
 
     def __init__(self, ctx: Context, logits: torch.Tensor, params, *, semantics, vocab, row_ptr,
                  entries, bitmask, mask_bits, mask_tail, uniforms, philox_keys, probe_tokens,
-                 want_processed, want_keep, want_stats, row_len=None):
+                 want_processed, want_keep, want_stats, row_len=None, suppress_ids=None):
         dev = logits.device
         if logits.dim() != 2:
             raise ValueError("logits must be [rows, row_stride]")
@@ -342,6 +343,13 @@ class PreparedSample:
             pt = dev_tensor(probe_tokens, np.int32, torch.int32)
             self.keep_alive.append(pt)
             a.probe_tokens = pt.data_ptr()
+        if suppress_ids is not None and len(suppress_ids) > 0:
+            si = dev_tensor(suppress_ids, np.int32, torch.int32)
+            if si.dtype != torch.int32:
+                si = si.to(torch.int32)
+            self.keep_alive.append(si)
+            a.suppress_ids = si.data_ptr()
+            a.n_suppress = int(si.numel())
         self.tokens = torch.empty(rows, dtype=torch.int32, device=dev)
         self.row_flags = torch.empty(rows, dtype=torch.int32, device=dev)
         a.tokens = self.tokens.data_ptr()

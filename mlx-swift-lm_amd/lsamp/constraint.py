@@ -76,6 +76,15 @@ class _MaskCache:
     def slots(self) -> List[int]:
         return [s for _, s in self.entries]
 
+    def evict_oldest(self, avoid) -> Optional[int]:
+        """Drop the least recent entry whose pool row is not in `avoid`;
+        returns that pool row, or None."""
+        for i, (_, slot) in enumerate(self.entries):
+            if slot not in avoid:
+                self.entries.pop(i)
+                return slot
+        return None
+
 
 @dataclass
 class _RowState:
@@ -180,6 +189,7 @@ class ConstraintMasks:
         build = np.zeros(n, np.uint8)
         ptr = np.zeros(n + 1, np.int32)
         ids: List[np.ndarray] = []
+        in_use = set()  # pool rows this step reads or builds
         for r, rid in enumerate(request_ids):
             row = self.rows.get(rid)
             if row is None:
@@ -193,6 +203,7 @@ class ConstraintMasks:
             if slot is not None:
                 self.mask_cache_hit_count += 1
                 src[r] = slot
+                in_use.add(slot)
             else:
                 allowed = (list(row.constraint.allowed_token_ids(row.state, remaining))
                            if row.failure is None else [])
@@ -200,14 +211,15 @@ class ConstraintMasks:
                     failure = IMPOSSIBLE_STATE
                     allowed = [row.constraint.fallback_token_id]
                 self.mask_build_count += 1
+                slot = None
                 if key is not None and failure is None:
-                    # insert first: a full cache lets its least recent row go
-                    self._free.extend(row.masks.insert(key, -1))
-                    if not self._free:
-                        raise RuntimeError("mask pool exhausted")
-                    slot = self._free.pop()
-                    row.masks.entries[-1] = (key, slot)
-                else:
+                    slot = self._take_slot(row, in_use)
+                    if slot is not None:
+                        self._free.extend(row.masks.insert(key, slot))
+                        in_use.add(slot)
+                if slot is None:
+                    # not cached: the step's own row (no key, an impossible
+                    # state, or no pool row free of this step's reads)
                     slot = self.cache_rows + r
                 src[r] = slot
                 build[r] = 1
@@ -229,6 +241,27 @@ class ConstraintMasks:
                 row.successor_failure = None
         flat = np.concatenate(ids) if ids else np.zeros(0, np.int32)
         return MaskPlan(src, build, ptr, flat)
+
+    def _take_slot(self, row: _RowState, in_use) -> Optional[int]:
+        """A pool row for a new cache entry of `row`, taken before the cache
+        changes: the row's own least recent entry when its cache is full (the
+        LRU would drop it), else a free row, else the least recent entry of
+        another row's cache that this step does not read (the masks are only
+        a cache; that row rebuilds on its next miss).  None: every pool row
+        is read by this step."""
+        if len(row.masks.entries) >= row.masks.capacity:
+            slot = row.masks.evict_oldest(in_use)
+            if slot is not None:
+                return slot
+        if self._free:
+            return self._free.pop()
+        for other in self.rows.values():
+            if other is row:
+                continue
+            slot = other.masks.evict_oldest(in_use)
+            if slot is not None:
+                return slot
+        return None
 
     # ----------------------------------------------------------- confirmation
     def confirm(self, tokens: Sequence[int], request_ids: Sequence[int]):

@@ -114,9 +114,14 @@ class Cbv2RowState:
         return t >= 0 and (self.vocab is None or t < self.vocab)
 
     def commit(self, token: int) -> None:
-        """LogitsPipelineV2.commit for one row (:357-384)."""
+        """LogitsPipelineV2.commit for one row (:357-384).  A token outside
+        [0, vocab) -- the -1 of an EMPTY / OVERFLOW / TIMEOUT row, which the
+        reference never produces -- commits nothing, as lsamp_commit and the
+        oracle's lso_penalty_commit do: the ring does not advance."""
         token = int(token)
-        if self.counts_on and self._in_vocab(token):
+        if not self._in_vocab(token):
+            return
+        if self.counts_on:
             self.output_counts[token] += 1
         if self.repetition_on:
             self.window[self.ring_pos] = token

@@ -85,6 +85,17 @@ uint16_t lso_f32_to_f16(float f) {
   return (uint16_t)(sign | h);
 }
 
+/* Array forms of the converters, for the known-answer tests. */
+void lso_f32_to_bf16_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = lso_f32_to_bf16(in[i]);
+}
+void lso_f32_to_f16_n(const float* in, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = lso_f32_to_f16(in[i]);
+}
+void lso_f16_to_f32_n(const uint16_t* in, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = lso_f16_to_f32(in[i]);
+}
+
 static inline float load_logit(const void* row, int32_t dtype, int64_t i) {
   switch (dtype) {
     case LSAMP_DTYPE_BF16: return lso_bf16_to_f32(((const uint16_t*)row)[i]);
@@ -295,6 +306,16 @@ static void scratch_free(scratch_t* s) {
   free(s->cum);
 }
 
+/* SuppressTokensProcessor.process (SuppressTokens.swift:67-81): putAlong of
+ * -inf at the suppressed ids, ids at or past the vocabulary dropped (the
+ * reference's slow path), negative ids dropped at init (:55-56). */
+static void suppress_apply(const lso_sample_args* a, float* x) {
+  for (int32_t j = 0; j < a->n_suppress; ++j) {
+    const int32_t id = a->suppress_ids[j];
+    if (id >= 0 && id < a->vocab) x[id] = -INFINITY;
+  }
+}
+
 /* ------------------------------------------------------- CBv2 transforms */
 
 /* LogitsPipelineV2.process stages (0)-(3) plus the hard mask
@@ -369,6 +390,7 @@ static void cbv2_transform(const lso_sample_args* a, int32_t r, scratch_t* s) {
     for (int32_t i = 0; i < V; ++i)
       if (!mask_allows(mrow, a->mask_words, a->mask_bits, a->mask_tail, i)) x[i] = -INFINITY;
   }
+  suppress_apply(a, x);
 }
 
 /* ------------------------------------------------------ mlx-lm transforms */
@@ -428,6 +450,7 @@ static void mlxlm_transform(const lso_sample_args* a, int32_t r, scratch_t* s) {
     for (int32_t i = 0; i < V; ++i)
       if (!mask_allows(mrow, a->mask_words, a->mask_bits, a->mask_tail, i)) x[i] = -INFINITY;
   }
+  suppress_apply(a, x);
 }
 
 /* ----------------------------------------------------------------- filters */
@@ -459,15 +482,20 @@ static void cbv2_filter(const lsamp_row_params* p, int32_t V, const float* x, sc
   const float mp = p->min_p > 0.0f ? (p->min_p > 1.0f ? 1.0f : p->min_p) : 0.0f;
   const float p0 = s->cum[0] / z;
   const float mp_thr = mp * p0;
+  /* The top-p test uses the exclusive mass in double precision: MLX's fp32
+   * cumsum order is not vendored, and a sequential fp32 sum over thousands
+   * of terms drifts by more than the 1e-6 of cumulative mass the parity rule
+   * allows.  The fp32 sequential margin is still reported (tp_margin). */
   float cum = 0.0f;
-  double cum_x = 0.0; /* exact-arithmetic exclusive mass */
+  double cum_x = 0.0; /* exclusive mass, double precision */
   for (int32_t r = 0; r < V; ++r) {
     const float pr = s->cum[r] / z;
     cum += pr;
     const float excl = cum - pr;
-    if (tp_exact) tp_exact[o[r].i] = (double)tp - cum_x;
+    const double excl_x = cum_x;
+    if (tp_exact) tp_exact[o[r].i] = (double)tp - excl_x;
     cum_x += exp((double)o[r].v - (double)m) / zx;
-    const int keep = (r < k) && (excl <= tp) && (pr >= mp_thr);
+    const int keep = (r < k) && (excl_x <= (double)tp) && (pr >= mp_thr);
     const int32_t i = o[r].i;
     s->keep[i] = (uint8_t)(keep && x[i] > -INFINITY);
     if (tp_margin) tp_margin[i] = tp - excl;
@@ -505,6 +533,9 @@ static void mlxlm_filter(const lsamp_row_params* p, int32_t V, const float* x, s
       o[i].i = i;
     }
     qsort(o, (size_t)V, sizeof(vi_t), cmp_asc_idasc);
+    /* keep where the inclusive ascending mass exceeds 1 - topP; the mass is
+     * summed in double (see cbv2_filter), the threshold is the reference's
+     * fp32 constant */
     const float thr = 1.0f - p->top_p;
     float cum = 0.0f;
     double cum_x = 0.0;
@@ -512,7 +543,7 @@ static void mlxlm_filter(const lsamp_row_params* p, int32_t V, const float* x, s
       cum += expf(o[r].v);
       const int32_t i = o[r].i;
       cum_x += exp((double)x[i] - lse_x);
-      if (!(cum > thr)) s->keep[i] = 0;
+      if (!(cum_x > (double)thr)) s->keep[i] = 0;
       if (tp_margin) tp_margin[i] = cum - thr;
       if (tp_exact) tp_exact[i] = cum_x - (double)thr;
     }

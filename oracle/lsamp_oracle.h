@@ -45,11 +45,18 @@ typedef struct lso_sample_args {
   uint32_t* row_flags;   /* [rows] */
   float* processed;      /* [rows, vocab] filter-space logits before the filters */
   uint8_t* keep;         /* [rows, vocab] 1 = token survives the filters */
-  float* top_p_margin;   /* [rows, vocab] signed distance of the top-p test */
+  float* top_p_margin;   /* [rows, vocab] signed distance of the top-p test
+                            in the reference's fp32 sequential cumsum
+                            (diagnostic; the decision uses the exact mass) */
   float* min_p_margin;   /* [rows, vocab] signed distance of the min-p test */
   double* top_p_margin_exact; /* [rows, vocab] the top-p distance in exact
-                                 (double) arithmetic from the same logits */
+                                 (double) arithmetic from the same logits: the
+                                 quantity the top-p test decides on */
   lsamp_row_stats* stats;/* [rows] */
+  /* SuppressTokensProcessor (SuppressTokens.swift:67-81): ids masked to -inf
+   * after the penalties and the bitmask; negatives and ids >= vocab ignored */
+  const int32_t* suppress_ids;
+  int32_t n_suppress;
 } lso_sample_args;
 
 /* Full sampling step (both semantics).  Returns 0 or a negative status. */
@@ -134,6 +141,9 @@ float lso_bf16_to_f32(uint16_t h);
 uint16_t lso_f32_to_bf16(float f);
 float lso_f16_to_f32(uint16_t h);
 uint16_t lso_f32_to_f16(float f);
+void lso_f32_to_bf16_n(const float* in, uint16_t* out, int64_t n);
+void lso_f32_to_f16_n(const float* in, uint16_t* out, int64_t n);
+void lso_f16_to_f32_n(const uint16_t* in, float* out, int64_t n);
 
 #ifdef __cplusplus
 }

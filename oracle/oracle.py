@@ -33,6 +33,7 @@ class LsoSampleArgs(Structure):
         ("tokens", c_void_p), ("row_flags", c_void_p), ("processed", c_void_p),
         ("keep", c_void_p), ("top_p_margin", c_void_p), ("min_p_margin", c_void_p),
         ("top_p_margin_exact", c_void_p), ("stats", c_void_p),
+        ("suppress_ids", c_void_p), ("n_suppress", c_int32),
     ]
 
 
@@ -95,6 +96,9 @@ def lib():
         L.lso_f32_to_bf16.restype = ctypes.c_uint16
         L.lso_bf16_to_f32.argtypes = [ctypes.c_uint16]
         L.lso_bf16_to_f32.restype = c_float
+        for name in ("lso_f32_to_bf16_n", "lso_f32_to_f16_n", "lso_f16_to_f32_n"):
+            getattr(L, name).argtypes = [c_void_p, c_void_p, c_int64]
+            getattr(L, name).restype = None
         _lib = L
     return _lib
 
@@ -151,7 +155,7 @@ STATS_DTYPE = np.dtype([
 def sample(*, semantics, logits, dtype, params, row_ptr=None, entries=None, bitmask=None,
            mask_bits=0, mask_tail=0, uniforms=None, philox_keys=None, probe_tokens=None,
            threads=1, want_processed=False, want_keep=False, want_margins=False,
-           want_stats=False, vocab=None, row_stride=None):
+           want_stats=False, vocab=None, row_stride=None, suppress_ids=None):
     """Run the oracle.  `logits` is a 2-D numpy array: float32, or uint16 bit
     patterns for bf16 / f16 (dtype says which)."""
     logits = np.ascontiguousarray(logits)
@@ -198,6 +202,10 @@ def sample(*, semantics, logits, dtype, params, row_ptr=None, entries=None, bitm
     if probe_tokens is not None:
         probe_tokens = np.ascontiguousarray(probe_tokens, np.int32)
         a.probe_tokens = _ptr(probe_tokens)
+    if suppress_ids is not None and len(suppress_ids) > 0:
+        suppress_ids = np.ascontiguousarray(suppress_ids, np.int32)
+        a.suppress_ids = _ptr(suppress_ids)
+        a.n_suppress = len(suppress_ids)
     a.threads = threads
     for k in ("tokens", "row_flags", "processed", "keep", "top_p_margin", "min_p_margin",
               "top_p_margin_exact", "stats"):
@@ -391,3 +399,27 @@ def assemble_masks(plan, pool, vocab):
                 flags[r] = _ffi.MASK_ID_RANGE
         out[r] = pool[s]
     return out, flags
+
+
+def f32_to_bf16(x):
+    """The oracle's round-to-nearest-even float32 -> bfloat16 bits (uint16)."""
+    a = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.empty(a.shape, np.uint16)
+    lib().lso_f32_to_bf16_n(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def f32_to_f16(x):
+    """The oracle's round-to-nearest-even float32 -> IEEE half bits (uint16)."""
+    a = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.empty(a.shape, np.uint16)
+    lib().lso_f32_to_f16_n(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def f16_to_f32(h):
+    """The oracle's IEEE half bits -> float32."""
+    a = np.ascontiguousarray(h, np.uint16).reshape(-1)
+    out = np.empty(a.shape, np.float32)
+    lib().lso_f16_to_f32_n(_ptr(a), _ptr(out), a.size)
+    return out

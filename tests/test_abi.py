@@ -195,6 +195,14 @@ def test_rng_key_matches_the_oracle(lib):
         assert lib.lsamp_rng_key(s, i, t) == O.rng_key(s, i, t)
 
 
+def test_rng_key_splitmix64_known_answer(lib):
+    # the published SplitMix64 outputs of seed 1234567, composed as
+    # SamplerV2.mix composes them (SamplerV2.swift:183-191)
+    from test_oracle_golden import splitmix_known_answers
+    for seed, rid, step, key in splitmix_known_answers():
+        assert lib.lsamp_rng_key(seed, rid, step) == key
+
+
 def test_rng_uniform_matches_the_oracle(lib):
     rng = np.random.default_rng(10)
     for _ in range(200):

@@ -215,6 +215,11 @@ def test_configs_full(ctx, n):
     boundary = compare(cfg, g, o, label=f"config{n}")
     print(f"config{n}: {len(boundary)} of {cfg['rows']} rows differ only at a top-p / min-p "
           f"boundary: {boundary}")
+    # a row differs only where its boundary token's exact mass lies within
+    # 1e-6 of the threshold; the kernel's masses are accurate to ~3e-7, so
+    # such rows are rare (about 1 in 300 for wide nuclei)
+    limit = 2 + cfg["rows"] // 64
+    assert len(boundary) <= limit, f"config{n}: {len(boundary)} boundary rows (limit {limit})"
     if n == 4:
         assert g["tokens"][cfg["eos_row"]] == W.EOS_ID
 

@@ -59,9 +59,9 @@ def run_both(ctx, mode, target, draft, drafts, params, uniforms, dtype, delta=0.
 
 def check(g, o, label, typical=False):
     if typical:
-        # decisions may differ only where p(draft) sits within 1e-5 of the
+        # decisions may differ only where p(draft) sits within 1e-6 of the
         # floor (the kernel derives p and H from fixed-point draw weights)
-        near = np.abs(o["typical_margin"]) <= 1e-5
+        near = np.abs(o["typical_margin"]) <= 1e-6
         assert np.array_equal(g["accept_mask"][~near], o["accept_mask"][~near]), label
         assert np.array_equal(g["tokens"], o["tokens"]), label
         return

@@ -84,6 +84,17 @@ def test_tokens_outside_the_vocabulary_commit_nothing():
     st.commit(V)
     assert np.array_equal(st.counts, before[0]) and np.array_equal(st.window_counts, before[1])
     assert np.array_equal(st.window, before[2]) and st.ring_pos == before[3]
+    # the host mirror follows the same rule: its ring does not advance either
+    host = Cbv2RowState([3], [3], 4, repetition_on=True, counts_on=True, vocab=V)
+    win, pos, ent = list(host.window), host.ring_pos, host.entries().tolist()
+    host.commit(-1)
+    host.commit(V)
+    assert list(host.window) == win and host.ring_pos == pos and host.entries().tolist() == ent
+    for t in (5, -1, 6):
+        host.commit(t)
+        st.commit(t)
+    rot = np.concatenate([st.window[st.ring_pos:], st.window[:st.ring_pos]])
+    assert host.ring_pos == st.ring_pos and list(host.window) == st.window.tolist(), rot
 
 
 # ------------------------------------------------- penalty-aware verify windows

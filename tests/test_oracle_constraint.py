@@ -176,6 +176,33 @@ def test_cache_slots_return_to_the_pool():
     assert sorted(cm._free) == list(range(cm.cache_rows))
 
 
+def test_pool_past_max_rows_never_opens_a_row():
+    """More live constrained requests than max_rows (parked or unfinished
+    requests keep their 8 cached rows): once the pool is exhausted a miss
+    takes another request's least recent row (or the step's own uncached
+    row), never a row the same step reads, and no constrained row is ever
+    planned as open (-1)."""
+    V, rows = 512, 2
+    cm, pool = fresh(rows, V)
+    cs = {rid: CyclicKeyedConstraint(V, states=3, density=0.02, seed=40 + rid)
+          for rid in range(6)}
+    cm.configure([(rid, c, []) for rid, c in cs.items()])
+    rng = np.random.default_rng(3)
+    for step in range(60):
+        batch = [int(v) for v in rng.choice(6, rows, replace=False)]
+        plan = cm.plan(batch)
+        assert (plan.row_source >= 0).all(), "a constrained row went open"
+        out, _ = O.assemble_masks(plan, pool, V)
+        for r, rid in enumerate(batch):
+            st = cm.rows[rid].state
+            assert np.array_equal(out[r], O.device_mask_words(cs[rid].sets[st], V)), (step, rid)
+        cm.confirm([int(cs[rid].sets[cm.rows[rid].state][0]) for rid in batch], batch)
+        used = [sl for row in cm.rows.values() for sl in row.masks.slots()]
+        assert len(used) == len(set(used)) and -1 not in used
+        assert sorted(used + cm._free) == list(range(cm.cache_rows))
+    assert cm.mask_cache_hit_count > 0
+
+
 def test_same_constraint_reconfigure_keeps_masks_new_instance_drops_them():
     V = 256
     cm, pool = fresh(1, V)

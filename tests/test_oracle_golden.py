@@ -24,7 +24,7 @@ F32 = _ffi.DTYPE_F32
 
 # ----------------------------------------------------------------- helpers
 def run(semantics, logits, params, entries=None, uniforms=None, dtype=F32, bitmask=None,
-        mask_bits=0, mask_tail=0):
+        mask_bits=0, mask_tail=0, suppress_ids=None):
     logits = np.atleast_2d(np.asarray(logits))
     if dtype == F32:
         logits = logits.astype(np.float32)
@@ -39,7 +39,7 @@ def run(semantics, logits, params, entries=None, uniforms=None, dtype=F32, bitma
     return O.sample(semantics=semantics, logits=logits, dtype=dtype, params=W._params(params),
                     uniforms=np.asarray(uniforms, np.float32), want_processed=True,
                     want_keep=True, want_stats=True, bitmask=bitmask, mask_bits=mask_bits,
-                    mask_tail=mask_tail, **kw)
+                    mask_tail=mask_tail, suppress_ids=suppress_ids, **kw)
 
 
 def mlx_processed(logits, rep=None, rep_ctx=20, pres=None, pres_ctx=20, freq=None,
@@ -498,6 +498,69 @@ def test_cbv2_mask_precedes_top_k_and_survives_negative_penalty():
     assert out["processed"][0][3] == -np.inf
 
 
+# ----------------------------------------------- suppressed ids, chain order
+SUPPRESS_LOGITS = [0.5, 5.0, 1.0, 9.0, 2.0]
+
+
+@pytest.mark.parametrize("semantics", [_ffi.SEM_MLXLM, _ffi.SEM_CBV2])
+def test_suppress_masks_only_the_given_ids(semantics):
+    # SuppressTokensTests.swift testSuppressTokensProcessorMasksOnlyGivenIds
+    p = (W.resolve_mlxlm(temperature=1.0) if semantics == _ffi.SEM_MLXLM
+         else W.resolve_cbv2(temperature=1.0, vocab=5))
+    v = run(semantics, SUPPRESS_LOGITS, p, suppress_ids=[1, 3])["processed"][0]
+    assert v.tolist() == [0.5, -np.inf, 1.0, -np.inf, 2.0]
+
+
+def test_suppressed_token_is_never_the_argmax():
+    # testSuppressedTokenIsNeverArgMax: 9.0 at id 3 suppressed -> id 1
+    out = run(_ffi.SEM_MLXLM, SUPPRESS_LOGITS, W.resolve_mlxlm(temperature=0.0), suppress_ids=[3])
+    assert out["tokens"][0] == 1
+
+
+def test_suppress_ignores_out_of_range_and_negative_ids():
+    # testSuppressTokensProcessorIgnoresOutOfRangeIds / AllOutOfRangeIsNoOp /
+    # IgnoresNegativeIds
+    p = W.resolve_mlxlm(temperature=1.0)
+    v = run(_ffi.SEM_MLXLM, SUPPRESS_LOGITS, p, suppress_ids=[1, 258882, 258883])["processed"][0]
+    assert v[1] == -np.inf and v[3] == 9.0
+    v = run(_ffi.SEM_MLXLM, [0.5, 5.0, 1.0], p, suppress_ids=[258882, 258883])["processed"][0]
+    assert v.tolist() == [0.5, 5.0, 1.0]
+    v = run(_ffi.SEM_MLXLM, [0.5, 5.0, 1.0], p, suppress_ids=[-1, -106])["processed"][0]
+    assert v.tolist() == [0.5, 5.0, 1.0]
+
+
+def test_chained_suppressors_apply_both():
+    # testChainedLogitProcessorAppliesAllProcessors: [1] then [3]
+    v = run(_ffi.SEM_MLXLM, SUPPRESS_LOGITS, W.resolve_mlxlm(temperature=1.0),
+            suppress_ids=[1, 3])["processed"][0]
+    assert v[1] == -np.inf and v[3] == -np.inf and v[4] == 2.0
+
+
+def test_mlxlm_custom_processor_runs_after_the_penalties():
+    """SampleTests.swift:431-454 pins the chain order penalty -> custom
+    (GenerationComponents.swift:112-124), there with a scaling processor.
+    Here the custom processor is the grammar mask and suppression runs last
+    (:126-141).  A negative repetition penalty on a masked / suppressed token
+    tells the orders apart: applied after the penalty the token stays -inf;
+    masked first, -inf * (-1.5) would come back as +inf and be drawn."""
+    prompt = [1, 2, 3]
+    ring = TokenRing(5)
+    ring.load_prompt(prompt)
+    pres = TokenRing(5)
+    pres.load_prompt([1])
+    ents = mlxlm_entries(ring, pres, None)
+    p = W.resolve_mlxlm(temperature=0.0, repetition_penalty=-1.5, repetition_context_size=5,
+                        presence_penalty=0.5, presence_context_size=5)
+    bm = np.array([[0b1011]], np.uint32)  # token 2 forbidden by the mask
+    out = run(_ffi.SEM_MLXLM, [1.0, 2.0, 3.0, 4.0], p, entries=[ents], bitmask=bm, mask_bits=4,
+              suppress_ids=[3])
+    v = out["processed"][0]
+    # token 1: repetition x / -1.5 then presence -0.5 -> -1.8333; 2 masked; 3 suppressed
+    np.testing.assert_allclose(v[:2], [1.0, 2.0 / -1.5 - 0.5], rtol=1e-6)
+    assert v[2] == -np.inf and v[3] == -np.inf
+    assert out["tokens"][0] == 0
+
+
 # ------------------------------------------------------ grammar bitmask
 def test_bitmask_lsb_first_allows_exactly_the_set_bits():
     # MaskRelocationTests.swift:15-33: vocab 8, only id 5 allowed
@@ -719,6 +782,40 @@ def test_rng_uniform_is_uniform():
     assert chi2 < 45.0  # 19 degrees of freedom, p ~ 1e-3
 
 
+# Published SplitMix64 outputs (the generator of Steele, Lea & Flood, "Fast
+# splittable pseudorandom number generators", OOPSLA 2014, as listed for
+# seed 1234567 by the Rosetta Code task "Pseudo-random numbers/Splitmix64"):
+# the state advances by the golden gamma and each output mixes the new state.
+_GAMMA = 0x9E3779B97F4A7C15
+_SPLITMIX_1234567 = [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                     4593380528125082431, 16408922859458223821]
+
+
+def splitmix_known_answers():
+    """(seed, id, step, key) for which each stage of SamplerV2.mix
+    (SamplerV2.swift:183-191), splitmix(splitmix(splitmix(seed) ^ id) ^ step),
+    lands on a published output.  splitmix(v) mixes v + gamma, so
+    splitmix(1234567 + k * gamma) is output k: with seed = 1234567 + j * gamma,
+    stage one gives output j, the id turns it into state j + 1 (output j + 1)
+    and the step into state j + 2 (output j + 2)."""
+    M = (1 << 64) - 1
+    s, out = 1234567, _SPLITMIX_1234567
+    cases = []
+    for j in range(3):
+        seed = (s + j * _GAMMA) & M
+        rid = out[j] ^ ((s + (j + 1) * _GAMMA) & M)
+        step = out[j + 1] ^ ((s + (j + 2) * _GAMMA) & M)
+        cases.append((seed, rid, step, out[j + 2]))
+    return cases
+
+
+@pytest.mark.parametrize("seed,rid,step,key", splitmix_known_answers())
+def test_rng_key_splitmix64_known_answer(seed, rid, step, key):
+    """The key mix against the published SplitMix64 sequence: a wrong shift,
+    multiplier, increment or composition order fails here."""
+    assert O.rng_key(seed, rid, step) == key
+
+
 def test_rng_key_depends_on_all_three_inputs():
     # CBv2SamplingTests.swift:471-476 (SamplerV2.mix)
     base = O.rng_key(1, 2, 3)
@@ -737,3 +834,53 @@ def test_rows_are_independent_of_their_batch():
                        params=cfg["params"][r:r + 1], row_ptr=np.array([0, hi - lo], np.int32),
                        entries=cfg["entries"][lo:hi], uniforms=cfg["uniforms"][r:r + 1])
         assert one["tokens"][0] == full["tokens"][r]
+
+
+# ------------------------------------------------------- dtype conversions
+def _dense_f32_patterns():
+    """Every bfloat16 prefix with the low halves that decide rounding (ties to
+    even and odd, one ulp either side, zero, all ones), plus random patterns:
+    covers subnormals, both zeros, infinities and NaNs."""
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF, 0x1000, 0x0FFF, 0x1001,
+                     0x2000, 0x3000, 0x6000], np.uint32)
+    grid = (hi[:, None] | lows[None, :]).reshape(-1)
+    rnd = np.random.default_rng(77).integers(0, 1 << 32, 1 << 21, dtype=np.uint64).astype(np.uint32)
+    return np.concatenate([grid, rnd]).view(np.float32)
+
+
+def test_f32_to_bf16_matches_torch():
+    """The oracle's float32 -> bfloat16 rounding (used for mlx-lm penalties on
+    16-bit logits) against torch's converter, bit for bit (NaN: any NaN)."""
+    import torch
+    x = _dense_f32_patterns()
+    got = O.f32_to_bf16(x)
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert ((got[nan] & 0x7F80) == 0x7F80).all() and ((got[nan] & 0x7F) != 0).all()
+
+
+def test_f32_to_f16_matches_torch():
+    import torch
+    x = _dense_f32_patterns()
+    got = O.f32_to_f16(x)
+    want = torch.from_numpy(x.copy()).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert ((got[nan] & 0x7C00) == 0x7C00).all() and ((got[nan] & 0x3FF) != 0).all()
+
+
+def test_16bit_to_f32_all_patterns_match_torch():
+    """All 2^16 bfloat16 and half patterns widen exactly as torch widens them."""
+    import torch
+    h = np.arange(1 << 16, dtype=np.uint16)
+    bf = np.array([O.lib().lso_bf16_to_f32(int(v)) for v in h[::257]], np.float32)
+    want_bf = torch.from_numpy(h.view(np.int16).copy()).view(torch.bfloat16).float().numpy()
+    assert np.array_equal(bf.view(np.uint32), want_bf[::257].view(np.uint32))
+    assert np.array_equal(W.bf16_bits_to_f32(h).view(np.uint32), want_bf.view(np.uint32))
+    got = O.f16_to_f32(h)
+    want = torch.from_numpy(h.view(np.int16).copy()).view(torch.float16).float().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.isnan(got[nan]).all()
