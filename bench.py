@@ -394,33 +394,183 @@ def bench_masks(args):
 
 
 def cpu_baseline(cfg, seconds):
-    """Time whole oracle steps on the host's cores (bounded sample)."""
+    """The oracle on whole steps of the headline workload (cpu_baseline_of)."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
-    threads = min(16, os.cpu_count() or 1)
-    kw = dict(semantics=cfg["semantics"], logits=cfg["logits"], dtype=cfg["dtype"],
-              params=cfg["params"], row_ptr=cfg["row_ptr"], entries=cfg["entries"],
+
+    def step(threads, nrows):
+        rp = cfg["row_ptr"]
+        O.sample(semantics=cfg["semantics"], logits=cfg["logits"][:nrows], dtype=cfg["dtype"],
+                 params=cfg["params"][:nrows], row_ptr=rp[:nrows + 1] - rp[0],
+                 entries=cfg["entries"][rp[0]:rp[nrows]], uniforms=cfg["uniforms"][:nrows],
+                 threads=threads)
+
+    return cpu_baseline_of(step, cfg["rows"], seconds)
+
+
+def bench_config(args, n):
+    """Configuration 1, 3 or 4 of the metric: steps/s from HIP-graph replays
+    over `--copies` distinct input copies (c1: a single row, so copies are
+    cheap), the step duration from HIP events on the launch stream, and the
+    oracle on the same workload as the CPU baseline."""
+    import numpy as np
+    import torch
+
+    from lsamp import _ffi, workloads as W
+    from lsamp.api import Context
+
+    cfg = W.CONFIGS[n]()
+    B, V = cfg["rows"], cfg["vocab"]
+    R = args.copies if n != 3 else min(args.copies, 4)  # c3 copies are 134 MB each
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(100 + n)
+    if cfg["dtype"] == _ffi.DTYPE_F32:
+        base = torch.from_numpy(np.ascontiguousarray(cfg["logits"], np.float32))
+        tdt = torch.float32
+    else:
+        base = torch.from_numpy(cfg["logits"].view(np.int16)).view(torch.bfloat16)
+        tdt = torch.bfloat16
+    copies = torch.empty((R, B, V), dtype=tdt, device=dev)
+    for i in range(R):
+        copies[i].copy_(base)
+        if i:  # one perturbed token per row: no two copies share every line
+            idx = torch.from_numpy(rng.integers(0, V, B)).to(dev)
+            copies[i, torch.arange(B, device=dev), idx] = 0.0
+    ctx = Context(0, max_rows=B, max_vocab=V)
+    kw = dict(semantics=cfg["semantics"], row_ptr=cfg.get("row_ptr"), entries=cfg.get("entries"),
               uniforms=cfg["uniforms"])
-    O.sample(threads=threads, **kw)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        O.sample(threads=threads, **kw)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 3:
-            break
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": n / el, "unit": "steps/s", "cores": threads, "kind": "port",
-            "sample": f"{n} whole steps of the same workload ({cfg['rows']} rows) in {el:.1f} s, "
-                      f"rows over {threads} threads; host {model}; ms/step {1e3 * el / n:.2f}"}
+    if cfg.get("bitmask") is not None:
+        kw.update(bitmask=cfg["bitmask"], mask_bits=cfg["mask_bits"], mask_tail=cfg["mask_tail"])
+    preps = [ctx.prepare_sample(copies[i], cfg["params"], **kw) for i in range(R)]
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        for p in preps:
+            p.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    run = graph_runner([(lambda p=p: p.launch(stream.cuda_stream)) for p in preps], stream)
+    wall_s, ev_ms = time_steps(run, stream, args.steps, args.warmup)
+    launch = ctx.last_launch()
+    step_us = 1e3 * ev_ms / args.steps
+    alg = W.algorithmic_bytes(cfg)
+    achieved = alg / (step_us * 1e-6) / 1e9
+    out = {
+        "metric": METRIC.replace("B=64 V=151,936", f"B={B} V={V:,}"),
+        "value": args.steps / wall_s, "unit": "steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": 1e3 * wall_s / args.steps,
+        "us_per_step_events": step_us, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg["workload"], "rows": B, "vocab": V,
+                   "logits_dtype": "fp32" if cfg["dtype"] == _ffi.DTYPE_F32 else "bf16",
+                   "semantics": "mlx-lm" if cfg["semantics"] == _ffi.SEM_MLXLM else "CBv2",
+                   "input_copies": R},
+        "launch": launch,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg,
+                     "kernel": "k_fused" if launch["fused"] else "k_stats+k_select",
+                     "launch_us": step_us},
+        "cpu_baseline": None,
+    }
+    if n == 1:
+        # single-launch latency: each launch waited for before the next
+        lat = []
+        for i in range(max(20, min(args.steps, 200))):
+            t0 = time.perf_counter()
+            preps[i % R].launch(stream.cuda_stream)
+            stream.synchronize()
+            lat.append(time.perf_counter() - t0)
+        out["single_launch_us"] = 1e6 * sorted(lat)[len(lat) // 2]
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+
+        def step(threads, nrows):
+            r = slice(0, nrows)
+            rp = cfg.get("row_ptr")
+            kw2 = {}
+            if rp is not None:
+                kw2["row_ptr"] = rp[:nrows + 1] - rp[0]
+                kw2["entries"] = cfg["entries"][rp[0]:rp[nrows]]
+            if cfg.get("bitmask") is not None:
+                kw2.update(bitmask=cfg["bitmask"][r], mask_bits=cfg["mask_bits"],
+                           mask_tail=cfg["mask_tail"])
+            O.sample(semantics=cfg["semantics"], logits=cfg["logits"][r], dtype=cfg["dtype"],
+                     params=cfg["params"][r], uniforms=cfg["uniforms"][r], threads=threads, **kw2)
+
+        out["cpu_baseline"] = cpu_baseline_of(step, B, args.cpu_seconds)
+    ctx.close()
+    print(json.dumps(out))
+    return 0
+
+
+def bench_c5(args):
+    """Configuration 5: textbook speculative verification (lsamp_verify,
+    RESIDUAL) of 32 sequences x 4 positions with draft logits.  The drafts
+    are the draft rows' own draws (lsamp_sample with the draft uniforms,
+    outside the timed region)."""
+    import numpy as np
+    import torch
+
+    from lsamp import _ffi, workloads as W
+    from lsamp.api import Context
+
+    cfg = W.config5()
+    S, Wn, V = cfg["sequences"], cfg["window"], cfg["vocab"]
+    D = Wn - 1
+    R = min(args.copies, 4)
+    dev = torch.device("cuda", 0)
+    ctx = Context(0, max_rows=S * (2 * Wn - 1), max_vocab=V)
+    tgt = torch.from_numpy(cfg["target"].view(np.int16)).view(torch.bfloat16)
+    dft = torch.from_numpy(cfg["draft"].view(np.int16)).view(torch.bfloat16)
+    tc = torch.empty((R, S, Wn, V), dtype=torch.bfloat16, device=dev)
+    dc = torch.empty((R, S, D, V), dtype=torch.bfloat16, device=dev)
+    for i in range(R):
+        tc[i].copy_(tgt)
+        dc[i].copy_(dft)
+    drafts = ctx.sample(dc[0].reshape(S * D, V), np.repeat(cfg["params"], D),
+                        semantics=_ffi.SEM_CBV2,
+                        uniforms=cfg["draft_uniforms"].reshape(-1))["tokens"].reshape(S, D)
+    torch.cuda.synchronize()
+    preps = [ctx.prepare_verify(tc[i], dc[i], drafts, cfg["params"], cfg["uniforms"],
+                                mode=_ffi.VERIFY_RESIDUAL) for i in range(R)]
+    stream = torch.cuda.Stream(device=dev)
+    for p_ in preps:
+        p_.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    run = graph_runner([(lambda p=p_: p.launch(stream.cuda_stream)) for p_ in preps], stream)
+    wall_s, ev_ms = time_steps(run, stream, args.steps, args.warmup)
+    us = 1e3 * ev_ms / args.steps
+    alg = W.algorithmic_bytes(cfg)
+    achieved = alg / (us * 1e-6) / 1e9
+    out = {
+        "metric": f"MTP verify windows/s at S={S} W={Wn} V={V:,} (lsamp_verify RESIDUAL); "
+                  "achieved HBM GB/s vs 8 TB/s",
+        "value": args.steps / wall_s, "unit": "verifies/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": 1e3 * wall_s / args.steps, "us_per_launch": us,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"] + " RESIDUAL, draft [S,W-1,V] bf16",
+                   "input_copies": R},
+        "launch": ctx.last_launch(),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg,
+                     "kernel": "k_fused + k_verify_finish", "launch_us": us},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import oracle as O
+        dnp = drafts.cpu().numpy()
+
+        def step(threads, nseq):
+            O.verify(mode=_ffi.VERIFY_RESIDUAL, target=cfg["target"][:nseq],
+                     draft=cfg["draft"][:nseq], draft_tokens=dnp[:nseq], dtype=_ffi.DTYPE_BF16,
+                     params=cfg["params"][:nseq], uniforms=cfg["uniforms"][:nseq],
+                     threads=threads)
+
+        out["cpu_baseline"] = cpu_baseline_of(step, S, args.cpu_seconds, unit="verifies/s")
+    ctx.close()
+    print(json.dumps(out))
+    return 0
 
 
 def bench_verify(args):
@@ -435,8 +585,7 @@ def bench_verify(args):
     cfg = W.config5()
     S, Wn, V = cfg["sequences"], cfg["window"], cfg["vocab"]
     R = 4
-    steps = max(R, (args.steps + R - 1) // R * R)
-    warm = max(R, (args.warmup + R - 1) // R * R)
+    steps, warm = args.steps, args.warmup
     dev = torch.device("cuda", 0)
     rng = np.random.default_rng(13)
     ctx = Context(0, max_rows=S * (2 * Wn - 1), max_vocab=V)
@@ -467,24 +616,9 @@ def bench_verify(args):
     for p_ in preps:
         p_.launch(stream.cuda_stream)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for p_ in preps:
-            p_.launch(stream.cuda_stream)
-    torch.cuda.synchronize()
-    for _ in range(warm // R):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    with torch.cuda.stream(stream):
-        for _ in range(steps // R):
-            graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall_s = time.perf_counter() - t0
-    us = 1e3 * e0.elapsed_time(e1) / steps
+    run = graph_runner([(lambda p=p_: p.launch(stream.cuda_stream)) for p_ in preps], stream)
+    wall_s, ev_ms = time_steps(run, stream, steps, warm)
+    us = 1e3 * ev_ms / steps
     achieved = alg / (us * 1e-6) / 1e9
     out = {
         "metric": f"MTP verify windows/s at S={S} W={Wn} V={V} (lsamp_verify EXACT"
@@ -523,8 +657,7 @@ def main():
 
     cfg = W.config2()
     B, V, R = cfg["rows"], cfg["vocab"], args.copies
-    steps = max(R, (args.steps + R - 1) // R * R)
-    warm = max(R, (args.warmup + R - 1) // R * R)
+    steps, warm = args.steps, args.warmup
     dev = torch.device("cuda", 0)
     rng = np.random.default_rng(7)
     base = torch.from_numpy(cfg["logits"].view(np.int16)).view(torch.bfloat16)
@@ -567,27 +700,9 @@ def main():
         ctx.close()
         return 0
 
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for p in preps:
-            p.launch()
-    torch.cuda.synchronize()
-
-    # warm-up, then exactly `steps` steps
-    for _ in range(warm // R):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps // R):
-        graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    wall_s = t1 - t0
-    ev_ms = e0.elapsed_time(e1)
+    # warm-up, then exactly `steps` steps (graphs over the input copies)
+    run = graph_runner([(lambda p=p: p.launch()) for p in preps], stream)
+    wall_s, ev_ms = time_steps(run, stream, steps, warm)
     us_step = 1e6 * wall_s / steps
 
     # per-kernel durations: eager launches with the timing hook, queue kept full
