@@ -282,6 +282,23 @@ void lsamp_context_destroy(lsamp_context* ctx);
 /* Enqueue one sampling step on `stream`. */
 lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* args, void* stream);
 
+/* ---- the sampling step without a context -----------------------------------
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  lsamp_sample on the CURRENT device with its workspace in
+ * a file-scope device array of LSAMP_NOALLOC_SCRATCH_BYTES (11 MiB, held by
+ * each GPU the library runs on until the process ends) instead of a context:
+ * at most LSAMP_NOALLOC_MAX_ROWS rows of at most LSAMP_NOALLOC_MAX_VOCAB logits
+ * (larger calls return LSAMP_ERR_CAPACITY).  Same arguments, results and
+ * errors as lsamp_sample in the AUTO arrangement; allocates nothing and calls
+ * no allocating routine.  Every call on one GPU shares that GPU's array: a
+ * call clears its counters first (a fill kernel, capturable), and calls that
+ * overlap on one GPU (unordered streams) race. */
+#define LSAMP_NOALLOC_MAX_ROWS 64
+#define LSAMP_NOALLOC_MAX_VOCAB 262144
+#define LSAMP_NOALLOC_SCRATCH_BYTES (11u << 20)
+lsamp_status lsamp_sample_noalloc(const lsamp_sample_args* args, void* stream);
+
 /* Per-kernel timing hook, off by default (the role CBv2StepProfiler plays for
  * the reference, StepProfilerV2.swift:15-60).  While enabled, each
  * lsamp_sample call that is not under graph capture records three HIP events

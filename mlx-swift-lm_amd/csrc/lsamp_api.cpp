@@ -35,6 +35,22 @@ lsamp_status ok() {
   return LSAMP_OK;
 }
 
+}  // namespace
+
+lsamp_status lsamp::set_error(lsamp_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+lsamp_status lsamp::clear_error() { return ok(); }
+
+namespace {
+
 // Restores the caller's current device on scope exit.
 struct DeviceGuard {
   int prev = -1;
@@ -61,8 +77,7 @@ struct lsamp_context {
   uint32_t* arrive_rank; // [max_rows] (in `block`)
   int32_t* vrow_ptr;     // [max_rows] penalty-aware verify: per-position runs (in `block`)
   int32_t* vrow_len;     // [max_rows] (in `block`)
-  uint32_t* smask;       // [max_rows][smask_words] bitmask with suppressed ids (in `block`)
-  int32_t smask_words;
+  WorkspaceViews views;  // every part of `block`
   void* block;  // single device allocation backing the workspace
   size_t bytes;
   // timing hook
@@ -148,6 +163,113 @@ lsamp_status rank_common(lsamp_context* ctx, RankPlan& P, int32_t min_vocab, voi
 
 }  // namespace
 
+lsamp_status lsamp::sample_step(const WorkspaceViews& v, int32_t cus, const int32_t blocks_per_cu[3],
+                                int32_t mode, const lsamp_sample_args* a, void* stream,
+                                void* const* ev, lsamp_launch_info* last) {
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->semantics != LSAMP_SEM_MLXLM && a->semantics != LSAMP_SEM_CBV2)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown semantics %d", a->semantics);
+  if (a->dtype != LSAMP_DTYPE_F32 && a->dtype != LSAMP_DTYPE_BF16 && a->dtype != LSAMP_DTYPE_F16)
+    return fail(LSAMP_ERR_DTYPE, "unsupported dtype %d", a->dtype);
+  if (a->rows <= 0 || a->rows > v.ws.max_rows)
+    return fail(a->rows <= 0 ? LSAMP_ERR_SHAPE : LSAMP_ERR_CAPACITY,
+                "rows %d outside [1, %d]", a->rows, v.ws.max_rows);
+  if (a->vocab <= 0 || a->vocab > v.ws.max_vocab)
+    return fail(a->vocab <= 0 ? LSAMP_ERR_SHAPE : LSAMP_ERR_CAPACITY,
+                "vocab %d outside [1, %d]", a->vocab, v.ws.max_vocab);
+  if (a->row_stride < a->vocab)
+    return fail(LSAMP_ERR_SHAPE, "row_stride %lld < vocab %d", (long long)a->row_stride, a->vocab);
+  if (!a->logits || !a->params || !a->tokens)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "logits, params and tokens are required");
+  if (!a->uniforms && !a->philox_keys)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "either uniforms or philox_keys is required");
+  if ((a->penalty_row_ptr == nullptr) != (a->penalty_entries == nullptr))
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "penalty_row_ptr and penalty_entries go together");
+  if (a->penalty_row_len && !a->penalty_row_ptr)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "penalty_row_len needs penalty_row_ptr");
+  if (a->bitmask) {
+    if (a->mask_words <= 0 || a->mask_bits < 0)
+      return fail(LSAMP_ERR_SHAPE, "mask_words %d / mask_bits %d invalid", a->mask_words,
+                  a->mask_bits);
+    // xgrammar: vocab_size <= bitmask words * 32 (grammar_matcher.cc:219-222)
+    if ((int64_t)a->mask_bits > (int64_t)a->mask_words * 32)
+      return fail(LSAMP_ERR_SHAPE, "mask_bits %d exceed %d words", a->mask_bits, a->mask_words);
+    if (a->mask_tail != LSAMP_MASK_TAIL_KEEP && a->mask_tail != LSAMP_MASK_TAIL_FORBID)
+      return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown mask_tail %d", a->mask_tail);
+  }
+  if (a->n_suppress < 0 || a->n_suppress > LSAMP_MAX_SUPPRESS)
+    return fail(LSAMP_ERR_SHAPE, "n_suppress %d outside [0, %d]", a->n_suppress,
+                LSAMP_MAX_SUPPRESS);
+  if (a->n_suppress > 0 && !a->suppress_ids)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "suppress_ids is NULL");
+  SamplePlan P{};
+  P.semantics = a->semantics;
+  P.rows = a->rows;
+  P.vocab = a->vocab;
+  P.dtype = a->dtype;
+  P.row_stride = a->row_stride;
+  const int32_t bpc = blocks_per_cu[a->dtype];
+  const int32_t slots = cus * (bpc > 0 ? bpc : 1);
+  plan_slices(a->rows, a->vocab, slots, &P.slices, &P.slice_len, &P.nchunks);
+  P.fused = mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;
+  P.rows_per_round = P.fused ? slots / P.slices : a->rows;
+  const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
+  P.aligned = aligned16(a->logits) && ((size_t)a->row_stride * es) % 16 == 0;
+  P.logits = a->logits;
+  P.logits2 = a->logits;
+  P.rows_split = a->rows;
+  P.params = a->params;
+  P.row_ptr = a->penalty_row_ptr;
+  P.row_len = a->penalty_row_len;
+  P.entries = a->penalty_entries;
+  P.bitmask = a->bitmask;
+  P.mask_words = a->mask_words;
+  P.mask_bits = a->mask_bits;
+  P.mask_tail = a->mask_tail;
+  P.uniforms = a->uniforms;
+  P.philox_keys = a->philox_keys;
+  P.probe_tokens = a->probe_tokens;
+  P.tokens = a->tokens;
+  P.row_flags = a->row_flags;
+  P.processed = a->processed;
+  P.keep = a->keep;
+  P.stats = a->stats;
+  P.stats_full = a->stats != nullptr;
+  if (a->n_suppress > 0) {
+    // the suppressed ids and the caller's bitmask become one bitmask over
+    // the whole vocabulary, which the sampling kernels apply as any other
+    SuppressPlan S{};
+    S.rows = a->rows;
+    S.vocab = a->vocab;
+    S.words = (a->vocab + 31) / 32;
+    S.bitmask = a->bitmask;
+    S.mask_words = a->mask_words;
+    S.mask_bits = a->mask_bits;
+    S.mask_tail = a->mask_tail;
+    S.ids = a->suppress_ids;
+    S.n = a->n_suppress;
+    S.out = v.smask;
+    const int err = launch_suppress_mask(S, stream);
+    if (err != 0)
+      return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+    P.bitmask = v.smask;
+    P.mask_words = S.words;
+    P.mask_bits = a->vocab;
+    P.mask_tail = LSAMP_MASK_TAIL_KEEP;
+  }
+  last->fused = P.fused;
+  last->slices = P.slices;
+  last->slice_len = P.slice_len;
+  last->rows_per_round = P.rows_per_round;
+  last->grid = P.fused ? (P.rows < P.rows_per_round ? P.rows : P.rows_per_round) * P.slices
+                       : P.rows * P.slices;
+  const int err = launch_sample(v.ws, P, stream, ev);
+  if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
+                            hipGetErrorString((hipError_t)err));
+  return ok();
+}
+
+
 extern "C" {
 
 const char* lsamp_last_error(void) { return g_last_error.c_str(); }
@@ -190,35 +312,7 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   if (hipGetDeviceProperties(&prop, device) != hipSuccess)
     return fail(LSAMP_ERR_DEVICE, "hipGetDeviceProperties failed");
 
-  const size_t R = (size_t)max_rows;
-  const size_t chunks = (size_t)((max_vocab + kChunk - 1) / kChunk);
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    const size_t o = off;
-    off = align_up(off + bytes, 256);
-    return o;
-  };
-  const size_t o_sum = take(R * kMaxSlices * sizeof(SliceSummary));
-  const size_t o_rows = take(R * sizeof(RowInfo));
-  const size_t o_chunk = take(R * chunks * sizeof(uint64_t));
-  const size_t o_cand = take(R * kCandCap * sizeof(Candidate));
-  const size_t o_klist = take(R * kMaxSlices * kKeptCap * sizeof(KeptItem));
-  const size_t o_part = take(R * kMaxSlices * sizeof(SelectPartial));
-  const size_t o_status = take(sizeof(uint32_t));
-  const size_t o_cc = take(R * sizeof(uint32_t));
-  const size_t o_as = take(R * sizeof(uint32_t));
-  const size_t o_asel = take(R * sizeof(uint32_t));
-  const size_t o_vstats = take(R * sizeof(lsamp_row_stats));
-  const size_t o_vtok = take(R * sizeof(int32_t));
-  const size_t o_vfl = take(R * sizeof(uint32_t));
-  const size_t o_rpart = take(R * kRankMaxSlices * sizeof(RankSlice));
-  const size_t o_arank = take(R * sizeof(uint32_t));
-  const size_t o_vrp = take(R * sizeof(int32_t));
-  const size_t o_vrl = take(R * sizeof(int32_t));
-  const size_t smask_words = (size_t)((max_vocab + 31) / 32);
-  const size_t o_smask = take(R * smask_words * sizeof(uint32_t));
-  const size_t total = off;
-
+  const size_t total = workspace_layout((size_t)max_rows, (size_t)max_vocab).total;
   void* block = nullptr;
   if (hipMalloc(&block, total) != hipSuccess)
     return fail(LSAMP_ERR_DEVICE, "hipMalloc(%zu) failed", total);
@@ -234,30 +328,12 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   for (int dt = 0; dt < 3; ++dt) ctx->blocks_per_cu[dt] = fused_blocks_per_cu(dt);
   ctx->block = block;
   ctx->bytes = total;
-  char* b = reinterpret_cast<char*>(block);
-  Workspace& ws = ctx->ws;
-  ws.max_rows = max_rows;
-  ws.max_vocab = max_vocab;
-  ws.max_chunks = (int32_t)chunks;
-  ws.summaries = reinterpret_cast<SliceSummary*>(b + o_sum);
-  ws.rows = reinterpret_cast<RowInfo*>(b + o_rows);
-  ws.chunk_w = reinterpret_cast<uint64_t*>(b + o_chunk);
-  ws.cands = reinterpret_cast<Candidate*>(b + o_cand);
-  ws.klist = reinterpret_cast<KeptItem*>(b + o_klist);
-  ws.status = reinterpret_cast<uint32_t*>(b + o_status);
-  ws.partials = reinterpret_cast<SelectPartial*>(b + o_part);
-  ws.cand_count = reinterpret_cast<uint32_t*>(b + o_cc);
-  ws.arrive_stats = reinterpret_cast<uint32_t*>(b + o_as);
-  ws.arrive_select = reinterpret_cast<uint32_t*>(b + o_asel);
-  ws.vstats = reinterpret_cast<lsamp_row_stats*>(b + o_vstats);
-  ws.vtokens = reinterpret_cast<int32_t*>(b + o_vtok);
-  ws.vflags = reinterpret_cast<uint32_t*>(b + o_vfl);
-  ctx->rank_part = reinterpret_cast<RankSlice*>(b + o_rpart);
-  ctx->arrive_rank = reinterpret_cast<uint32_t*>(b + o_arank);
-  ctx->vrow_ptr = reinterpret_cast<int32_t*>(b + o_vrp);
-  ctx->vrow_len = reinterpret_cast<int32_t*>(b + o_vrl);
-  ctx->smask = reinterpret_cast<uint32_t*>(b + o_smask);
-  ctx->smask_words = (int32_t)smask_words;
+  ctx->views = bind_workspace(reinterpret_cast<char*>(block), max_rows, max_vocab);
+  ctx->ws = ctx->views.ws;
+  ctx->rank_part = ctx->views.rank_part;
+  ctx->arrive_rank = ctx->views.arrive_rank;
+  ctx->vrow_ptr = ctx->views.vrow_ptr;
+  ctx->vrow_len = ctx->views.vrow_len;
   *out = ctx;
   return ok();
 }
@@ -361,117 +437,18 @@ lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, dou
 
 lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* stream) {
   if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
-  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
-  if (a->semantics != LSAMP_SEM_MLXLM && a->semantics != LSAMP_SEM_CBV2)
-    return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown semantics %d", a->semantics);
-  if (a->dtype != LSAMP_DTYPE_F32 && a->dtype != LSAMP_DTYPE_BF16 && a->dtype != LSAMP_DTYPE_F16)
-    return fail(LSAMP_ERR_DTYPE, "unsupported dtype %d", a->dtype);
-  if (a->rows <= 0 || a->rows > ctx->ws.max_rows)
-    return fail(a->rows <= 0 ? LSAMP_ERR_SHAPE : LSAMP_ERR_CAPACITY,
-                "rows %d outside [1, %d]", a->rows, ctx->ws.max_rows);
-  if (a->vocab <= 0 || a->vocab > ctx->ws.max_vocab)
-    return fail(a->vocab <= 0 ? LSAMP_ERR_SHAPE : LSAMP_ERR_CAPACITY,
-                "vocab %d outside [1, %d]", a->vocab, ctx->ws.max_vocab);
-  if (a->row_stride < a->vocab)
-    return fail(LSAMP_ERR_SHAPE, "row_stride %lld < vocab %d", (long long)a->row_stride, a->vocab);
-  if (!a->logits || !a->params || !a->tokens)
-    return fail(LSAMP_ERR_INVALID_ARGUMENT, "logits, params and tokens are required");
-  if (!a->uniforms && !a->philox_keys)
-    return fail(LSAMP_ERR_INVALID_ARGUMENT, "either uniforms or philox_keys is required");
-  if ((a->penalty_row_ptr == nullptr) != (a->penalty_entries == nullptr))
-    return fail(LSAMP_ERR_INVALID_ARGUMENT, "penalty_row_ptr and penalty_entries go together");
-  if (a->penalty_row_len && !a->penalty_row_ptr)
-    return fail(LSAMP_ERR_INVALID_ARGUMENT, "penalty_row_len needs penalty_row_ptr");
-  if (a->bitmask) {
-    if (a->mask_words <= 0 || a->mask_bits < 0)
-      return fail(LSAMP_ERR_SHAPE, "mask_words %d / mask_bits %d invalid", a->mask_words,
-                  a->mask_bits);
-    // xgrammar: vocab_size <= bitmask words * 32 (grammar_matcher.cc:219-222)
-    if ((int64_t)a->mask_bits > (int64_t)a->mask_words * 32)
-      return fail(LSAMP_ERR_SHAPE, "mask_bits %d exceed %d words", a->mask_bits, a->mask_words);
-    if (a->mask_tail != LSAMP_MASK_TAIL_KEEP && a->mask_tail != LSAMP_MASK_TAIL_FORBID)
-      return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown mask_tail %d", a->mask_tail);
-  }
-  if (a->n_suppress < 0 || a->n_suppress > LSAMP_MAX_SUPPRESS)
-    return fail(LSAMP_ERR_SHAPE, "n_suppress %d outside [0, %d]", a->n_suppress,
-                LSAMP_MAX_SUPPRESS);
-  if (a->n_suppress > 0 && !a->suppress_ids)
-    return fail(LSAMP_ERR_INVALID_ARGUMENT, "suppress_ids is NULL");
-  SamplePlan P{};
-  P.semantics = a->semantics;
-  P.rows = a->rows;
-  P.vocab = a->vocab;
-  P.dtype = a->dtype;
-  P.row_stride = a->row_stride;
-  const int32_t bpc = ctx->blocks_per_cu[a->dtype];
-  const int32_t slots = ctx->cus * (bpc > 0 ? bpc : 1);
-  plan_slices(a->rows, a->vocab, slots, &P.slices, &P.slice_len, &P.nchunks);
-  P.fused = ctx->mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;
-  P.rows_per_round = P.fused ? slots / P.slices : a->rows;
-  const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
-  P.aligned = aligned16(a->logits) && ((size_t)a->row_stride * es) % 16 == 0;
-  P.logits = a->logits;
-  P.logits2 = a->logits;
-  P.rows_split = a->rows;
-  P.params = a->params;
-  P.row_ptr = a->penalty_row_ptr;
-  P.row_len = a->penalty_row_len;
-  P.entries = a->penalty_entries;
-  P.bitmask = a->bitmask;
-  P.mask_words = a->mask_words;
-  P.mask_bits = a->mask_bits;
-  P.mask_tail = a->mask_tail;
-  P.uniforms = a->uniforms;
-  P.philox_keys = a->philox_keys;
-  P.probe_tokens = a->probe_tokens;
-  P.tokens = a->tokens;
-  P.row_flags = a->row_flags;
-  P.processed = a->processed;
-  P.keep = a->keep;
-  P.stats = a->stats;
-  P.stats_full = a->stats != nullptr;
   DeviceGuard guard(ctx->device);
-  if (a->n_suppress > 0) {
-    // the suppressed ids and the caller's bitmask become one bitmask over
-    // the whole vocabulary, which the sampling kernels apply as any other
-    SuppressPlan S{};
-    S.rows = a->rows;
-    S.vocab = a->vocab;
-    S.words = (a->vocab + 31) / 32;
-    S.bitmask = a->bitmask;
-    S.mask_words = a->mask_words;
-    S.mask_bits = a->mask_bits;
-    S.mask_tail = a->mask_tail;
-    S.ids = a->suppress_ids;
-    S.n = a->n_suppress;
-    S.out = ctx->smask;
-    const int err = launch_suppress_mask(S, stream);
-    if (err != 0)
-      return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
-    P.bitmask = ctx->smask;
-    P.mask_words = S.words;
-    P.mask_bits = a->vocab;
-    P.mask_tail = LSAMP_MASK_TAIL_KEEP;
-  }
   void* const* ev = nullptr;
   if (ctx->timing && ctx->timed < lsamp_context::kTimedCalls) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(reinterpret_cast<hipStream_t>(stream), &cs) == hipSuccess &&
-        cs == hipStreamCaptureStatusNone) {
+        cs == hipStreamCaptureStatusNone)
       ev = reinterpret_cast<void* const*>(ctx->events + 3 * ctx->timed);
-      ++ctx->timed;
-    }
   }
-  ctx->last.fused = P.fused;
-  ctx->last.slices = P.slices;
-  ctx->last.slice_len = P.slice_len;
-  ctx->last.rows_per_round = P.rows_per_round;
-  ctx->last.grid = P.fused ? (P.rows < P.rows_per_round ? P.rows : P.rows_per_round) * P.slices
-                           : P.rows * P.slices;
-  const int err = launch_sample(ctx->ws, P, stream, ev);
-  if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
-                            hipGetErrorString((hipError_t)err));
-  return ok();
+  const lsamp_status st =
+      sample_step(ctx->views, ctx->cus, ctx->blocks_per_cu, ctx->mode, a, stream, ev, &ctx->last);
+  if (st == LSAMP_OK && ev) ++ctx->timed;
+  return st;
 }
 
 lsamp_status lsamp_step(lsamp_context* ctx, const lsamp_step_args* a, void* stream) {

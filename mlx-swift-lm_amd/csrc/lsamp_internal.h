@@ -166,6 +166,46 @@ struct Workspace {
   uint32_t* vflags;         // [max_rows]
 };
 
+// Byte layout of a workspace for max_rows rows of up to max_vocab logits:
+// offsets from its base, every part 256-byte aligned.  The words that must
+// start at zero (the status word, candidate counts, arrival counters) form
+// the one range [zero_begin, zero_end); the kernels return them to zero at
+// the end of every step.
+struct WorkspaceLayout {
+  size_t sum, rows, chunk, cand, klist, part, status, cc, as, asel;
+  size_t vstats, vtok, vfl, rpart, arank, vrp, vrl, smask;
+  size_t zero_begin, zero_end, total;
+};
+constexpr size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
+  const size_t chunks = (max_vocab + kChunk - 1) / kChunk;
+  const size_t words = (max_vocab + 31) / 32;
+  WorkspaceLayout L{};
+  size_t off = 0;
+  L.sum = off;    off = align256(off + R * kMaxSlices * sizeof(SliceSummary));
+  L.rows = off;   off = align256(off + R * sizeof(RowInfo));
+  L.chunk = off;  off = align256(off + R * chunks * sizeof(uint64_t));
+  L.cand = off;   off = align256(off + R * kCandCap * sizeof(Candidate));
+  L.klist = off;  off = align256(off + R * kMaxSlices * kKeptCap * sizeof(KeptItem));
+  L.part = off;   off = align256(off + R * kMaxSlices * sizeof(SelectPartial));
+  L.zero_begin = off;
+  L.status = off; off = align256(off + sizeof(uint32_t));
+  L.cc = off;     off = align256(off + R * sizeof(uint32_t));
+  L.as = off;     off = align256(off + R * sizeof(uint32_t));
+  L.asel = off;   off = align256(off + R * sizeof(uint32_t));
+  L.zero_end = off;
+  L.vstats = off; off = align256(off + R * sizeof(lsamp_row_stats));
+  L.vtok = off;   off = align256(off + R * sizeof(int32_t));
+  L.vfl = off;    off = align256(off + R * sizeof(uint32_t));
+  L.rpart = off;  off = align256(off + R * kRankMaxSlices * sizeof(RankSlice));
+  L.arank = off;  off = align256(off + R * sizeof(uint32_t));
+  L.vrp = off;    off = align256(off + R * sizeof(int32_t));
+  L.vrl = off;    off = align256(off + R * sizeof(int32_t));
+  L.smask = off;  off = align256(off + R * words * sizeof(uint32_t));
+  L.total = off;
+  return L;
+}
+
 struct RankPlan {
   int32_t rows;
   int32_t vocab;
@@ -332,5 +372,61 @@ struct SuppressPlan {
   uint32_t* out;            // [rows, words]
 };
 int launch_suppress_mask(const SuppressPlan& plan, void* stream);
+
+// Device views of a workspace laid out by workspace_layout at `base`.
+struct WorkspaceViews {
+  Workspace ws;
+  RankSlice* rank_part;   // [max_rows][kRankMaxSlices]
+  uint32_t* arrive_rank;  // [max_rows]
+  int32_t* vrow_ptr;      // [max_rows] penalty-aware verify: per-position runs
+  int32_t* vrow_len;      // [max_rows]
+  uint32_t* smask;        // [max_rows][smask_words]: bitmask with suppressed ids
+  int32_t smask_words;
+  char* zero_begin;       // the words that must start at zero
+  size_t zero_bytes;
+};
+inline WorkspaceViews bind_workspace(char* b, int32_t max_rows, int32_t max_vocab) {
+  const WorkspaceLayout L = workspace_layout((size_t)max_rows, (size_t)max_vocab);
+  WorkspaceViews v{};
+  Workspace& ws = v.ws;
+  ws.max_rows = max_rows;
+  ws.max_vocab = max_vocab;
+  ws.max_chunks = (max_vocab + kChunk - 1) / kChunk;
+  ws.summaries = reinterpret_cast<SliceSummary*>(b + L.sum);
+  ws.rows = reinterpret_cast<RowInfo*>(b + L.rows);
+  ws.chunk_w = reinterpret_cast<uint64_t*>(b + L.chunk);
+  ws.cands = reinterpret_cast<Candidate*>(b + L.cand);
+  ws.klist = reinterpret_cast<KeptItem*>(b + L.klist);
+  ws.partials = reinterpret_cast<SelectPartial*>(b + L.part);
+  ws.status = reinterpret_cast<uint32_t*>(b + L.status);
+  ws.cand_count = reinterpret_cast<uint32_t*>(b + L.cc);
+  ws.arrive_stats = reinterpret_cast<uint32_t*>(b + L.as);
+  ws.arrive_select = reinterpret_cast<uint32_t*>(b + L.asel);
+  ws.vstats = reinterpret_cast<lsamp_row_stats*>(b + L.vstats);
+  ws.vtokens = reinterpret_cast<int32_t*>(b + L.vtok);
+  ws.vflags = reinterpret_cast<uint32_t*>(b + L.vfl);
+  v.rank_part = reinterpret_cast<RankSlice*>(b + L.rpart);
+  v.arrive_rank = reinterpret_cast<uint32_t*>(b + L.arank);
+  v.vrow_ptr = reinterpret_cast<int32_t*>(b + L.vrp);
+  v.vrow_len = reinterpret_cast<int32_t*>(b + L.vrl);
+  v.smask = reinterpret_cast<uint32_t*>(b + L.smask);
+  v.smask_words = (max_vocab + 31) / 32;
+  v.zero_begin = b + L.zero_begin;
+  v.zero_bytes = L.zero_end - L.zero_begin;
+  return v;
+}
+
+// Validation, planning and launch of one sampling step (lsamp_sample) over a
+// workspace; records the launch shape in *last.  Sets the thread's last
+// error and returns its status.
+lsamp_status sample_step(const WorkspaceViews& v, int32_t cus, const int32_t blocks_per_cu[3],
+                         int32_t mode, const lsamp_sample_args* a, void* stream,
+                         void* const* events, lsamp_launch_info* last);
+// The thread's last-error string (xgrammar_c.h:63-69 convention).
+lsamp_status set_error(lsamp_status st, const char* fmt, ...);
+lsamp_status clear_error();
+// Zero `bytes` (a multiple of 4) at `p` on `stream` with a fill kernel (no
+// memset node, so the call can be captured in a HIP graph).
+int launch_zero_words(void* p, size_t bytes, void* stream);
 
 }  // namespace lsamp

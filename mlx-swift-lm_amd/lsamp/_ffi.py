@@ -298,6 +298,8 @@ def load_library(path: str | None = None):
     lib.lsamp_context_set_mode.restype = c_int32
     lib.lsamp_context_read_status.argtypes = [c_void_p, POINTER(c_uint32)]
     lib.lsamp_context_read_status.restype = c_int32
+    lib.lsamp_sample_noalloc.argtypes = [POINTER(SampleArgs), c_void_p]
+    lib.lsamp_sample_noalloc.restype = c_int32
     lib.lsamp_set_spin_test.argtypes = [c_int32, c_int32]
     lib.lsamp_set_spin_test.restype = c_int32
     lib.lsamp_context_last_launch.argtypes = [c_void_p, POINTER(LaunchInfo)]
