@@ -440,7 +440,7 @@ def bench_config(args, n):
     kw = dict(semantics=cfg["semantics"], row_ptr=cfg.get("row_ptr"), entries=cfg.get("entries"),
               uniforms=cfg["uniforms"])
     if cfg.get("bitmask") is not None:
-        kw.update(bitmask=cfg["bitmask"], mask_bits=cfg["mask_bits"], mask_tail=cfg["mask_tail"])
+        kw.update(bitmask=cfg["bitmask"], mask_bits=cfg["mask_bits"], mask_tail=cfg.get("mask_tail", 0))
     preps = [ctx.prepare_sample(copies[i], cfg["params"], **kw) for i in range(R)]
     stream = torch.cuda.Stream(device=dev)
     with torch.cuda.stream(stream):
@@ -492,7 +492,7 @@ def bench_config(args, n):
                 kw2["entries"] = cfg["entries"][rp[0]:rp[nrows]]
             if cfg.get("bitmask") is not None:
                 kw2.update(bitmask=cfg["bitmask"][r], mask_bits=cfg["mask_bits"],
-                           mask_tail=cfg["mask_tail"])
+                           mask_tail=cfg.get("mask_tail", 0))
             O.sample(semantics=cfg["semantics"], logits=cfg["logits"][r], dtype=cfg["dtype"],
                      params=cfg["params"][r], uniforms=cfg["uniforms"][r], threads=threads, **kw2)
 

@@ -203,7 +203,17 @@ typedef struct lsamp_sample_args {
    * does not change a value).                                               */
   const int32_t* suppress_ids;
   int32_t n_suppress; /* 0 .. LSAMP_MAX_SUPPRESS                             */
+
+  /* [rows] HOST copy of `params`, or NULL.  Used only to choose the kernel
+   * arrangement: when every row is an argmax row, or a CBv2 row whose top-k is
+   * active and at most LSAMP_TOPK_MAX_K, the step runs the one-pass top-k
+   * kernel (lsamp_launch_info.fused = 2).  It must describe `params`; a row
+   * of `params` that the top-k kernel cannot sample comes back as token -1
+   * with LSAMP_ROW_OVERFLOW. */
+  const lsamp_row_params* params_host;
 } lsamp_sample_args;
+
+#define LSAMP_TOPK_MAX_K 64
 
 #define LSAMP_MAX_SUPPRESS 65536
 
@@ -311,11 +321,14 @@ lsamp_status lsamp_context_set_timing(lsamp_context* ctx, int32_t enable);
 lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, double* select_ms,
                                        int64_t* calls);
 
-/* Kernel arrangement.  AUTO (default) runs one kernel whose grid fits on the
- * device at once (the slices of a row hand their results to each other while
- * the logits stay in registers); SPLIT runs two kernels with no co-residency
- * requirement (the second re-reads each slice from L2).  Both give identical
- * results. */
+/* Kernel arrangement.  AUTO (default) runs the one-pass top-k kernel when
+ * `params_host` shows every row is argmax or CBv2 top-k <= LSAMP_TOPK_MAX_K
+ * (each slice of a row publishes its best keys; the slice that starts last
+ * merges and draws; no co-residency needed), else one kernel whose grid fits
+ * on the device at once (the slices of a row hand their results to each
+ * other while the logits stay in registers).  FUSED never takes the top-k
+ * kernel; SPLIT runs two kernels with no co-residency requirement (the
+ * second re-reads each slice from L2).  All give identical results. */
 #define LSAMP_MODE_AUTO 0
 #define LSAMP_MODE_FUSED 1
 #define LSAMP_MODE_SPLIT 2
@@ -339,8 +352,8 @@ lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
 lsamp_status lsamp_set_spin_test(int32_t device, int32_t polls);
 
 /* Launch shape of the context's last lsamp_sample call (diagnostics; no
- * device work): fused (1) or split (0), slices per row, tokens per slice,
- * rows per round of the fused grid, work-groups per kernel launch. */
+ * device work): top-k (2), fused (1) or split (0), slices per row, tokens per
+ * slice, rows per round of the fused grid, work-groups per kernel launch. */
 typedef struct lsamp_launch_info {
   int32_t fused;
   int32_t slices;

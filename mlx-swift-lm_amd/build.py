@@ -38,8 +38,8 @@ DEVICE = [
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES_HIP = ["lsamp_kernels.hip", "lsamp_rank.hip", "lsamp_commit.hip", "lsamp_mask.hip",
-               "lsamp_noalloc.hip"]
+SOURCES_HIP = ["lsamp_kernels.hip", "lsamp_topk.hip", "lsamp_rank.hip", "lsamp_commit.hip",
+               "lsamp_mask.hip", "lsamp_noalloc.hip"]
 SOURCES_CPP = ["lsamp_api.cpp"]
 HEADERS = ["lsamp_internal.h", "lsamp_device.h"]
 

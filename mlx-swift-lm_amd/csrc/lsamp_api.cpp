@@ -71,7 +71,7 @@ struct lsamp_context {
   int32_t device;
   int32_t cus;
   int32_t mode = LSAMP_MODE_AUTO;
-  int32_t blocks_per_cu[3] = {0, 0, 0};  // fused-kernel occupancy per dtype
+  DeviceShape shape{};  // CUs and kernel occupancies
   Workspace ws;
   RankSlice* rank_part;  // [max_rows][kRankMaxSlices] (in `block`)
   uint32_t* arrive_rank; // [max_rows] (in `block`)
@@ -163,9 +163,26 @@ lsamp_status rank_common(lsamp_context* ctx, RankPlan& P, int32_t min_vocab, voi
 
 }  // namespace
 
-lsamp_status lsamp::sample_step(const WorkspaceViews& v, int32_t cus, const int32_t blocks_per_cu[3],
-                                int32_t mode, const lsamp_sample_args* a, void* stream,
-                                void* const* ev, lsamp_launch_info* last) {
+// Can the one-pass top-k kernel sample every row (the host copy of the
+// parameters says so)?  Argmax rows (a sampled row whose temperature defines
+// no distribution draws the argmax too), and CBv2 rows with an active top-k
+// of at most kTopkMaxK.
+static bool topk_eligible(const lsamp_sample_args* a) {
+  if (!a->params_host) return false;
+  for (int32_t r = 0; r < a->rows; ++r) {
+    const lsamp_row_params& p = a->params_host[r];
+    const bool argmax = p.kind == LSAMP_KIND_ARGMAX ||
+                        !(p.temperature > 0.0f && p.temperature < INFINITY);
+    if (argmax) continue;
+    if (a->semantics != LSAMP_SEM_CBV2 || p.kind != LSAMP_KIND_FILTERED) return false;
+    if (!(p.top_k > 0 && p.top_k < a->vocab && p.top_k <= kTopkMaxK)) return false;
+  }
+  return true;
+}
+
+lsamp_status lsamp::sample_step(const WorkspaceViews& v, const DeviceShape& d, int32_t mode,
+                                const lsamp_sample_args* a, void* stream, void* const* ev,
+                                lsamp_launch_info* last) {
   if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
   if (a->semantics != LSAMP_SEM_MLXLM && a->semantics != LSAMP_SEM_CBV2)
     return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown semantics %d", a->semantics);
@@ -208,10 +225,13 @@ lsamp_status lsamp::sample_step(const WorkspaceViews& v, int32_t cus, const int3
   P.vocab = a->vocab;
   P.dtype = a->dtype;
   P.row_stride = a->row_stride;
-  const int32_t bpc = blocks_per_cu[a->dtype];
-  const int32_t slots = cus * (bpc > 0 ? bpc : 1);
-  plan_slices(a->rows, a->vocab, slots, &P.slices, &P.slice_len, &P.nchunks);
-  P.fused = mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;
+  const bool topk = mode == LSAMP_MODE_AUTO && d.topk_bpc[a->dtype] > 0 && topk_eligible(a);
+  const int32_t bpc = topk ? d.topk_bpc[a->dtype] : d.fused_bpc[a->dtype];
+  const int32_t slots = d.cus * (bpc > 0 ? bpc : 1);
+  // (the top-k kernel: one work-group per CU is enough, and fewer slices per
+  // row mean a shorter merge)
+  plan_slices(a->rows, a->vocab, topk ? d.cus : slots, &P.slices, &P.slice_len, &P.nchunks);
+  P.fused = !topk && mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;
   P.rows_per_round = P.fused ? slots / P.slices : a->rows;
   const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
   P.aligned = aligned16(a->logits) && ((size_t)a->row_stride * es) % 16 == 0;
@@ -257,13 +277,14 @@ lsamp_status lsamp::sample_step(const WorkspaceViews& v, int32_t cus, const int3
     P.mask_bits = a->vocab;
     P.mask_tail = LSAMP_MASK_TAIL_KEEP;
   }
-  last->fused = P.fused;
+  last->fused = topk ? 2 : P.fused;
   last->slices = P.slices;
   last->slice_len = P.slice_len;
   last->rows_per_round = P.rows_per_round;
-  last->grid = P.fused ? (P.rows < P.rows_per_round ? P.rows : P.rows_per_round) * P.slices
-                       : P.rows * P.slices;
-  const int err = launch_sample(v.ws, P, stream, ev);
+  last->grid = topk ? (P.rows + 7) / 8 * 8 * P.slices
+                    : P.fused ? (P.rows < P.rows_per_round ? P.rows : P.rows_per_round) * P.slices
+                              : P.rows * P.slices;
+  const int err = topk ? launch_topk(P, v.topk, stream, ev) : launch_sample(v.ws, P, stream, ev);
   if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                             hipGetErrorString((hipError_t)err));
   return ok();
@@ -325,7 +346,7 @@ lsamp_status lsamp_context_create(int32_t device, int32_t max_rows, int32_t max_
   lsamp_context* ctx = new lsamp_context();
   ctx->device = device;
   ctx->cus = prop.multiProcessorCount;
-  for (int dt = 0; dt < 3; ++dt) ctx->blocks_per_cu[dt] = fused_blocks_per_cu(dt);
+  ctx->shape = query_device_shape(prop.multiProcessorCount);
   ctx->block = block;
   ctx->bytes = total;
   ctx->views = bind_workspace(reinterpret_cast<char*>(block), max_rows, max_vocab);
@@ -446,7 +467,7 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
       ev = reinterpret_cast<void* const*>(ctx->events + 3 * ctx->timed);
   }
   const lsamp_status st =
-      sample_step(ctx->views, ctx->cus, ctx->blocks_per_cu, ctx->mode, a, stream, ev, &ctx->last);
+      sample_step(ctx->views, ctx->shape, ctx->mode, a, stream, ev, &ctx->last);
   if (st == LSAMP_OK && ev) ++ctx->timed;
   return st;
 }
@@ -851,7 +872,7 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   P.vocab = a->vocab;
   P.dtype = a->dtype;
   P.row_stride = a->vocab;
-  const int32_t bpc = ctx->blocks_per_cu[a->dtype];
+  const int32_t bpc = ctx->shape.fused_bpc[a->dtype];
   const int32_t slots = ctx->cus * (bpc > 0 ? bpc : 1);
   plan_slices(P.rows, P.vocab, slots, &P.slices, &P.slice_len, &P.nchunks);
   P.fused = ctx->mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;

@@ -166,14 +166,31 @@ struct Workspace {
   uint32_t* vflags;         // [max_rows]
 };
 
+// The one-pass top-k kernel (lsamp_topk.hip) takes steps whose rows are all
+// argmax rows or CBv2 rows with 0 < top-k <= kTopkMaxK.  Each row has a
+// ticket counter (taken when a slice starts; the slice with the last ticket
+// finalizes the row and returns the counter to zero), an epoch (the tag of
+// the step's payload words; the finalizer advances it) and, per slice, a
+// payload of tagged 64-bit words: tag (epoch + 1) in the high half, data in
+// the low half, so every word shows on its own whether it is this step's.
+constexpr int kTopkMaxK = 64;
+constexpr int kTopkHead = 8;                       // header words per slice
+constexpr int kTopkWords = kTopkHead + 2 * kTopkMaxK;  // + (value, id) per key
+struct TopkWs {
+  uint64_t* pub;     // [max_rows][kMaxSlices][kTopkWords]
+  uint32_t* ticket;  // [max_rows]
+  uint32_t* epoch;   // [max_rows]
+  uint32_t* status;  // the workspace's sticky status word
+};
+
 // Byte layout of a workspace for max_rows rows of up to max_vocab logits:
 // offsets from its base, every part 256-byte aligned.  The words that must
 // start at zero (the status word, candidate counts, arrival counters) form
 // the one range [zero_begin, zero_end); the kernels return them to zero at
 // the end of every step.
 struct WorkspaceLayout {
-  size_t sum, rows, chunk, cand, klist, part, status, cc, as, asel;
-  size_t vstats, vtok, vfl, rpart, arank, vrp, vrl, smask;
+  size_t sum, rows, chunk, cand, klist, part, status, cc, as, asel, tticket;
+  size_t vstats, vtok, vfl, rpart, arank, vrp, vrl, smask, tpub, tepoch;
   size_t zero_begin, zero_end, total;
 };
 constexpr size_t align256(size_t v) { return (v + 255) / 256 * 256; }
@@ -193,6 +210,7 @@ constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
   L.cc = off;     off = align256(off + R * sizeof(uint32_t));
   L.as = off;     off = align256(off + R * sizeof(uint32_t));
   L.asel = off;   off = align256(off + R * sizeof(uint32_t));
+  L.tticket = off; off = align256(off + R * sizeof(uint32_t));
   L.zero_end = off;
   L.vstats = off; off = align256(off + R * sizeof(lsamp_row_stats));
   L.vtok = off;   off = align256(off + R * sizeof(int32_t));
@@ -202,6 +220,10 @@ constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
   L.vrp = off;    off = align256(off + R * sizeof(int32_t));
   L.vrl = off;    off = align256(off + R * sizeof(int32_t));
   L.smask = off;  off = align256(off + R * words * sizeof(uint32_t));
+  // (the epochs are outside the zeroed range: a payload word left by an
+  // earlier step must never carry the current step's tag)
+  L.tpub = off;   off = align256(off + R * kMaxSlices * kTopkWords * sizeof(uint64_t));
+  L.tepoch = off; off = align256(off + R * sizeof(uint32_t));
   L.total = off;
   return L;
 }
@@ -297,6 +319,12 @@ struct VerifyPlan {
   uint8_t* accept_mask;
 };
 
+// The one-pass top-k kernel over a plan whose rows all qualify (see TopkWs);
+// `events` as launch_sample's.  Returns a hipError_t as int.
+int launch_topk(const SamplePlan& plan, const TopkWs& tw, void* stream, void* const* events);
+// Work-groups of the top-k kernel that fit on one CU.
+int topk_blocks_per_cu(int dtype);
+
 // Kernel launchers (lsamp_kernels.hip).  Return a hipError_t as int.
 // `events` (3 hipEvent_t or NULL) bracket the step: before, between the two
 // kernels (split mode; same as before in fused mode), after.
@@ -382,6 +410,7 @@ struct WorkspaceViews {
   int32_t* vrow_len;      // [max_rows]
   uint32_t* smask;        // [max_rows][smask_words]: bitmask with suppressed ids
   int32_t smask_words;
+  TopkWs topk;            // the one-pass top-k kernel's exchange
   char* zero_begin;       // the words that must start at zero
   size_t zero_bytes;
 };
@@ -411,17 +440,38 @@ inline WorkspaceViews bind_workspace(char* b, int32_t max_rows, int32_t max_voca
   v.vrow_len = reinterpret_cast<int32_t*>(b + L.vrl);
   v.smask = reinterpret_cast<uint32_t*>(b + L.smask);
   v.smask_words = (max_vocab + 31) / 32;
+  v.topk.pub = reinterpret_cast<uint64_t*>(b + L.tpub);
+  v.topk.ticket = reinterpret_cast<uint32_t*>(b + L.tticket);
+  v.topk.epoch = reinterpret_cast<uint32_t*>(b + L.tepoch);
+  v.topk.status = ws.status;
   v.zero_begin = b + L.zero_begin;
   v.zero_bytes = L.zero_end - L.zero_begin;
   return v;
 }
 
+// What the planner needs to know about a device: its CUs and how many
+// work-groups of each sampling kernel fit on one (per dtype).
+struct DeviceShape {
+  int32_t cus;
+  int32_t fused_bpc[3];
+  int32_t topk_bpc[3];
+};
+inline DeviceShape query_device_shape(int32_t cus) {
+  DeviceShape d{};
+  d.cus = cus;
+  for (int dt = 0; dt < 3; ++dt) {
+    d.fused_bpc[dt] = fused_blocks_per_cu(dt);
+    d.topk_bpc[dt] = topk_blocks_per_cu(dt);
+  }
+  return d;
+}
+
 // Validation, planning and launch of one sampling step (lsamp_sample) over a
 // workspace; records the launch shape in *last.  Sets the thread's last
 // error and returns its status.
-lsamp_status sample_step(const WorkspaceViews& v, int32_t cus, const int32_t blocks_per_cu[3],
-                         int32_t mode, const lsamp_sample_args* a, void* stream,
-                         void* const* events, lsamp_launch_info* last);
+lsamp_status sample_step(const WorkspaceViews& v, const DeviceShape& d, int32_t mode,
+                         const lsamp_sample_args* a, void* stream, void* const* events,
+                         lsamp_launch_info* last);
 // The thread's last-error string (xgrammar_c.h:63-69 convention).
 lsamp_status set_error(lsamp_status st, const char* fmt, ...);
 lsamp_status clear_error();

@@ -40,8 +40,7 @@ struct DeviceScratch {
   std::once_flag once;
   lsamp_status status = LSAMP_OK;
   char* ptr = nullptr;  // the device address of `scratch` on this device
-  int32_t cus = 0;
-  int32_t blocks_per_cu[3] = {0, 0, 0};
+  DeviceShape shape{};
   WorkspaceViews views{};
 };
 DeviceScratch g_devices[kMaxDevices];
@@ -59,8 +58,7 @@ void setup_device(DeviceScratch& d, int device) {
     return;
   }
   d.ptr = static_cast<char*>(ptr);
-  d.cus = cus;
-  for (int dt = 0; dt < 3; ++dt) d.blocks_per_cu[dt] = fused_blocks_per_cu(dt);
+  d.shape = query_device_shape(cus);
   d.views = bind_workspace(d.ptr, LSAMP_NOALLOC_MAX_ROWS, LSAMP_NOALLOC_MAX_VOCAB);
 }
 
@@ -101,5 +99,5 @@ extern "C" lsamp_status lsamp_sample_noalloc(const lsamp_sample_args* a, void* s
     return set_error(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                      hipGetErrorString((hipError_t)err));
   lsamp_launch_info last{};
-  return sample_step(d.views, d.cus, d.blocks_per_cu, LSAMP_MODE_AUTO, a, stream, nullptr, &last);
+  return sample_step(d.views, d.shape, LSAMP_MODE_AUTO, a, stream, nullptr, &last);
 }

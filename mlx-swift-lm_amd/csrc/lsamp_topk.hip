@@ -1,0 +1,901 @@
+// lsamp_topk.hip — the one-pass top-k kernel of a sampling step.
+//
+// Rows: argmax rows (either semantics) and CBv2 rows whose top-k is active
+// and at most kTopkMaxK.  The CBv2 keep rule (LogitsPipelineV2.
+// applyTopKTopPMinP, LogitsPipelineV2.swift:421-453) keeps only tokens ranked
+// below k, so a row needs just its k best keys (filter-space value
+// descending, token id ascending), its maximum and its total mass.
+//
+// One 512-thread work-group owns one slice of one row and keeps the slice in
+// registers from the load to the end: penalties, the grammar bitmask and the
+// temperature are applied as the reference orders them (lsamp_row.h), the
+// slice's best keys are found from a threshold, sorted, and published with
+// the slice's maximum and mass.  The slice that starts last finalizes the
+// row: it merges the slices' sorted lists, applies the keep rule and draws by
+// inverse CDF in token-id order (the fixed-point draw of lsamp.h).
+//
+// Placement: work-groups are dispatched round-robin over the 8 XCDs, so work-
+// group b runs on XCD b % 8.  Row r's slices are given to work-groups of XCD
+// r % 8, so a row's penalty entries and gathered logits are read through one
+// L2.
+//
+// Hand-off without co-residency: each work-group takes a ticket (an atomic on
+// the row's counter) as it starts.  Only the last ticket of a row waits, and
+// only for slices that started before it, which finish without waiting for
+// anyone.  Their payloads are 64-bit words tagged with the step's epoch, each
+// stored and loaded atomically, so every word shows on its own whether it is
+// this step's and no fence has to order them.
+//
+// Threshold: with min-p on, a token below the slice maximum + T ln(min-p)
+// cannot be kept (the row maximum is at least the slice's), so that bound is
+// tried first.  Otherwise (or when it leaves more than kCandCap tokens), the
+// k-th largest thread maximum bounds the slice's k-th key from below; a slice
+// whose candidates still overflow (many equal values) finds its exact k-th
+// key by a radix select over the 64-bit keys.
+#include <hip/hip_runtime.h>
+
+#include "lsamp_device.h"
+#include "lsamp_internal.h"
+#include "lsamp_row.h"
+
+namespace lsamp {
+namespace {
+
+using namespace dev;
+using namespace rowops;
+
+constexpr int kCandCap = 1024;   // candidate keys a slice keeps in LDS
+constexpr int kTkTauBins = 1024;  // thread-maximum histogram
+constexpr int kSpin = 1 << 20;   // polls before the finalizer gives a slice up
+static_assert(kTopkWords <= kThreads, "one payload word per thread");
+static_assert(kMaxSlices * kTopkMaxK <= kThreads, "one merged key per thread");
+
+// Header words of a slice's payload.
+enum : int { kHMax = 0, kHZHi, kHZLo, kHNpub, kHFlags, kHNinf };
+// Slice flags (header word kHFlags).
+constexpr uint32_t kFNonfinite = 1u;   // a raw logit is NaN or +-inf
+constexpr uint32_t kFLive = 2u;        // a token survived masking (finite or +inf)
+constexpr uint32_t kFPosInf = 4u;      // a transformed logit is +inf
+constexpr uint32_t kFEntOverflow = 8u; // more penalty entries than the slice table holds
+
+struct TopkLds {
+  uint32_t pen[kSliceWords];
+  int32_t etok[kSliceEntryCap];
+  float ex[kSliceEntryCap];
+  uint64_t cand[kCandCap];
+  int32_t racc[kCandCap];
+  uint64_t best[kMaxSlices * kTopkMaxK];  // slice s's sorted keys at s * kTopkMaxK
+  uint64_t merged[kTopkMaxK];             // the row's best keys, sorted
+  uint32_t hist[kTkTauBins];
+  // the row's slice headers (finalizer)
+  float hmax[kMaxSlices];
+  double hz[kMaxSlices];
+  int32_t hnpub[kMaxSlices];
+  uint32_t hflags[kMaxSlices];
+  int32_t hninf[kMaxSlices];
+  // reductions
+  float redf[kWaves];
+  float redf2[kWaves];
+  uint32_t redu[kWaves];
+  int32_t redi[kWaves];
+  uint64_t redz[kWaves];
+  int32_t misc[8];
+  uint64_t prefix;
+  int32_t ecount;
+  int32_t ncand;
+  uint32_t tag;
+  int32_t last;
+  int32_t lost;  // the finalizer gave up waiting for a slice
+};
+
+// Ordered 64-bit key of an element of the slice (filter space, id).
+__device__ __forceinline__ uint64_t elem_key(const RowCtx& c, float x, int32_t id) {
+  return cand_key(to_filter(c, x), id);
+}
+
+// The exact K-th largest key among a slice's tokens x >= t, for a slice
+// whose candidates overflow (many equal values): a radix select over the
+// 64-bit keys, eight bits a pass from the top, reading the slice again from
+// memory (L2) with the same exclusions as the first pass (the entry bitmap
+// and table in LDS, the grammar mask, NaN).  Called by the whole work-group.
+template <int DT>
+__device__ __noinline__ uint64_t kth_key_mem(const RowCtx c, const char* rowp,
+                                             const uint32_t* mrow, int32_t mask_words,
+                                             int32_t mask_bits, int32_t mask_tail, int32_t base32,
+                                             int32_t end32, int n_ent, float t, int K,
+                                             TopkLds& L) {
+  const int tid = (int)threadIdx.x;
+  uint64_t prefix = 0ull;
+  int need = K;
+#pragma unroll 1
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    const uint64_t hmask = shift == 56 ? 0ull : ~0ull << (shift + 8);
+    for (int i = tid; i < 256; i += kThreads) L.hist[i] = 0u;
+    __syncthreads();
+    auto count = [&](float x, int32_t id) {
+      if (!(x >= t) || !(x > kNegInf)) return;
+      const uint64_t key = elem_key(c, x, id);
+      if ((key & hmask) == prefix) atomicAdd(&L.hist[(key >> shift) & 255u], 1u);
+    };
+#pragma unroll 1
+    for (int32_t i = base32 + tid; i < end32; i += kThreads) {
+      const int32_t li = i - base32;
+      if ((L.pen[li >> 5] >> (li & 31)) & 1u) continue;  // an entry: from the table
+      if (mrow && !mask_allows(mrow, mask_words, mask_bits, mask_tail, i)) continue;
+      count(load_scalar<DT>(rowp, i), i);  // (a NaN fails x >= t)
+    }
+    for (int j = tid; j < n_ent; j += kThreads) count(L.ex[j], L.etok[j]);
+    __syncthreads();
+    if (tid < 64) {
+      // digits from the top: lane l holds digits 255 - 4l .. 252 - 4l
+      uint32_t cb[4];
+      uint32_t cs = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        cb[i] = L.hist[255 - (4 * tid + i)];
+        cs += cb[i];
+      }
+      const uint32_t ic = wave_incl_scan(cs);
+      const uint64_t hit = __ballot(ic >= (uint32_t)need);
+      const int f = hit ? __builtin_ctzll(hit) : 63;
+      uint32_t acc = read_lane(ic - cs, f);
+      int digit = 0, above = 0;
+      if (tid == f) {
+        for (int i = 0; i < 4; ++i) {
+          if (acc + cb[i] >= (uint32_t)need) {
+            digit = 255 - (4 * tid + i);
+            above = (int)acc;
+            break;
+          }
+          acc += cb[i];
+        }
+      }
+      digit = read_lane(digit, f);
+      above = read_lane(above, f);
+      if (tid == 0) {
+        L.misc[0] = digit;
+        L.misc[1] = above;
+      }
+    }
+    __syncthreads();
+    prefix |= (uint64_t)(uint32_t)L.misc[0] << shift;
+    need -= L.misc[1];
+  }
+  return prefix;
+}
+
+template <int DT>
+__device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, int row, int slice,
+                                          TopkLds& L) {
+  constexpr int N = Vec<DT>::N;
+  constexpr int Q = Slab<DT>::Q;
+  constexpr uint32_t FULL = (1u << N) - 1u;
+  constexpr int ES = Vec<DT>::ESIZE;
+  const int tid = fresh_tid();
+  const int l = tid & 63;
+  const int wv = tid >> 6;
+  const int G = P.slices;
+  const int64_t V = P.vocab;
+  const int64_t base = (int64_t)slice * P.slice_len;
+  const int64_t end = (base + P.slice_len < V) ? base + P.slice_len : V;
+  const char* rowp = row_base(P, row);
+  const bool aligned = P.aligned != 0;
+  const int32_t base32 = (int32_t)base, end32 = (int32_t)end;
+  const int nq = (P.slice_len + kThreads * N - 1) / (kThreads * N);
+
+  // ---------------------------------------------------------- A: loads
+  // the ticket and the epoch first (their round trip overlaps everything),
+  // then the parameters, the CSR bounds, the first penalty entries and the
+  // slice itself
+  uint32_t ticket = 0u, epoch = 0u;
+  if (tid == 0) {
+    epoch = __hip_atomic_load(&T.epoch[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ticket = __hip_atomic_fetch_add(&T.ticket[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const lsamp_row_params prm = load_params(P, row);
+  EntryPrefetch ep;
+  entry_bounds(P, row, ep);
+  const RowCtx c = make_ctx(P.semantics, prm);
+  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
+  prefetch_entries(P, tid, ep);
+  Slab<DT> S;
+  {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(rowp) + (size_t)base32 * ES, 0, aligned ? (end32 - base32) * ES : 0,
+        kBufferWord3);
+    const int lane_off = tid * 16;
+    // (every quad of the slab, without a branch: quads past the slice read
+    // zero, and straight-line loads let each later wait name its own quad)
+#pragma unroll
+    for (int g = 0; g < Q; ++g) {
+      const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, g * kThreads * 16, 0);
+      quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, make_uint4(w[0], w[1], w[2], w[3]));
+    }
+  }
+  // the row's sampler: argmax rows, and CBv2 rows with an active top-k of at
+  // most kTopkMaxK; any other row (a caller whose host copy of the
+  // parameters did not match) fails closed
+  const int Kr = short_k(c, prm, V);
+  const bool bad_row = Kr <= 0 || Kr > kTopkMaxK ||
+                       (c.kind == LSAMP_KIND_FILTERED && P.semantics != LSAMP_SEM_CBV2);
+  const int K = bad_row ? 1 : Kr;
+  const bool zon = c.kind != LSAMP_KIND_ARGMAX;
+  if (tid == 0) {
+    L.ncand = 0;
+    L.lost = 0;
+  }
+  for (int i = tid; i < kCandCap; i += kThreads) L.racc[i] = 0;
+
+  // ---------------------------------------------------------- B: entries
+  SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
+  EntryMarks em;
+  float emax = kNegInf;
+  mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
+  if (!aligned || (end32 & (N - 1)) != 0) {
+    // unaligned rows, or the row's last partial quad: element by element
+    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+      const int32_t i0 = base32 + (tid + g * kThreads) * N;
+      if (i0 >= end32 || (aligned && i0 + N <= end32)) return false;
+      uint32_t bb[N];
+#pragma unroll
+      for (int e = 0; e < N; ++e) bb[e] = i0 + e < end32 ? load_raw_bits<DT>(rowp, i0 + e) : 0u;
+      if constexpr (N == 4) {
+        v = make_uint4(bb[0], bb[1], bb[2], bb[3]);
+      } else {
+        v = make_uint4(bb[0] | (bb[1] << 16), bb[2] | (bb[3] << 16), bb[4] | (bb[5] << 16),
+                       bb[6] | (bb[7] << 16));
+      }
+      return true;
+    });
+  }
+
+  // ---------------------------------------------------------- C: pass 1
+  // Masked tokens, entry tokens (patched values in L.ex), lanes past the
+  // slice and NaNs become -inf in the registers.  The thread's maximum, its
+  // quads' maxima and its sum of exp((x - m) / T_f) (anchored at a quad
+  // maximum, re-anchored by an exact power of two) are taken as quads land.
+  const float lgz = (float)(1.4426950408889634 / c.tf);
+  const uint32_t* penw = L.pen + ((tid * N) >> 5);
+  constexpr int kQuadWords = kThreads * N / 32;
+  const uint32_t pen_shift = (uint32_t)((tid * N) & 31);
+  const int32_t lim = end32 - base32 - tid * N;
+  uint32_t pw = penw[0];
+  uint32_t nf_acc = 0u;
+  float xmax = kNegInf;
+  float zt = 0.0f, nbz = __FLT_MAX__;
+  int32_t ninf = 0;  // +inf tokens (counted in the rare quads that hold one)
+  for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
+    const int32_t i0 = base32 + (tid + g * kThreads) * N;
+    const uint32_t pcur = pw;
+    if (g + 1 < Q) pw = penw[(g + 1) * kQuadWords];
+    const uint32_t probe = nonfinite_probe<DT>(v);
+    nf_acc |= probe;
+    const int32_t rem = lim - g * (kThreads * N);
+    const uint32_t tail = ~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem));
+    uint32_t ex = ((pcur >> pen_shift) | tail) & FULL;
+    if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
+    if (nonfinite_seen<DT>(probe)) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float x = vec_elem<DT>(v, e);
+        if (x != x) ex |= 1u << e;
+      }
+    }
+    exclude_elems<DT>(v, ex);
+    const float qm = vec_max_nn<DT>(v);
+    xmax = __builtin_elementwise_maximum(xmax, qm);
+    if (qm == kPosInf) {
+#pragma unroll
+      for (int e = 0; e < N; ++e) ninf += vec_elem<DT>(v, e) == kPosInf ? 1 : 0;
+    }
+    if (zon) {
+      if (__builtin_fmaf(qm, lgz, nbz) > 64.0f) {
+        const float nn = -__builtin_ceilf(__builtin_amdgcn_fmed3f(qm * lgz, -0x1p20f, 0x1p20f));
+        zt = __builtin_ldexpf(zt, (int)__builtin_fmaxf(nn - nbz, -512.0f));
+        nbz = nn;
+      }
+#pragma unroll
+      for (int e = 0; e < N; ++e)
+        zt += __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(v, e), lgz, nbz));
+    }
+    return true;
+  });
+  const bool zref = nbz < __FLT_MAX__;
+  finish_slice_entries<DT>(P, c, prm, mrow, se, ep, em, emax);
+  xmax = __builtin_fmaxf(xmax, emax);
+  lds_barrier();  // the entry table is complete
+  const int n_all = L.ecount;
+  const bool ent_overflow = n_all > kSliceEntryCap;
+  const int n_ent = n_all < kSliceEntryCap ? n_all : kSliceEntryCap;
+
+  // ---------------------------------------------------------- D: slice max
+  for (int j = tid; j < n_ent; j += kThreads) ninf += L.ex[j] == kPosInf ? 1 : 0;
+  const float tmax = xmax;
+  {
+    const float hi = wave_max(tmax);
+    const float lo = wave_min(tmax > kNegInf ? tmax : kPosInf);
+    const uint32_t nf = __ballot(nonfinite_seen<DT>(nf_acc)) != 0ull ? kFNonfinite : 0u;
+    const int32_t ni = wave_sum(ninf);
+    if (l == 0) {
+      L.redf[wv] = hi;
+      L.redf2[wv] = lo;
+      L.redu[wv] = nf;
+      L.redi[wv] = ni;
+    }
+  }
+  __syncthreads();
+  float smax = L.redf[0], tlo = L.redf2[0];
+  uint32_t sflags = L.redu[0];
+  int32_t sninf = L.redi[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) {
+    smax = __builtin_fmaxf(smax, L.redf[i]);
+    tlo = __builtin_fminf(tlo, L.redf2[i]);
+    sflags |= L.redu[i];
+    sninf += L.redi[i];
+  }
+  const bool posinf = smax == kPosInf;
+  const bool has_finite = smax > kNegInf && !posinf;
+  if (smax > kNegInf) sflags |= kFLive;
+  if (posinf) sflags |= kFPosInf;
+  if (ent_overflow) sflags |= kFEntOverflow;
+
+  // the slice's mass sum exp((x - smax) / T_f), in 2^40 fixed point (exact in
+  // any order: the entry table's order depends on atomics)
+  uint64_t ze = 0ull;
+  if (zon && has_finite) {
+    const float nb = -smax * lgz;
+    const float nb_err = __builtin_fmaf(-smax, lgz, -nb);
+    const float enb = __builtin_amdgcn_exp2f(nb_err);
+    for (int j = tid; j < n_ent; j += kThreads) {
+      const float x = L.ex[j];
+      if (x > kNegInf) ze += (uint64_t)(__builtin_amdgcn_exp2f(__builtin_fmaf(x, lgz, nb)) * enb * 0x1p40f);
+    }
+    const float bh = smax * lgz;
+    const float bl = __builtin_fmaf(smax, lgz, -bh);
+    const float zr = zref ? zt * __builtin_amdgcn_exp2f((-nbz - bh) - bl) : 0.0f;
+    ze += zr < 0x1p20f ? (uint64_t)(zr * 0x1p40f) : 0ull;
+  }
+  ze = wave_sum(ze);
+  if (l == 0) L.redz[wv] = ze;
+
+  // ---------------------------------------------------------- E: threshold
+  // candidates are the tokens x >= tc (x-space); tempered rows compare
+  // fl(x / T), so a margin of 2^-20 keeps every token whose filter-space
+  // value could tie with the k-th
+  const float mp = prm.min_p > 1.0f ? 1.0f : prm.min_p;
+  const bool m_on = c.kind == LSAMP_KIND_FILTERED && mp > 0.0f && !bad_row;
+  auto margin = [&](float t) {
+    if (!(t < kPosInf)) return t;  // +inf: exactly the +inf tokens
+    const float tc = c.tempered ? t - (__builtin_fabsf(t) * 0x1p-20f + 1e-30f) : t;
+    return __builtin_fmaxf(tc, -__FLT_MAX__);
+  };
+  // min-p: a kept token has y >= y_max + ln(min_p) >= y_smax + ln(min_p); in
+  // x-space, with a hundredth of a nat to spare for the rounding of x / T
+  const float tau_m = m_on ? smax + (float)c.tf * (__builtin_logf(mp) - 0.01f) : kNegInf;
+  // the k-th largest thread maximum, from a histogram of the maxima below
+  // the slice maximum (half a bin of slack covers the bin index's rounding)
+  auto tau_hist = [&]() -> float {
+    for (int i = tid; i < kTkTauBins; i += kThreads) L.hist[i] = 0u;
+    __syncthreads();
+    const float D = __builtin_fminf(smax - tlo, (float)(32.0 * c.tf));
+    const float sc = D > 0.0f ? (float)(kTkTauBins - 1) / D : 0.0f;
+    if (tmax > kNegInf) {
+      const float fb = (smax - tmax) * sc;
+      const int b = fb < (float)(kTkTauBins - 1) ? (int)fb : kTkTauBins - 1;
+      atomicAdd(&L.hist[b], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      constexpr int kPer = kTkTauBins / 64;
+      uint32_t cb[kPer];
+      uint32_t cs = 0u;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        cb[i] = L.hist[kPer * tid + i];
+        cs += cb[i];
+      }
+      const uint32_t ic = wave_incl_scan(cs);
+      const uint64_t hit = __ballot(ic >= (uint32_t)K);
+      int bs = kTkTauBins;
+      if (hit) {
+        uint32_t acc = ic - cs;
+        int pos = kPer - 1;
+        bool found = false;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          acc += cb[i];
+          const bool h = !found && acc >= (uint32_t)K;
+          pos = h ? i : pos;
+          found = found || h;
+        }
+        const int f = __builtin_ctzll(hit);
+        bs = kPer * f + read_lane(pos, f);
+      }
+      if (tid == 0) L.misc[6] = bs;
+    }
+    __syncthreads();
+    const int bs = L.misc[6];
+    return bs >= kTkTauBins
+               ? kNegInf
+               : ((bs == kTkTauBins - 1 || sc == 0.0f) ? tlo : smax - ((float)bs + 1.5f) / sc);
+  };
+
+  // ---------------------------------------------------------- F: candidates
+  // the tokens x >= t (and, after a radix select, key >= kmin) as keys in
+  // L.cand; L.ncand counts them all, kept or not
+  auto extract = [&](float t, bool by_key, uint64_t kmin) {
+    // one quad at a time: a bitmask of its hits, one slot range per wave
+    // (a scan and one LDS atomic), keys only for the few hits
+    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+      const int32_t i0 = base32 + (tid + g * kThreads) * N;
+      uint32_t hits = 0u;
+#pragma unroll
+      for (int e = 0; e < N; ++e) hits |= (vec_elem<DT>(v, e) >= t ? 1u : 0u) << e;
+      if (by_key) {
+        uint32_t h2 = 0u;
+        for (uint32_t h = hits; h; h &= h - 1u) {
+          const int e = __builtin_ctz(h);
+          if (elem_key(c, vec_elem_dyn<DT>(v, e), i0 + e) >= kmin) h2 |= 1u << e;
+        }
+        hits = h2;
+      }
+      const int cnt = __builtin_popcount(hits);
+      if (__ballot(cnt > 0) == 0ull) return false;
+      const int incl = wave_incl_scan(cnt);
+      int wbase = 0;
+      if (l == 63) wbase = atomicAdd(&L.ncand, incl);
+      int slot = read_lane(wbase, 63) + incl - cnt;
+      for (uint32_t h = hits; h; h &= h - 1u, ++slot) {
+        const int e = __builtin_ctz(h);
+        if (slot < kCandCap) L.cand[slot] = elem_key(c, vec_elem_dyn<DT>(v, e), i0 + e);
+      }
+      return false;
+    });
+    for (int k0 = 0; k0 < n_ent; k0 += kThreads) {
+      const int j = k0 + tid;
+      const float x = j < n_ent ? L.ex[j] : kNegInf;
+      bool hit = x >= t && x > kNegInf;
+      uint64_t key = 0ull;
+      if (hit) key = elem_key(c, x, L.etok[j]);
+      if (by_key) hit = hit && key >= kmin;
+      const int slot = wave_append(hit, &L.ncand);
+      if (hit && slot < kCandCap) L.cand[slot] = key;
+    }
+  };
+
+  // First threshold: +inf tokens, the maximum (k = 1), the min-p bound, or
+  // the k-th largest thread maximum.  Too many candidates: the min-p bound
+  // with the thread-maximum bound, then the exact k-th key.
+  float t0;
+  if (posinf) {
+    t0 = kPosInf;
+  } else if (K == 1) {
+    t0 = smax;
+  } else if (m_on) {
+    t0 = tau_m;
+  } else {
+    t0 = tau_hist();
+  }
+  float tc = margin(t0);
+  bool by_key = false, hist_tried = !(m_on && !posinf && K > 1);
+  uint64_t kmin = 0ull;
+  int n = 0;
+#pragma unroll 1
+  for (int attempt = 0; attempt < 3; ++attempt) {
+    if (smax > kNegInf) extract(tc, by_key, kmin);
+    __syncthreads();
+    n = L.ncand;
+    if (n <= kCandCap) break;
+    if (!hist_tried) {
+      hist_tried = true;
+      tc = margin(__builtin_fmaxf(tau_hist(), tau_m));
+    } else {
+      kmin = kth_key_mem<DT>(c, rowp, mrow, P.mask_words, P.mask_bits, P.mask_tail, base32,
+                             end32, n_ent, tc, K, L);
+      by_key = true;
+    }
+    if (tid == 0) L.ncand = 0;
+    __syncthreads();
+  }
+  if (n > kCandCap) n = kCandCap;  // (cannot happen: the select leaves K)
+
+  // ---------------------------------------------------------- G: sort
+  // rank of a key = the keys above it (keys are distinct: ids are); the
+  // comparisons of a key are split over `parts` threads
+  const int npub = n < K ? n : K;
+  uint64_t* mine = L.best + slice * kTopkMaxK;
+  if (n > 0) {
+    const int parts = n <= kThreads / 2 ? kThreads / n : 1;
+    if (parts > 1) {
+      const int i = tid % n, part = tid / n;
+      if (part < parts) {
+        const uint64_t key = L.cand[i];
+        const int j0 = (n * part) / parts, j1 = (n * (part + 1)) / parts;
+        int r = 0;
+        for (int j = j0; j < j1; ++j) r += L.cand[j] > key ? 1 : 0;
+        if (r) atomicAdd(&L.racc[i], r);
+      }
+      __syncthreads();
+      for (int i2 = tid; i2 < n; i2 += kThreads) {
+        const int r = L.racc[i2];
+        if (r < npub) mine[r] = L.cand[i2];
+      }
+    } else {
+      for (int i = tid; i < n; i += kThreads) {
+        const uint64_t key = L.cand[i];
+        int r = 0;
+        for (int j = 0; j < n; ++j) r += L.cand[j] > key ? 1 : 0;
+        if (r < npub) mine[r] = key;
+      }
+    }
+  }
+
+  // ---------------------------------------------------------- parity outputs
+  if (P.processed) {
+    float* out = P.processed + (size_t)row * (size_t)V;
+    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+      const int32_t i0 = base32 + (tid + g * kThreads) * N;
+      if (i0 >= end32) return false;
+      const int32_t li0 = i0 - base32;
+      const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        if (i0 + e >= end32 || ((pen >> e) & 1u)) continue;
+        out[i0 + e] = to_filter(c, vec_elem<DT>(v, e));
+      }
+      return false;
+    });
+    for (int j = tid; j < n_ent; j += kThreads) out[L.etok[j]] = to_filter(c, L.ex[j]);
+  }
+  if (P.keep) {
+    // the slice's keep bytes: a sampled row whose maximum is +inf keeps
+    // exactly its +inf tokens (each slice marks its own); otherwise the
+    // finalizer marks the kept tokens after every slice has cleared its range
+    uint8_t* kr = P.keep + (size_t)row * (size_t)V;
+    const bool inf_keep = posinf && c.kind == LSAMP_KIND_FILTERED && !bad_row;
+    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+      const int32_t i0 = base32 + (tid + g * kThreads) * N;
+#pragma unroll
+      for (int e = 0; e < N; ++e)
+        if (i0 + e < end32) kr[i0 + e] = (inf_keep && vec_elem<DT>(v, e) == kPosInf) ? 1 : 0;
+      return false;
+    });
+    __syncthreads();
+    if (inf_keep)
+      for (int j = tid; j < n_ent; j += kThreads)
+        if (L.ex[j] == kPosInf) kr[L.etok[j]] = 1;
+    drain_memory();  // these bytes land before the payload says the slice is done
+  }
+
+  // ---------------------------------------------------------- H: publish
+  if (tid == 0) {
+    L.tag = epoch + 1u;
+    L.last = ticket + 1u == (uint32_t)G ? 1 : 0;
+  }
+  __syncthreads();
+  const uint32_t tag = L.tag;
+  const bool last = L.last != 0;
+  uint64_t zs = 0ull;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) zs += L.redz[i];
+  const double zsum = (double)zs * 0x1p-40;
+  auto word = [&](int w) -> uint32_t {
+    if (w >= kTopkHead) {
+      const int p = (w - kTopkHead) >> 1;
+      if (p >= npub) return 0u;
+      const uint64_t key = mine[p];
+      return (w - kTopkHead) & 1 ? (uint32_t)key : (uint32_t)(key >> 32);
+    }
+    const uint64_t zb = __builtin_bit_cast(uint64_t, zsum);
+    switch (w) {
+      case kHMax: return __float_as_uint(smax);
+      case kHZHi: return (uint32_t)(zb >> 32);
+      case kHZLo: return (uint32_t)zb;
+      case kHNpub: return (uint32_t)npub;
+      case kHFlags: return sflags;
+      case kHNinf: return (uint32_t)sninf;
+      default: return 0u;
+    }
+  };
+  if (!last) {
+    uint64_t* pub = T.pub + ((size_t)row * kMaxSlices + slice) * kTopkWords;
+    if (tid < kTopkWords) st_coherent(&pub[tid], ((uint64_t)tag << 32) | word(tid));
+    return;
+  }
+
+  // ---------------------------------------------------------- I: finalize
+  // this slice's header; the others' words, polled until tagged with this
+  // step (their slices started before this one, so each finishes)
+  if (tid < kTopkHead) {
+    const uint32_t w = word(tid);
+    switch (tid) {
+      case kHMax: L.hmax[slice] = __uint_as_float(w); break;
+      case kHNpub: L.hnpub[slice] = (int32_t)w; break;
+      case kHFlags: L.hflags[slice] = w; break;
+      case kHNinf: L.hninf[slice] = (int32_t)w; break;
+      default: break;
+    }
+  }
+  if (tid == 0) L.hz[slice] = zsum;
+  if (tid < kTopkWords) {
+    // every slice's word in one round trip, then only the missing ones again
+    const uint64_t* pub0 = T.pub + (size_t)row * kMaxSlices * kTopkWords + tid;
+    uint64_t w8[kMaxSlices];
+#pragma unroll
+    for (int s = 0; s < kMaxSlices; ++s)
+      w8[s] = (s < G && s != slice) ? ld_coherent(pub0 + s * kTopkWords) : ((uint64_t)tag << 32);
+    for (int it = 0;; ++it) {
+      bool all = true;
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) all = all && (uint32_t)(w8[s] >> 32) == tag;
+      if (all) break;
+      if (it >= kSpin) {
+        L.lost = 1;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s)
+        if ((uint32_t)(w8[s] >> 32) != tag) w8[s] = ld_coherent(pub0 + s * kTopkWords);
+    }
+    for (int s = 0; s < G; ++s) {
+      if (s == slice) continue;
+      const uint32_t d = (uint32_t)w8[s];
+      if (tid >= kTopkHead) {
+        const int p = (tid - kTopkHead) >> 1;
+        uint32_t* half = reinterpret_cast<uint32_t*>(&L.best[s * kTopkMaxK + p]);
+        half[(tid - kTopkHead) & 1 ? 0 : 1] = d;
+      } else if (tid == kHMax) {
+        L.hmax[s] = __uint_as_float(d);
+      } else if (tid == kHZHi) {
+        reinterpret_cast<uint32_t*>(&L.hz[s])[1] = d;
+      } else if (tid == kHZLo) {
+        reinterpret_cast<uint32_t*>(&L.hz[s])[0] = d;
+      } else if (tid == kHNpub) {
+        L.hnpub[s] = (int32_t)d;
+      } else if (tid == kHFlags) {
+        L.hflags[s] = d;
+      } else if (tid == kHNinf) {
+        L.hninf[s] = (int32_t)d;
+      }
+    }
+  }
+  __syncthreads();
+  // merge: rank of key (s, p) = p + the keys of the other slices above it
+  // (binary searches in their sorted lists)
+  {
+    const int s = tid / kTopkMaxK, p = tid % kTopkMaxK;
+    if (s < G && p < L.hnpub[s]) {
+      const uint64_t key = L.best[s * kTopkMaxK + p];
+      int r = p;
+      for (int s2 = 0; s2 < G; ++s2) {
+        if (s2 == s) continue;
+        const uint64_t* lst = L.best + s2 * kTopkMaxK;
+        int lo = 0, hi = L.hnpub[s2];
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (lst[mid] > key) lo = mid + 1; else hi = mid;
+        }
+        r += lo;
+      }
+      if (r < kTopkMaxK) L.merged[r] = key;
+    }
+  }
+  __syncthreads();
+  if (tid >= 64) {
+    if (tid == 64) {
+      T.ticket[row] = 0u;
+      T.epoch[row] = tag;
+    }
+    return;
+  }
+
+  // ---------------------------------------------------------- J: the row
+  int total = 0;
+  float row_max = kNegInf;
+  uint32_t rfl = 0u;
+  int32_t ninf_row = 0;
+  double z = 0.0;
+  {
+    const bool sl = l < G;
+    const uint32_t f = sl ? L.hflags[l] : 0u;
+    const bool live = (f & kFLive) != 0u;
+    const float hx = sl ? L.hmax[l] : kNegInf;
+    rfl = sl ? f : 0u;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) rfl |= (uint32_t)__shfl_xor((int)rfl, d, 64);
+    row_max = wave_max(live ? hx : kNegInf);
+    total = wave_sum(sl ? L.hnpub[l] : 0);
+    ninf_row = wave_sum(sl ? L.hninf[l] : 0);
+    if (c.kind != LSAMP_KIND_ARGMAX && row_max > kNegInf && row_max < kPosInf)
+      z = wave_sum(live && hx > kNegInf ? L.hz[l] * (double)__builtin_expf((hx - row_max) / (float)c.tf)
+                                        : 0.0);
+  }
+  const bool any = (rfl & kFLive) != 0u;
+  const bool lost = L.lost != 0;
+  uint32_t flags = (rfl & kFNonfinite) ? LSAMP_ROW_NONFINITE : 0u;
+  float u = 0.0f;
+  if (P.uniforms)
+    u = P.uniforms[row];
+  else if (P.philox_keys)
+    u = philox_uniform(P.philox_keys[row], 0u);
+  const int32_t probe = P.probe_tokens ? P.probe_tokens[row] : -1;
+  uint8_t* kr = P.keep ? P.keep + (size_t)row * (size_t)V : nullptr;
+
+  int32_t token = -1;
+  uint64_t W = 0ull, probe_w = 0ull;
+  int32_t kept_c = 0;
+  float cmin = kPosInf;
+  double cent = 0.0;
+  float y_max = any ? to_filter(c, row_max) : 0.0f;
+  const bool inf_mode = any && row_max == kPosInf && c.kind == LSAMP_KIND_FILTERED;
+  if (lost) {
+    flags |= LSAMP_ROW_TIMEOUT;
+  } else if (bad_row || (rfl & kFEntOverflow)) {
+    flags |= LSAMP_ROW_OVERFLOW;
+  } else if (!any) {
+    flags |= LSAMP_ROW_EMPTY;
+  } else if (inf_mode) {
+    // the +inf tokens, equally weighted: the token at index (U n) >> 32 of
+    // the row's +inf tokens in id order; each slice listed its first ones
+    y_max = kPosInf;
+    W = (uint64_t)ninf_row << 40;
+    const uint64_t j = ((uint64_t)uniform_u32(u) * (uint64_t)ninf_row) >> 32;
+    int64_t pre = 0;
+    int32_t tk = -1;
+    bool beyond = false;
+    for (int s = 0; s < G; ++s) {
+      const int64_t ns = L.hninf[s];
+      if ((int64_t)j < pre + ns) {
+        const int jj = (int)((int64_t)j - pre);
+        if (jj < L.hnpub[s]) tk = key_id(L.best[s * kTopkMaxK + jj]);
+        else beyond = true;
+        break;
+      }
+      pre += ns;
+    }
+    if (beyond) {
+      // more +inf tokens in one slice than it lists: fail closed
+      flags |= LSAMP_ROW_OVERFLOW;
+      W = 0ull;
+    } else {
+      token = tk;
+      kept_c = ninf_row;
+      cmin = kPosInf;
+      cent = 0.0;
+    }
+  } else {
+    // the keep rule over the row's best keys (CBv2: rank < k, exclusive mass
+    // <= top-p of the total, p >= min-p of the top; argmax rows: the first)
+    const int nc = total < K ? total : K;
+    const bool in = l < nc;
+    const uint64_t key = in ? L.merged[l] : 0ull;
+    const float y = key_y(key);
+    const int32_t id = key_id(key);
+    const double P_lim = top_p_limit(P, c, prm, z);
+    const bool p_on = P_lim >= 0.0;
+    const int32_t k_lim = c.kind == LSAMP_KIND_ARGMAX ? 1 : prm.top_k;
+    const double e = in ? (double)__builtin_expf(y - y_max) : 0.0;
+    const double e_excl = wave_incl_scan(e) - e;
+    bool keep_p = true, keep_m = true;
+    if (p_on) keep_p = e_excl <= P_lim;
+    if (m_on) keep_m = __builtin_expf(y - y_max) >= mp;
+    if (l >= k_lim) keep_p = false;
+    const bool keep = in && keep_p && keep_m;
+    kept_c = (int32_t)__popcll(__ballot(keep));  // each rule keeps a prefix
+    const uint64_t w = keep ? weight(y, y_max, c.scale) : 0ull;
+    // the kept in id order, then a running sum: the token is the one whose
+    // run crosses the target
+    uint64_t* dw = L.cand;                              // [64] weights by id rank
+    int32_t* sid = reinterpret_cast<int32_t*>(L.racc);  // [64] kept ids, then by id rank
+    if (keep) sid[l] = id;
+    if (l >= kept_c) sid[l] = 0x7fffffff;
+    __builtin_amdgcn_wave_barrier();
+    int pos = 0;
+    for (int j0 = 0; j0 < kept_c; j0 += 16) {
+      int32_t ij[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) ij[q] = sid[j0 + q];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) pos += ij[q] < id ? 1 : 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    int32_t* sid2 = sid + 64;
+    if (keep) {
+      dw[pos] = w;
+      sid2[pos] = id;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const uint64_t wo = l < kept_c ? dw[l] : 0ull;
+    const int32_t io = l < kept_c ? sid2[l] : -1;
+    const uint64_t cum = wave_incl_scan(wo);
+    W = read_lane(cum, 63);
+    const uint64_t target = W ? scaled_target(uniform_u32(u), W) : 0ull;
+    const uint64_t hm = __ballot(wo != 0ull && cum > target && cum - wo <= target);
+    token = hm ? read_lane(io, __builtin_ctzll(hm)) : -1;
+    const uint64_t hp = __ballot(keep && probe >= 0 && id == probe);
+    probe_w = hp ? read_lane(w, __builtin_ctzll(hp)) : 0ull;
+    if (P.stats) {
+      cent = wave_sum(keep ? (double)w * (1.0 / 1099511627776.0) * (double)weight_arg(y, y_max, c.scale)
+                           : 0.0);
+      cmin = wave_min(keep ? y : kPosInf);
+    }
+    if (kr && in && keep) kr[id] = 1;
+    if (token < 0 || W == 0ull) flags |= LSAMP_ROW_EMPTY;
+  }
+  if (l == 0) {
+    if (lost) atomicOr(T.status, kStatusSpinTimeout);
+    P.tokens[row] = token;
+    if (P.row_flags) P.row_flags[row] = flags;
+    if (P.stats) {
+      lsamp_row_stats st;
+      st.max_value = y_max;
+      st.log_normalizer = z > 0.0 ? __builtin_logf((float)z) : 0.0f;
+      st.kept = kept_c;
+      st.token = token;
+      st.kept_weight = W;
+      st.probe_weight = probe_w;
+      st.cut_value = cmin;
+      const double zk = (double)W * (1.0 / 1099511627776.0);
+      st.kept_mass = (float)zk;
+      st.kept_entropy = zk > 0.0 ? __builtin_logf((float)zk) - (float)(cent / zk) : 0.0f;
+      st.probe_prob = W ? (float)((double)probe_w / (double)W) : 0.0f;
+      P.stats[row] = st;
+    }
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kThreads) void k_topk(SamplePlan Pk, TopkWs Tk) {
+  __shared__ TopkLds L;
+  const SamplePlan P = in_sgprs(Pk);
+  const TopkWs T = in_sgprs(Tk);
+  // work-group b runs on XCD b % 8; that XCD's rows are b % 8, + 8, + 16, ...
+  const int b = (int)blockIdx.x;
+  const int loc = b >> 3;
+  const int row = (b & 7) + 8 * (loc / P.slices);
+  const int slice = loc % P.slices;
+  if (row < P.rows) topk_task<DT>(P, T, row, slice, L);
+}
+
+template <int DT>
+int launch_topk_dt(const SamplePlan& P, const TopkWs& T, hipStream_t st, void* const* events) {
+  auto mark = [&](int i) {
+    if (events) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), st);
+  };
+  const int rows8 = (P.rows + 7) / 8 * 8;
+  mark(0);
+  hipLaunchKernelGGL(k_topk<DT>, dim3((unsigned)(rows8 * P.slices)), dim3(kThreads), 0, st, P, T);
+  mark(1);
+  mark(2);
+  return (int)hipGetLastError();
+}
+
+template <int DT>
+int topk_blocks_dt() {
+  int n = 0;
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_topk<DT>, kThreads, 0) == hipSuccess ? n
+                                                                                                   : 0;
+}
+
+}  // namespace
+
+int launch_topk(const SamplePlan& P, const TopkWs& T, void* stream, void* const* events) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  switch (P.dtype) {
+    case LSAMP_DTYPE_F32: return launch_topk_dt<LSAMP_DTYPE_F32>(P, T, st, events);
+    case LSAMP_DTYPE_BF16: return launch_topk_dt<LSAMP_DTYPE_BF16>(P, T, st, events);
+    default: return launch_topk_dt<LSAMP_DTYPE_F16>(P, T, st, events);
+  }
+}
+
+int topk_blocks_per_cu(int dtype) {
+  switch (dtype) {
+    case LSAMP_DTYPE_F32: return topk_blocks_dt<LSAMP_DTYPE_F32>();
+    case LSAMP_DTYPE_BF16: return topk_blocks_dt<LSAMP_DTYPE_BF16>();
+    default: return topk_blocks_dt<LSAMP_DTYPE_F16>();
+  }
+}
+
+}  // namespace lsamp

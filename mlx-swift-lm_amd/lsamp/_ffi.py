@@ -104,6 +104,7 @@ class SampleArgs(Structure):
         ("penalty_row_len", c_void_p),
         ("suppress_ids", c_void_p),
         ("n_suppress", c_int32),
+        ("params_host", c_void_p),
     ]
 
 

@@ -284,10 +284,13 @@ class PreparedSample:
         V = int(vocab) if vocab is not None else logits.shape[1]
         self.ctx = ctx
         self.keep_alive = [logits]
+        self.params_host = None
         if isinstance(params, torch.Tensor):
             self.params = params
         else:
-            self.params = to_device_bytes(params_array(params), dev)
+            # the host copy lets the library choose the kernel arrangement
+            self.params_host = np.ascontiguousarray(params_array(params))
+            self.params = to_device_bytes(self.params_host, dev)
         self.keep_alive.append(self.params)
         a = _ffi.SampleArgs()
         a.semantics = semantics
@@ -298,6 +301,8 @@ class PreparedSample:
         a.row_stride = logits.stride(0) if rows > 1 else logits.shape[1]
         a.logits = logits.data_ptr()
         a.params = self.params.data_ptr()
+        if self.params_host is not None and len(self.params_host) == rows:
+            a.params_host = self.params_host.ctypes.data
 
         def dev_tensor(x, np_dtype, torch_dtype):
             if x is None:
