@@ -19,6 +19,36 @@ constexpr int kBufferWord3 = 0x00020000;
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kPosInf = __builtin_huge_valf();
 
+// ---------------------------------------------------------------- global memory
+// Every pointer the kernels dereference addresses global memory, but the
+// pointers reach them as generic ones (fields of a plan passed by value), and
+// generic accesses compile to flat instructions.  A flat access may complete
+// out of order with the vector loads, so after one the compiler waits for
+// every load in flight (vmcnt(0)) before the next use of any of them, which
+// serialises a slice's loads with the work on it.  Accesses through the
+// global address space count only against the in-order vector counter, so a
+// use of one load waits for that load alone.
+template <typename T>
+using gptr = __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ gptr<const T> gmem(const T* p) {
+  return (gptr<const T>)p;
+}
+template <typename T>
+__device__ __forceinline__ gptr<T> gmem(T* p) {
+  return (gptr<T>)p;
+}
+// A 16-byte struct from global memory in one load (structs are read through
+// a plain vector type: C++ cannot copy a class object out of another address
+// space).
+template <typename T>
+__device__ __forceinline__ T gload16(const T* p) {
+  static_assert(sizeof(T) == 16, "a 16-byte struct");
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(T, *gmem(reinterpret_cast<const u32x4*>(p)));
+}
+
 // ---------------------------------------------------------------- dtypes
 template <int DT>
 struct Vec {
@@ -119,20 +149,20 @@ __device__ __forceinline__ void exclude_elems(uint4& r, uint32_t excl) {
 template <int DT>
 __device__ __forceinline__ float load_scalar(const void* row, int64_t i) {
   if constexpr (DT == LSAMP_DTYPE_F32) {
-    return reinterpret_cast<const float*>(row)[i];
+    return gmem(reinterpret_cast<const float*>(row))[i];
   } else if constexpr (DT == LSAMP_DTYPE_BF16) {
-    return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(row)[i] << 16);
+    return __uint_as_float((uint32_t)gmem(reinterpret_cast<const uint16_t*>(row))[i] << 16);
   } else {
-    return half_bits_to_f32(reinterpret_cast<const uint16_t*>(row)[i]);
+    return half_bits_to_f32(gmem(reinterpret_cast<const uint16_t*>(row))[i]);
   }
 }
 
 template <int DT>
 __device__ __forceinline__ uint32_t load_raw_bits(const void* row, int64_t i) {
   if constexpr (DT == LSAMP_DTYPE_F32)
-    return reinterpret_cast<const uint32_t*>(row)[i];
+    return gmem(reinterpret_cast<const uint32_t*>(row))[i];
   else
-    return reinterpret_cast<const uint16_t*>(row)[i];
+    return gmem(reinterpret_cast<const uint16_t*>(row))[i];
 }
 
 // Load the 16-byte vector starting at token i0; lanes past `end` (or the whole
@@ -142,8 +172,8 @@ template <int DT>
 __device__ __forceinline__ uint4 load_vec(const void* row, int64_t i0, int64_t end, bool aligned) {
   constexpr int N = Vec<DT>::N;
   if (aligned && i0 + N <= end) {
-    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(row) +
-                                           i0 * Vec<DT>::ESIZE);
+    return gload16(reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(row) +
+                                                  i0 * Vec<DT>::ESIZE));
   }
   uint32_t b[N];
 #pragma unroll
@@ -423,11 +453,11 @@ __device__ __forceinline__ T block_excl_scan(T v, T* scratch, T* total) {
 // point, never from a stale L2 line).
 template <typename T>
 __device__ __forceinline__ T ld_coherent(const T* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load(gmem(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 template <typename T>
 __device__ __forceinline__ void st_coherent(T* p, T v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(gmem(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_coherent_f32(float* p, float v) {
   st_coherent(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
@@ -482,7 +512,7 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev =
-        __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(gmem(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag = prev == expected - 1u;
   }
   __syncthreads();

@@ -138,7 +138,7 @@ __device__ __forceinline__ uint32_t mask_allow_bits(const uint32_t* mrow, int32_
   if (!mrow) return full;
   const int32_t wi = i0 >> 5;
   const bool word_in = wi < mask_words;
-  const uint32_t word = word_in ? mrow[wi] : 0u;
+  const uint32_t word = word_in ? gmem(mrow)[wi] : 0u;
   int32_t nin = word_in ? mask_bits - i0 : 0;  // leading positions the mask covers
   nin = nin < 0 ? 0 : (nin > N ? N : nin);
   const uint32_t in_mask = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
@@ -306,7 +306,7 @@ __device__ __forceinline__ void mark_slice_entries(const SamplePlan& P, const Ro
   }
   // the rest of a long history
   for (int32_t e = ep.e0 + tid + kEntPrefetch * kThreads; e < ep.e1; e += kThreads) {
-    const lsamp_penalty_entry ent = P.entries[e];
+    const lsamp_penalty_entry ent = gload16(P.entries + e);
     if (ent.token >= base && ent.token < end) {
       const int idx = mark(ent.token);
       if (idx < kSliceEntryCap) {
@@ -411,6 +411,30 @@ __device__ __forceinline__ void for_quads(Slab<DT>& S, int nq, F&& f) {
       if (f(b * kQuadsPerBank + s, v)) quad_set(S.bank[b], s, v);
     }
   }
+}
+
+// f(g, v) for the quads g whose bit is set in `sel` (uniform, Q <= 32): a
+// rolled loop over the set bits of each bank, so a pass that touches a few
+// quads costs a few iterations.  When f returns true the quad is written back.
+template <int DT, typename F>
+__device__ __forceinline__ void for_quads_sel(Slab<DT>& S, uint32_t sel, F&& f) {
+  static_assert(Slab<DT>::Q <= 32, "one mask word");
+#pragma unroll
+  for (int b = 0; b < Slab<DT>::NB; ++b) {
+#pragma unroll 1
+    for (uint32_t m = (sel >> (b * kQuadsPerBank)) & 0xffu; m != 0u; m &= m - 1u) {
+      const int s = __builtin_ctz(m);
+      uint4 v = quad_get(S.bank[b], s);
+      if (f(b * kQuadsPerBank + s, v)) quad_set(S.bank[b], s, v);
+    }
+  }
+}
+
+// The upper 16 bits of a float rounded toward +inf (an exact bf16 value keeps
+// its bits): an upper bound of the value that packs two to a register.
+__device__ __forceinline__ uint32_t hi16_up(float x) {
+  const uint32_t b = __float_as_uint(x);
+  return ((int32_t)b >= 0 ? b + 0xffffu : b) >> 16;
 }
 
 // for_quads with every quad at a static register position: fully unrolled

@@ -34,6 +34,8 @@
 // key by a radix select over the 64-bit keys.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "lsamp_device.h"
 #include "lsamp_internal.h"
 #include "lsamp_row.h"
@@ -47,6 +49,13 @@ using namespace rowops;
 constexpr int kCandCap = 1024;   // candidate keys a slice keeps in LDS
 constexpr int kTkTauBins = 1024;  // thread-maximum histogram
 constexpr int kSpin = 1 << 20;   // polls before the finalizer gives a slice up
+#ifndef LSAMP_TOPK_FIRST_QUADS
+#define LSAMP_TOPK_FIRST_QUADS 2
+#endif
+constexpr int kTopkFirstQuads = LSAMP_TOPK_FIRST_QUADS;  // slab quads requested ahead of the entries
+#ifndef LSAMP_TOPK_REST_AFTER_MARK
+#define LSAMP_TOPK_REST_AFTER_MARK 0  // the rest of the slab: 1 after the entries are marked
+#endif
 static_assert(kTopkWords <= kThreads, "one payload word per thread");
 static_assert(kMaxSlices * kTopkMaxK <= kThreads, "one merged key per thread");
 
@@ -87,6 +96,13 @@ struct TopkLds {
   int32_t last;
   int32_t lost;  // the finalizer gave up waiting for a slice
 };
+
+// The larger of each 16-bit half of a and b, unsigned (one packed op).
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a),
+                                                                __builtin_bit_cast(u16x2, b)));
+}
 
 // Ordered 64-bit key of an element of the slice (filter space, id).
 __device__ __forceinline__ uint64_t elem_key(const RowCtx& c, float x, int32_t id) {
@@ -184,33 +200,56 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   const int nq = (P.slice_len + kThreads * N - 1) / (kThreads * N);
 
   // ---------------------------------------------------------- A: loads
-  // the ticket and the epoch first (their round trip overlaps everything),
-  // then the parameters, the CSR bounds, the first penalty entries and the
-  // slice itself
-  uint32_t ticket = 0u, epoch = 0u;
-  if (tid == 0) {
-    epoch = __hip_atomic_load(&T.epoch[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ticket = __hip_atomic_fetch_add(&T.ticket[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  const lsamp_row_params prm = load_params(P, row);
-  EntryPrefetch ep;
-  entry_bounds(P, row, ep);
-  const RowCtx c = make_ctx(P.semantics, prm);
-  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
-  prefetch_entries(P, tid, ep);
+  // In dependency order, each request as early as its inputs allow: the
+  // first quads of the slice (they need only the kernel arguments), the
+  // row's scalar data (CSR bounds, parameters, draw inputs: one round trip),
+  // the first penalty entries (they need the bounds), the rest of the slice,
+  // then the epoch and the ticket.  The vector counter completes in issue
+  // order, so whatever is requested later holds up no wait for the data
+  // ahead of it.
+  //
+  // The slab is requested in two parts around the entries: the first pass
+  // waits for the entries, and a request behind the whole slab would wait
+  // for all of it.  (Every quad is loaded without a branch: quads past the
+  // slice read zero, and straight-line loads let each later wait name its
+  // own quad.)
   Slab<DT> S;
-  {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<char*>(rowp) + (size_t)base32 * ES, 0, aligned ? (end32 - base32) * ES : 0,
-        kBufferWord3);
-    const int lane_off = tid * 16;
-    // (every quad of the slab, without a branch: quads past the slice read
-    // zero, and straight-line loads let each later wait name its own quad)
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(rowp) + (size_t)base32 * ES, 0, aligned ? (end32 - base32) * ES : 0,
+      kBufferWord3);
+  const int lane_off = tid * 16;
+  constexpr int kFirst = Q < kTopkFirstQuads ? Q : kTopkFirstQuads;
+  auto load_quads = [&](auto g0, auto g1) {
 #pragma unroll
-    for (int g = 0; g < Q; ++g) {
+    for (int g = decltype(g0)::value; g < decltype(g1)::value; ++g) {
       const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, g * kThreads * 16, 0);
       quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, make_uint4(w[0], w[1], w[2], w[3]));
     }
+  };
+  load_quads(std::integral_constant<int, 0>{}, std::integral_constant<int, kFirst>{});
+  // (the parameters first: the bounds are used as soon as they arrive, and
+  // one wait then covers both)
+  const lsamp_row_params prm = load_params(P, row);
+  EntryPrefetch ep;
+  entry_bounds(P, row, ep);
+  prefetch_entries(P, tid, ep);
+#if LSAMP_TOPK_REST_AFTER_MARK == 0
+  load_quads(std::integral_constant<int, kFirst>{}, std::integral_constant<int, Q>{});
+#endif
+  const RowCtx c = make_ctx(P.semantics, prm);
+  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
+  // (defaults the compiler cannot see as constants: with constant ones it
+  // moves the later `+ 1`s into this branch, where they would wait for the
+  // atomic at once)
+  uint32_t ticket, epoch;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(ticket));
+  asm volatile("v_mov_b32 %0, 0" : "=v"(epoch));
+  if (tid == 0) {
+    epoch = __hip_atomic_load(gmem(T.epoch) + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // (an increment, not an add: the compiler rewrites a uniform add as a
+    // wave-aggregated one whose result it waits for on the spot)
+    ticket = __builtin_amdgcn_atomic_inc32(gmem(T.ticket) + row, 0xffffffffu, __ATOMIC_RELAXED,
+                                           "agent");
   }
   // the row's sampler: argmax rows, and CBv2 rows with an active top-k of at
   // most kTopkMaxK; any other row (a caller whose host copy of the
@@ -231,6 +270,9 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   EntryMarks em;
   float emax = kNegInf;
   mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
+#if LSAMP_TOPK_REST_AFTER_MARK != 0
+  load_quads(std::integral_constant<int, kFirst>{}, std::integral_constant<int, Q>{});
+#endif
   if (!aligned || (end32 & (N - 1)) != 0) {
     // unaligned rows, or the row's last partial quad: element by element
     for_quads(S, nq, [&](int g, uint4& v) -> bool {
@@ -259,35 +301,79 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   constexpr int kQuadWords = kThreads * N / 32;
   const uint32_t pen_shift = (uint32_t)((tid * N) & 31);
   const int32_t lim = end32 - base32 - tid * N;
+  // the first quad index that is not whole for every thread of this slice
+  const int nq_tail = (end32 - base32) / (kThreads * N);
   uint32_t pw = penw[0];
   uint32_t nf_acc = 0u;
   float xmax = kNegInf;
   float zt = 0.0f, nbz = __FLT_MAX__;
   int32_t ninf = 0;  // +inf tokens (counted in the rare quads that hold one)
+  // each quad's maximum, rounded up to 16 bits and packed two to a register:
+  // the candidate pass visits only the quads whose maximum reaches its bound
+  uint32_t qmp[Q / 2];
+#pragma unroll
+  for (int i = 0; i < Q / 2; ++i) qmp[i] = 0xff80ff80u;  // -inf, -inf
+  // (16-bit logits) the largest raw magnitude seen (sign bits cleared), as
+  // an unsigned 16-bit pair: NaN and +-inf are the patterns at or above the
+  // infinity's, so a packed maximum a word flags every one of them, masked,
+  // penalized or not
+  uint32_t rawhi = 0u;
+  constexpr uint32_t kInfHalf = DT == LSAMP_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
   for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
     const int32_t i0 = base32 + (tid + g * kThreads) * N;
     const uint32_t pcur = pw;
     if (g + 1 < Q) pw = penw[(g + 1) * kQuadWords];
-    const uint32_t probe = nonfinite_probe<DT>(v);
-    nf_acc |= probe;
-    const int32_t rem = lim - g * (kThreads * N);
-    const uint32_t tail = ~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem));
-    uint32_t ex = ((pcur >> pen_shift) | tail) & FULL;
+    uint32_t ex = (pcur >> pen_shift) & FULL;
+    if (g >= nq_tail) {
+      // the quads that can reach past this slice's end: every earlier one is
+      // whole for every thread (the last slice of a row is shorter)
+      const int32_t rem = lim - g * (kThreads * N);
+      ex |= (~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem))) & FULL;
+    }
     if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
-    if (nonfinite_seen<DT>(probe)) {
+    if constexpr (N == 8) {
+      constexpr uint32_t M = 0x7fff7fffu;
+      const uint32_t hw = pk_max_u16(pk_max_u16(v.x & M, v.y & M), pk_max_u16(v.z & M, v.w & M));
+      rawhi = pk_max_u16(rawhi, hw);
+    } else {
+      const uint32_t probe = nonfinite_probe<DT>(v);
+      nf_acc |= probe;
+      if (nonfinite_seen<DT>(probe)) {
 #pragma unroll
-      for (int e = 0; e < N; ++e) {
-        const float x = vec_elem<DT>(v, e);
-        if (x != x) ex |= 1u << e;
+        for (int e = 0; e < N; ++e) {
+          const float x = vec_elem<DT>(v, e);
+          if (x != x) ex |= 1u << e;
+        }
       }
     }
     exclude_elems<DT>(v, ex);
-    const float qm = vec_max_nn<DT>(v);
-    xmax = __builtin_elementwise_maximum(xmax, qm);
-    if (qm == kPosInf) {
+    float qm = vec_max_nn<DT>(v);
+    if constexpr (N == 8) {
+      // a NaN (the maximum propagates it) or +inf in the quad: NaNs out,
+      // +inf tokens counted (rare)
+      if (!(qm < kPosInf)) {
+        uint32_t nan = 0u;
 #pragma unroll
-      for (int e = 0; e < N; ++e) ninf += vec_elem<DT>(v, e) == kPosInf ? 1 : 0;
+        for (int e = 0; e < N; ++e) {
+          const float x = vec_elem<DT>(v, e);
+          nan |= (x != x ? 1u : 0u) << e;
+          ninf += x == kPosInf ? 1 : 0;
+        }
+        exclude_elems<DT>(v, nan);
+        qm = vec_max_nn<DT>(v);
+        nf_acc = 0x80008000u;
+      }
+    } else {
+      if (qm == kPosInf) {
+#pragma unroll
+        for (int e = 0; e < N; ++e) ninf += vec_elem<DT>(v, e) == kPosInf ? 1 : 0;
+      }
     }
+    xmax = __builtin_elementwise_maximum(xmax, qm);
+    if (g & 1)
+      qmp[g / 2] = (qmp[g / 2] & 0xffffu) | (hi16_up(qm) << 16);
+    else
+      qmp[g / 2] = (qmp[g / 2] & 0xffff0000u) | hi16_up(qm);
     if (zon) {
       if (__builtin_fmaf(qm, lgz, nbz) > 64.0f) {
         const float nn = -__builtin_ceilf(__builtin_amdgcn_fmed3f(qm * lgz, -0x1p20f, 0x1p20f));
@@ -300,6 +386,9 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     }
     return true;
   });
+  if constexpr (N == 8) {
+    if ((rawhi & 0xffffu) >= kInfHalf || (rawhi >> 16) >= kInfHalf) nf_acc = 0x80008000u;
+  }
   const bool zref = nbz < __FLT_MAX__;
   finish_slice_entries<DT>(P, c, prm, mrow, se, ep, em, emax);
   xmax = __builtin_fmaxf(xmax, emax);
@@ -425,9 +514,17 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   // the tokens x >= t (and, after a radix select, key >= kmin) as keys in
   // L.cand; L.ncand counts them all, kept or not
   auto extract = [&](float t, bool by_key, uint64_t kmin) {
-    // one quad at a time: a bitmask of its hits, one slot range per wave
-    // (a scan and one LDS atomic), keys only for the few hits
-    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+    // the quads of the wave where some lane's quad maximum reaches t, then
+    // one such quad at a time: a bitmask of its hits, one slot range per
+    // wave (a scan and one LDS atomic), keys only for the few hits
+    uint32_t sel = 0u;
+#pragma unroll
+    for (int g = 0; g < Q; ++g) {
+      const uint32_t w = qmp[g / 2];
+      const float qm = __uint_as_float(g & 1 ? w & 0xffff0000u : w << 16);
+      if (__ballot(qm >= t) != 0ull) sel |= 1u << g;
+    }
+    for_quads_sel(S, sel, [&](int g, uint4& v) -> bool {
       const int32_t i0 = base32 + (tid + g * kThreads) * N;
       uint32_t hits = 0u;
 #pragma unroll
@@ -505,7 +602,22 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   // comparisons of a key are split over `parts` threads
   const int npub = n < K ? n : K;
   uint64_t* mine = L.best + slice * kTopkMaxK;
-  if (n > 0) {
+  if (n > 0 && n <= 64) {
+    // a wave's worth: lane i ranks key i against all of them (broadcast
+    // reads, eight at a time), no atomics
+    if (tid < 64) {
+      const uint64_t key = tid < n ? L.cand[tid] : 0ull;
+      int r = 0;
+      for (int j0 = 0; j0 < n; j0 += 8) {
+        uint64_t cj[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) cj[q] = L.cand[j0 + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) r += (j0 + q < n && cj[q] > key) ? 1 : 0;
+      }
+      if (tid < n && r < npub) mine[r] = key;
+    }
+  } else if (n > 0) {
     const int parts = n <= kThreads / 2 ? kThreads / n : 1;
     if (parts > 1) {
       const int i = tid % n, part = tid / n;
@@ -605,6 +717,11 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   }
 
   // ---------------------------------------------------------- I: finalize
+  // the row's draw inputs, requested first: they arrive while the other
+  // slices' payloads are polled for
+  const float u_in = P.uniforms ? gmem(P.uniforms)[row] : 0.0f;
+  const uint64_t key_in = (!P.uniforms && P.philox_keys) ? gmem(P.philox_keys)[row] : 0ull;
+  const int32_t probe = P.probe_tokens ? gmem(P.probe_tokens)[row] : -1;
   // this slice's header; the others' words, polled until tagged with this
   // step (their slices started before this one, so each finishes)
   if (tid < kTopkHead) {
@@ -665,7 +782,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   // merge: rank of key (s, p) = p + the keys of the other slices above it
   // (binary searches in their sorted lists)
   {
-    const int s = tid / kTopkMaxK, p = tid % kTopkMaxK;
+    static_assert(kTopkMaxK == 64, "one wave per slice list");
+    const int s = __builtin_amdgcn_readfirstlane(tid) >> 6, p = l;
     if (s < G && p < L.hnpub[s]) {
       const uint64_t key = L.best[s * kTopkMaxK + p];
       int r = p;
@@ -685,8 +803,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   __syncthreads();
   if (tid >= 64) {
     if (tid == 64) {
-      T.ticket[row] = 0u;
-      T.epoch[row] = tag;
+      gmem(T.ticket)[row] = 0u;
+      gmem(T.epoch)[row] = tag;
     }
     return;
   }
@@ -715,12 +833,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   const bool any = (rfl & kFLive) != 0u;
   const bool lost = L.lost != 0;
   uint32_t flags = (rfl & kFNonfinite) ? LSAMP_ROW_NONFINITE : 0u;
-  float u = 0.0f;
-  if (P.uniforms)
-    u = P.uniforms[row];
-  else if (P.philox_keys)
-    u = philox_uniform(P.philox_keys[row], 0u);
-  const int32_t probe = P.probe_tokens ? P.probe_tokens[row] : -1;
+  float u = u_in;
+  if (!P.uniforms && P.philox_keys) u = philox_uniform(key_in, 0u);
   uint8_t* kr = P.keep ? P.keep + (size_t)row * (size_t)V : nullptr;
 
   int32_t token = -1;
@@ -826,8 +940,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   }
   if (l == 0) {
     if (lost) atomicOr(T.status, kStatusSpinTimeout);
-    P.tokens[row] = token;
-    if (P.row_flags) P.row_flags[row] = flags;
+    gmem(P.tokens)[row] = token;
+    if (P.row_flags) gmem(P.row_flags)[row] = flags;
     if (P.stats) {
       lsamp_row_stats st;
       st.max_value = y_max;
@@ -849,8 +963,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void k_topk(SamplePlan Pk, TopkWs Tk) {
   __shared__ TopkLds L;
-  const SamplePlan P = in_sgprs(Pk);
-  const TopkWs T = in_sgprs(Tk);
+  const SamplePlan& P = Pk;
+  const TopkWs& T = Tk;
   // work-group b runs on XCD b % 8; that XCD's rows are b % 8, + 8, + 16, ...
   const int b = (int)blockIdx.x;
   const int loc = b >> 3;
