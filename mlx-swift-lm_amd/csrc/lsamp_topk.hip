@@ -108,6 +108,13 @@ __device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint64_t elem_key(const RowCtx& c, float x, int32_t id) {
   return cand_key(to_filter(c, x), id);
 }
+// A candidate as first listed (its transformed value and id), and its key.
+__device__ __forceinline__ uint64_t raw_cand(float x, int32_t id) {
+  return ((uint64_t)__float_as_uint(x) << 32) | (uint32_t)id;
+}
+__device__ __forceinline__ uint64_t cand_key_of(const RowCtx& c, uint64_t r) {
+  return elem_key(c, __uint_as_float((uint32_t)(r >> 32)), (int32_t)(uint32_t)r);
+}
 
 // The exact K-th largest key among a slice's tokens x >= t, for a slice
 // whose candidates overflow (many equal values): a radix select over the
@@ -511,12 +518,13 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   };
 
   // ---------------------------------------------------------- F: candidates
-  // the tokens x >= t (and, after a radix select, key >= kmin) as keys in
-  // L.cand; L.ncand counts them all, kept or not
+  // the tokens x >= t (and, after a radix select, key >= kmin) in L.cand as
+  // raw (x, id) pairs (their keys are computed by the sort, in parallel);
+  // L.ncand counts them all, kept or not
   auto extract = [&](float t, bool by_key, uint64_t kmin) {
     // the quads of the wave where some lane's quad maximum reaches t, then
-    // one such quad at a time: a bitmask of its hits, one slot range per
-    // wave (a scan and one LDS atomic), keys only for the few hits
+    // one such quad at a time: a bitmask of its hits, a slot range for the
+    // lanes with hits (one LDS atomic each)
     uint32_t sel = 0u;
 #pragma unroll
     for (int g = 0; g < Q; ++g) {
@@ -537,15 +545,12 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
         }
         hits = h2;
       }
-      const int cnt = __builtin_popcount(hits);
-      if (__ballot(cnt > 0) == 0ull) return false;
-      const int incl = wave_incl_scan(cnt);
-      int wbase = 0;
-      if (l == 63) wbase = atomicAdd(&L.ncand, incl);
-      int slot = read_lane(wbase, 63) + incl - cnt;
-      for (uint32_t h = hits; h; h &= h - 1u, ++slot) {
-        const int e = __builtin_ctz(h);
-        if (slot < kCandCap) L.cand[slot] = elem_key(c, vec_elem_dyn<DT>(v, e), i0 + e);
+      if (hits) {
+        int slot = atomicAdd(&L.ncand, __builtin_popcount(hits));
+        for (uint32_t h = hits; h; h &= h - 1u, ++slot) {
+          const int e = __builtin_ctz(h);
+          if (slot < kCandCap) L.cand[slot] = raw_cand(vec_elem_dyn<DT>(v, e), i0 + e);
+        }
       }
       return false;
     });
@@ -553,11 +558,9 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
       const int j = k0 + tid;
       const float x = j < n_ent ? L.ex[j] : kNegInf;
       bool hit = x >= t && x > kNegInf;
-      uint64_t key = 0ull;
-      if (hit) key = elem_key(c, x, L.etok[j]);
-      if (by_key) hit = hit && key >= kmin;
+      if (by_key && hit) hit = elem_key(c, x, L.etok[j]) >= kmin;
       const int slot = wave_append(hit, &L.ncand);
-      if (hit && slot < kCandCap) L.cand[slot] = key;
+      if (hit && slot < kCandCap) L.cand[slot] = raw_cand(x, L.etok[j]);
     }
   };
 
@@ -603,10 +606,12 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   const int npub = n < K ? n : K;
   uint64_t* mine = L.best + slice * kTopkMaxK;
   if (n > 0 && n <= 64) {
-    // a wave's worth: lane i ranks key i against all of them (broadcast
-    // reads, eight at a time), no atomics
+    // a wave's worth: lane i turns candidate i into its key, then ranks it
+    // against all of them (broadcast reads, eight at a time), no atomics
     if (tid < 64) {
-      const uint64_t key = tid < n ? L.cand[tid] : 0ull;
+      const uint64_t key = tid < n ? cand_key_of(c, L.cand[tid]) : 0ull;
+      if (tid < n) L.cand[tid] = key;
+      __builtin_amdgcn_wave_barrier();
       int r = 0;
       for (int j0 = 0; j0 < n; j0 += 8) {
         uint64_t cj[8];
@@ -618,6 +623,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
       if (tid < n && r < npub) mine[r] = key;
     }
   } else if (n > 0) {
+    for (int i = tid; i < n; i += kThreads) L.cand[i] = cand_key_of(c, L.cand[i]);
+    __syncthreads();
     const int parts = n <= kThreads / 2 ? kThreads / n : 1;
     if (parts > 1) {
       const int i = tid % n, part = tid / n;
@@ -779,10 +786,64 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     }
   }
   __syncthreads();
-  // merge: rank of key (s, p) = p + the keys of the other slices above it
-  // (binary searches in their sorted lists)
-  {
-    static_assert(kTopkMaxK == 64, "one wave per slice list");
+  // The row's header totals, every lane from the slices' headers (broadcast
+  // reads, no cross-lane steps).
+  // (unrolled, every header read unconditionally and masked, so that the
+  // reads go out together and one wait covers them)
+  int total = 0;
+  float row_max = kNegInf;
+  uint32_t rfl = 0u;
+  int32_t ninf_row = 0;
+  int npub_s[kMaxSlices];
+#pragma unroll
+  for (int s = 0; s < kMaxSlices; ++s) {
+    const bool in = s < G;
+    const uint32_t f = in ? L.hflags[s] : 0u;
+    const float hx = L.hmax[s];
+    npub_s[s] = in ? L.hnpub[s] : 0;
+    rfl |= f;
+    row_max = __builtin_fmaxf(row_max, (f & kFLive) ? hx : kNegInf);
+    total += npub_s[s];
+    ninf_row += in ? L.hninf[s] : 0;
+  }
+  // The row's best keys in order, in L.merged.  At most 64 keys in all
+  // (every slice's list short, as min-p makes them): one wave ranks them.
+  // More: each slice's wave counts, for each of its keys, the keys above it
+  // in the other slices' sorted lists (binary searches).
+  static_assert(kTopkMaxK == 64, "one wave per slice list");
+  if (total <= 64) {
+    if (tid >= 64) {
+      if (tid == 64) {
+        gmem(T.ticket)[row] = 0u;
+        gmem(T.epoch)[row] = tag;
+      }
+      return;
+    }
+    // lane l's candidate: the l-th key of the lists laid end to end; its
+    // rank is the number of keys above it (compares against all of them,
+    // broadcast reads eight at a time), and it moves to that position
+    int sl = 0, pl = l;
+#pragma unroll
+    for (int s = 0; s < kMaxSlices; ++s) {
+      if (pl >= npub_s[s] && sl == s) {
+        pl -= npub_s[s];
+        sl = s + 1;
+      }
+    }
+    const uint64_t key = l < total ? L.best[sl * kTopkMaxK + pl] : 0ull;
+    L.cand[l] = key;
+    __builtin_amdgcn_wave_barrier();
+    int rk = 0;
+    for (int j0 = 0; j0 < total; j0 += 8) {
+      uint64_t kj[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) kj[q] = L.cand[j0 + q];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) rk += (j0 + q < total && kj[q] > key) ? 1 : 0;
+    }
+    if (l < total) L.merged[rk] = key;
+    __builtin_amdgcn_wave_barrier();
+  } else {
     const int s = __builtin_amdgcn_readfirstlane(tid) >> 6, p = l;
     if (s < G && p < L.hnpub[s]) {
       const uint64_t key = L.best[s * kTopkMaxK + p];
@@ -799,36 +860,28 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
       }
       if (r < kTopkMaxK) L.merged[r] = key;
     }
-  }
-  __syncthreads();
-  if (tid >= 64) {
-    if (tid == 64) {
-      gmem(T.ticket)[row] = 0u;
-      gmem(T.epoch)[row] = tag;
+    __syncthreads();
+    if (tid >= 64) {
+      if (tid == 64) {
+        gmem(T.ticket)[row] = 0u;
+        gmem(T.epoch)[row] = tag;
+      }
+      return;
     }
-    return;
   }
 
   // ---------------------------------------------------------- J: the row
-  int total = 0;
-  float row_max = kNegInf;
-  uint32_t rfl = 0u;
-  int32_t ninf_row = 0;
+  // the row's mass relative to its maximum (each slice's mass is relative to
+  // its own maximum)
   double z = 0.0;
-  {
-    const bool sl = l < G;
-    const uint32_t f = sl ? L.hflags[l] : 0u;
-    const bool live = (f & kFLive) != 0u;
-    const float hx = sl ? L.hmax[l] : kNegInf;
-    rfl = sl ? f : 0u;
+  if (c.kind != LSAMP_KIND_ARGMAX && row_max > kNegInf && row_max < kPosInf) {
 #pragma unroll
-    for (int d = 1; d < 64; d <<= 1) rfl |= (uint32_t)__shfl_xor((int)rfl, d, 64);
-    row_max = wave_max(live ? hx : kNegInf);
-    total = wave_sum(sl ? L.hnpub[l] : 0);
-    ninf_row = wave_sum(sl ? L.hninf[l] : 0);
-    if (c.kind != LSAMP_KIND_ARGMAX && row_max > kNegInf && row_max < kPosInf)
-      z = wave_sum(live && hx > kNegInf ? L.hz[l] * (double)__builtin_expf((hx - row_max) / (float)c.tf)
-                                        : 0.0);
+    for (int s = 0; s < kMaxSlices; ++s) {
+      const float hx = L.hmax[s];
+      const double hz = L.hz[s];
+      const bool live = s < G && (L.hflags[s] & kFLive) && hx > kNegInf;
+      z += live ? hz * (double)__builtin_amdgcn_exp2f((hx - row_max) * lgz) : 0.0;
+    }
   }
   const bool any = (rfl & kFLive) != 0u;
   const bool lost = L.lost != 0;
