@@ -93,6 +93,12 @@ def parse():
     return ap.parse_args()
 
 
+def sample_kernel_name(launch):
+    """The kernel(s) one sampling step launched (lsamp_launch_info.fused:
+    2 the one-pass top-k kernel, 1 the fused kernel, 0 the two-kernel split)."""
+    return {2: "k_topk", 1: "k_fused"}.get(launch["fused"], "k_stats+k_select")
+
+
 def graph_runner(launches, stream):
     """`launches`: callables, each enqueueing one step on `stream`.  Returns
     run(n), which enqueues exactly n steps: a graph of all of them replayed
@@ -466,7 +472,7 @@ def bench_config(args, n):
         "launch": launch,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg,
-                     "kernel": "k_fused" if launch["fused"] else "k_stats+k_select",
+                     "kernel": sample_kernel_name(launch),
                      "launch_us": step_us},
         "cpu_baseline": None,
     }
@@ -719,8 +725,9 @@ def main():
     k1_us = 1e3 * k1_ms / n_timed
     k2_us = 1e3 * k2_ms / n_timed
     if launch["fused"]:
-        kernel_us = {"k_fused": k1_us, "timed_calls": n_timed}
-        dom_name, dom_us = "k_fused", k1_us
+        dom_name = sample_kernel_name(launch)
+        kernel_us = {dom_name: k1_us, "timed_calls": n_timed}
+        dom_us = k1_us
     else:
         kernel_us = {"k_stats": k1_us, "k_select": k2_us, "timed_calls": n_timed}
         dom_name, dom_us = "k_stats+k_select", k1_us + k2_us
