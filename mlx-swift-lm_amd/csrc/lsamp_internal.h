@@ -317,6 +317,7 @@ struct VerifyPlan {
   int32_t* accepted;
   int32_t* tokens;
   uint8_t* accept_mask;
+  int32_t penalized;   // penalty-aware call: rows with a penalty accept exactly
 };
 
 // The one-pass top-k kernel over a plan whose rows all qualify (see TopkWs);

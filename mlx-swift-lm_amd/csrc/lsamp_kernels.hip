@@ -2158,6 +2158,11 @@ __global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, Verify
   if (tid == 0) {
     const lsamp_row_params prm = Q.params[s];
     const bool greedy = make_ctx(Q.semantics, prm).kind == LSAMP_KIND_ARGMAX;
+    // greedy rows, and rows with a presence or frequency penalty when the
+    // penalties are applied, accept exactly (DefaultSamplerV2.swift:496-502,
+    // CBv2MTPVerifyPenalties.applies, EngineLoopV2.swift:241-243)
+    const bool exact_row = greedy || (Q.penalized && (prm.presence_penalty != 0.0f ||
+                                                      prm.frequency_penalty != 0.0f));
     const int32_t* drafts = Q.draft_tokens + (size_t)s * D;
     const float* u = Q.uniforms + (size_t)s * W;
     uint8_t* am = Q.accept_mask ? Q.accept_mask + (size_t)s * D : nullptr;
@@ -2198,7 +2203,7 @@ __global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, Verify
         tok[j] = ws.vtokens[s * W + j];
         if (j >= D) continue;
         bool accept;
-        if (Q.mode == LSAMP_VERIFY_EXACT || greedy) {
+        if (Q.mode == LSAMP_VERIFY_EXACT || exact_row) {
           accept = tok[j] == drafts[j];
         } else {
           // p(draft) > min(1, delta * e^-H) on the filtered, tempered row

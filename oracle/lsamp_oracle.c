@@ -930,7 +930,9 @@ static void* verify_worker(void* arg) {
         tok[j] = draw_from_weights(V, wt, Wt, u[j]);
         if (j >= D) continue;
         int accept;
-        if (a->mode == LSAMP_VERIFY_EXACT || p->kind == LSAMP_KIND_ARGMAX) {
+        /* greedy rows, and penalty rows when penalties are applied, accept
+         * exactly (DefaultSamplerV2.swift:496-502) */
+        if (a->mode == LSAMP_VERIFY_EXACT || p->kind == LSAMP_KIND_ARGMAX || pen) {
           accept = tok[j] == drafts[j];
         } else {
           /* CBv2MTPTypicalAcceptanceTests.swift:16-33 restated in double on

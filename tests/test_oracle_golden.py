@@ -672,6 +672,43 @@ def test_typical_acceptance_uses_the_filtered_row():
         assert out["accept_mask"][0, 0] == want
 
 
+def test_penalized_typical_verify_accepts_penalty_rows_exactly():
+    # DefaultSamplerV2.swift:496-502: with penalties applied, rows whose
+    # params carry a presence or frequency penalty (CBv2MTPVerifyPenalties.
+    # applies, EngineLoopV2.swift:241-243) accept a draft only when it is the
+    # target draw; the other sampled rows keep the typical rule.  The drafts
+    # are the runner-up tokens, so the typical rule accepts where exact
+    # acceptance does not.
+    rng = np.random.default_rng(21)
+    S, Wn, V = 6, 4, 64
+    target = rng.normal(0, 0.3, (S, Wn, V)).astype(np.float32)
+    target[:, :, :2] += 3.0                    # two near-equal favourites
+    u = rng.random((S, Wn), dtype=np.float32)
+    pen = dict(temperature=1.0, presence_penalty=0.2, frequency_penalty=0.1)
+    plain = dict(temperature=1.0)
+    params = W._params([W.resolve_cbv2(vocab=V, **(pen if s % 2 == 0 else plain))
+                        for s in range(S)])
+    outs = [[] for _ in range(S)]                # no confirmed outputs
+    first = O.verify(mode=_ffi.VERIFY_EXACT, target=target, draft=None,
+                     draft_tokens=np.zeros((S, Wn - 1), np.int32), dtype=F32, params=params,
+                     uniforms=u, output_tokens=outs)
+    # the favourite the target draw did not pick, at every position
+    drafts = np.where(first["tokens"][:, :-1] == 0, 1, 0).astype(np.int32)
+    out = O.verify(mode=_ffi.VERIFY_TYPICAL, target=target, draft=None, draft_tokens=drafts,
+                   dtype=F32, params=params, uniforms=u, typical_delta=0.2, output_tokens=outs)
+    exact = out["tokens"][:, :-1] == drafts
+    typ = out["typical_margin"] > 0
+    for s in range(S):
+        if s % 2 == 0:
+            assert np.array_equal(out["accept_mask"][s].astype(bool), exact[s]), s
+        else:
+            assert np.array_equal(out["accept_mask"][s].astype(bool), typ[s]), s
+    # the rule matters here: on the plain rows the typical test accepts
+    # runner-up drafts that exact acceptance rejects (the penalty rows, built
+    # alike, would too under the typical rule)
+    assert (typ & ~exact)[1::2].any()
+
+
 @pytest.mark.parametrize("pkw", [dict(temperature=0.8, top_p=0.9), dict(temperature=0.0),
                                  dict(temperature=1.2, top_k=7, min_p=0.05)])
 def test_exact_verify_is_the_ordinary_draw_at_every_position(pkw):
