@@ -335,8 +335,8 @@ lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, dou
 lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode);
 
 /* Sticky device-side status bits raised since the last read (waits for the
- * device); clears them.  LSAMP_STATUS_SPIN_TIMEOUT: a fused step could not
- * gather all slices of a row (another workload held the CUs); the affected
+ * device); clears them.  LSAMP_STATUS_SPIN_TIMEOUT: a fused or top-k step
+ * could not gather all slices of a row (another workload held the CUs); the affected
  * rows carry LSAMP_ROW_TIMEOUT and token -1 in the same step's outputs. */
 #define LSAMP_STATUS_SPIN_TIMEOUT 1u
 /* a penalty-aware verify position had more entries than penalty_scratch_cap
@@ -344,11 +344,11 @@ lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode);
 #define LSAMP_STATUS_PENALTY_CAPACITY 2u
 lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
 
-/* Test hook of the fused arrangement's bounded waits, process-wide on
- * `device`: polls > 0 makes every wait's target unreachable and gives it up
- * after `polls` polls, so the fail-closed path (LSAMP_ROW_TIMEOUT) runs while
- * every kernel exits normally; 0 restores normal waits.  Synchronous; not for
- * use while other calls are in flight. */
+/* Test hook of the bounded waits (the fused arrangement's and the top-k
+ * kernel's finalizer), process-wide on `device`: polls > 0 makes every wait's
+ * target unreachable and gives it up after `polls` polls, so the fail-closed
+ * path (LSAMP_ROW_TIMEOUT) runs while every kernel exits normally; 0 restores
+ * normal waits.  Synchronous; not for use while other calls are in flight. */
 lsamp_status lsamp_set_spin_test(int32_t device, int32_t polls);
 
 /* Launch shape of the context's last lsamp_sample call (diagnostics; no

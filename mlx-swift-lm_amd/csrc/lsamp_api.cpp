@@ -404,7 +404,8 @@ lsamp_status lsamp_set_spin_test(int32_t device, int32_t polls) {
   if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
     return fail(LSAMP_ERR_DEVICE, "device %d not available (%d devices)", device, ndev);
   DeviceGuard guard(device);
-  if (set_spin_test(polls) != 0 || hipDeviceSynchronize() != hipSuccess)
+  if (set_spin_test(polls) != 0 || set_topk_spin_test(polls) != 0 ||
+      hipDeviceSynchronize() != hipSuccess)
     return fail(LSAMP_ERR_DEVICE, "setting the wait test hook failed");
   return ok();
 }

@@ -257,6 +257,7 @@ constexpr uint32_t kStatusSpinTimeout = 1u;  // a fused-kernel barrier wait time
 // 0 = normal; n > 0 = every wait's target is unreachable and it gives up after
 // n polls, so the fail-closed path runs while every kernel still exits.
 int set_spin_test(int32_t polls);
+int set_topk_spin_test(int32_t polls);  // the same hook for the top-k kernel's finalizer
 constexpr uint32_t kStatusPenaltyCapacity = 2u;  // a verify position's entries did not fit
 
 // Launch description resolved on the host.

@@ -49,6 +49,9 @@ using namespace rowops;
 constexpr int kCandCap = 1024;   // candidate keys a slice keeps in LDS
 constexpr int kTkTauBins = 1024;  // thread-maximum histogram
 constexpr int kSpin = 1 << 20;   // polls before the finalizer gives a slice up
+// lsamp_set_spin_test: > 0 makes the finalizer's wait unreachable (no word
+// counts as seen) and gives it up after this many polls
+__device__ int32_t g_topk_spin_test = 0;
 #ifndef LSAMP_TOPK_FIRST_QUADS
 #define LSAMP_TOPK_FIRST_QUADS 2
 #endif
@@ -729,6 +732,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   const float u_in = P.uniforms ? gmem(P.uniforms)[row] : 0.0f;
   const uint64_t key_in = (!P.uniforms && P.philox_keys) ? gmem(P.philox_keys)[row] : 0ull;
   const int32_t probe = P.probe_tokens ? gmem(P.probe_tokens)[row] : -1;
+  const int32_t spin_test =
+      __hip_atomic_load(&g_topk_spin_test, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // this slice's header; the others' words, polled until tagged with this
   // step (their slices started before this one, so each finishes)
   if (tid < kTopkHead) {
@@ -749,12 +754,13 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
 #pragma unroll
     for (int s = 0; s < kMaxSlices; ++s)
       w8[s] = (s < G && s != slice) ? ld_coherent(pub0 + s * kTopkWords) : ((uint64_t)tag << 32);
+    const int lim = spin_test > 0 ? spin_test : kSpin;
     for (int it = 0;; ++it) {
-      bool all = true;
+      bool all = spin_test <= 0;
 #pragma unroll
       for (int s = 0; s < kMaxSlices; ++s) all = all && (uint32_t)(w8[s] >> 32) == tag;
       if (all) break;
-      if (it >= kSpin) {
+      if (it >= lim) {
         L.lost = 1;
         break;
       }
@@ -1055,6 +1061,11 @@ int launch_topk(const SamplePlan& P, const TopkWs& T, void* stream, void* const*
     case LSAMP_DTYPE_BF16: return launch_topk_dt<LSAMP_DTYPE_BF16>(P, T, st, events);
     default: return launch_topk_dt<LSAMP_DTYPE_F16>(P, T, st, events);
   }
+}
+
+int set_topk_spin_test(int32_t polls) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_topk_spin_test), &polls, sizeof polls, 0,
+                                hipMemcpyHostToDevice);
 }
 
 int topk_blocks_per_cu(int dtype) {

@@ -1,4 +1,5 @@
-"""Fail-closed rows when the fused arrangement's bounded wait gives up.
+"""Fail-closed rows when a bounded wait gives up (the fused arrangement's
+waits, and the top-k kernel's finalizer).
 
 The wait test hook (lsamp_set_spin_test) makes every wait's target
 unreachable and its limit a few polls, forced from the host: every kernel
@@ -75,3 +76,28 @@ def test_split_mode_never_waits(ctx):
         ctx.set_mode(_ffi.MODE_AUTO)
     compare(cfg, g, o, label="split with the hook on")
     assert not (g["row_flags"] & _ffi.ROW_TIMEOUT).any()
+
+
+def test_topk_finalizer_timeout_fails_closed_and_recovers(ctx):
+    """The top-k kernel: every row's finalizer waits (for its other slices'
+    payloads, or, with one slice, through the hook alone), so with the hook
+    on every row fails closed; with it off the same step is exact again (the
+    tickets and epochs recover)."""
+    lib = _ffi.load_library()
+    cfg = W.config2(rows=16)
+    o = run_oracle(cfg, threads=16)
+    ctx.read_status()  # clear
+    _ffi.check(lib.lsamp_set_spin_test(0, 16), "lsamp_set_spin_test")
+    try:
+        g = run_gpu(ctx, cfg)
+        status = ctx.read_status()
+    finally:
+        _ffi.check(lib.lsamp_set_spin_test(0, 0), "lsamp_set_spin_test")
+    assert ctx.last_launch()["fused"] == 2
+    assert status & _ffi.STATUS_SPIN_TIMEOUT
+    assert ((g["row_flags"] & _ffi.ROW_TIMEOUT) != 0).all(), g["row_flags"]
+    assert (g["tokens"] == -1).all()
+    for _ in range(2):
+        compare(cfg, run_gpu(ctx, cfg), o, label="top-k after timeouts")
+        assert ctx.last_launch()["fused"] == 2
+    assert ctx.read_status() == 0
