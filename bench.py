@@ -86,17 +86,18 @@ def parse():
     ap.add_argument("--probe-steps", type=int, default=32)
     ap.add_argument("--path", default="sample",
                     choices=["sample", "c1", "c3", "c4", "c5", "top2", "logprobs", "commit",
-                             "verify", "masks"])
+                             "verify", "masks", "step"])
     ap.add_argument("--penalties", action="store_true",
                     help="--path verify: penalty-aware windows")
-    ap.add_argument("--top-k", type=int, default=20, help="--path logprobs: top_k")
+    ap.add_argument("--top-k", type=int, default=20,
+                    help="--path logprobs / step: top_k of the log-probabilities")
     return ap.parse_args()
 
 
 def sample_kernel_name(launch):
     """The kernel(s) one sampling step launched (lsamp_launch_info.fused:
     2 the one-pass top-k kernel, 1 the fused kernel, 0 the two-kernel split)."""
-    return {2: "k_topk", 1: "k_fused"}.get(launch["fused"], "k_stats+k_select")
+    return {3: "k_topk", 2: "k_topk", 1: "k_fused"}.get(launch["fused"], "k_stats+k_select")
 
 
 def graph_runner(launches, stream):
@@ -223,6 +224,8 @@ def bench_aux(args):
         return bench_config(args, int(args.path[1]))
     if args.path == "c5":
         return bench_c5(args)
+    if args.path == "step":
+        return bench_step(args)
     cfg = W.config2()
     B, V, R = cfg["rows"], cfg["vocab"], args.copies
     steps, warm = args.steps, args.warmup
@@ -310,6 +313,89 @@ def bench_aux(args):
                 break
         out["cpu_baseline"] = {"value": B * n / el, "unit": "rows/s", "cores": 1, "kind": "port",
                                "sample": f"{n} whole batches of {B} rows in {el:.1f} s, one thread"}
+    ctx.close()
+    print(json.dumps(out))
+    return 0
+
+
+def bench_step(args):
+    """One JSON line for lsamp_step on the headline batch (CBv2DefaultSampler.
+    sample: draw, penalty commit into a device table, raw log-probabilities
+    of the drawn tokens and the top --top-k): steps/s from a HIP graph of
+    `--copies` steps over distinct input copies, with and without the
+    log-probabilities, so the line shows what they cost.  The draw reads the
+    headline batch's penalty entries and the commit writes a table built from
+    the same histories: replaying fixed logits through a table that the draw
+    also read would pile penalties onto the drawn tokens step after step and
+    grow every row's history without bound, a workload no decode loop has."""
+    import numpy as np
+    import torch
+
+    from lsamp import workloads as W
+    from lsamp.api import Context, PenaltyTable
+    from lsamp.history import Cbv2RowState
+
+    cfg = W.config2()
+    B, V, R = cfg["rows"], cfg["vocab"], args.copies
+    steps, warm = args.steps, args.warmup
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(12)
+    ctx = Context(0, max_rows=B, max_vocab=V)
+    base = torch.from_numpy(cfg["logits"].view(np.int16)).view(torch.bfloat16)
+    copies = torch.empty((R, B, V), dtype=torch.bfloat16, device=dev)
+    for i in range(R):
+        copies[i].copy_(base)
+        if i:
+            idx = torch.from_numpy(rng.integers(0, V, B)).to(dev)
+            copies[i, torch.arange(B, device=dev), idx] = 0.0
+    u = torch.from_numpy(cfg["uniforms"]).to(dev)
+
+    def table():
+        states = []
+        for r in range(B):
+            e = cfg["entries"][cfg["row_ptr"][r]:cfg["row_ptr"][r + 1]]
+            hist = np.repeat(e["token"], e["count"])
+            states.append(Cbv2RowState(prompt=[], output=np.random.default_rng(r).permutation(hist),
+                                       repetition_window=64, repetition_on=False, counts_on=True,
+                                       vocab=V))
+        cap = max(len(st.entries()) for st in states) + steps + warm + 2 * R + 64
+        return PenaltyTable(states, capacity=cap, window_capacity=64)
+
+    stream = torch.cuda.Stream(device=dev)
+    res = {}
+    for k in (args.top_k, -1):
+        t = table()
+        preps = [ctx.prepare_step(copies[i], cfg["params"], table=t, uniforms=u, logprobs_top_k=k,
+                                  draw_from_table=False, row_ptr=cfg["row_ptr"],
+                                  entries=cfg["entries"])
+                 for i in range(R)]
+        with torch.cuda.stream(stream):
+            for p in preps:
+                p.launch(stream.cuda_stream)
+        torch.cuda.synchronize()
+        launch = ctx.last_launch()
+        run = graph_runner([(lambda p=p: p.launch(stream.cuda_stream)) for p in preps], stream)
+        wall_s, ev_ms = time_steps(run, stream, steps, warm)
+        res[k] = (wall_s, 1e3 * ev_ms / steps, launch)
+        del preps, run, t
+        torch.cuda.synchronize()
+    wall_s, us, launch = res[args.top_k]
+    wall0, us0, launch0 = res[-1]
+    kinds = {3: "k_topk with raw log-probabilities + k_commit", 2: "k_topk + k_commit + k_rank"}
+    out = {
+        "metric": f"decode steps/s with raw log-probabilities (top {args.top_k}) at B={B} V={V} "
+                  "(lsamp_step)",
+        "value": steps / wall_s, "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": 1e3 * wall_s / steps, "us_per_step_events": us,
+        "us_per_step_without_logprobs": us0, "logprob_cost_ratio": us / us0,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"] + f" + commit + log-probs top {args.top_k}",
+                   "input_copies": R,
+                   "kernels": kinds.get(launch["fused"], sample_kernel_name(launch)) ,
+                   "kernels_without_logprobs": sample_kernel_name(launch0) + " + k_commit"},
+        "roofline": None, "cpu_baseline": None,
+    }
     ctx.close()
     print(json.dumps(out))
     return 0

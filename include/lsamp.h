@@ -296,7 +296,7 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* args, voi
  * No counterpart in the reference: an entry point for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  lsamp_sample on the CURRENT device with its workspace in
- * a file-scope device array of LSAMP_NOALLOC_SCRATCH_BYTES (11 MiB, held by
+ * a file-scope device array of LSAMP_NOALLOC_SCRATCH_BYTES (12 MiB, held by
  * each GPU the library runs on until the process ends) instead of a context:
  * at most LSAMP_NOALLOC_MAX_ROWS rows of at most LSAMP_NOALLOC_MAX_VOCAB logits
  * (larger calls return LSAMP_ERR_CAPACITY).  Same arguments, results and
@@ -306,7 +306,7 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* args, voi
  * overlap on one GPU (unordered streams) race. */
 #define LSAMP_NOALLOC_MAX_ROWS 64
 #define LSAMP_NOALLOC_MAX_VOCAB 262144
-#define LSAMP_NOALLOC_SCRATCH_BYTES (11u << 20)
+#define LSAMP_NOALLOC_SCRATCH_BYTES (12u << 20)
 lsamp_status lsamp_sample_noalloc(const lsamp_sample_args* args, void* stream);
 
 /* Per-kernel timing hook, off by default (the role CBv2StepProfiler plays for
@@ -352,8 +352,9 @@ lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
 lsamp_status lsamp_set_spin_test(int32_t device, int32_t polls);
 
 /* Launch shape of the context's last lsamp_sample call (diagnostics; no
- * device work): top-k (2), fused (1) or split (0), slices per row, tokens per
- * slice, rows per round of the fused grid, work-groups per kernel launch. */
+ * device work): top-k with raw log-probabilities (3, lsamp_step), top-k (2),
+ * fused (1) or split (0), slices per row, tokens per slice, rows per round of
+ * the fused grid, work-groups per kernel launch. */
 typedef struct lsamp_launch_info {
   int32_t fused;
   int32_t slices;
@@ -482,9 +483,14 @@ lsamp_status lsamp_commit(lsamp_context* ctx, const lsamp_commit_args* args, voi
 /* ---- one decode step ----------------------------------------------------------
  * CBv2DefaultSampler.sample (DefaultSamplerV2.swift:84-181) as one call: the
  * draw (lsamp_sample), then the penalty commit of the drawn tokens into the
- * device table (lsamp_commit, :162), then the log-probabilities of the RAW
+ * device table (lsamp_commit, :162), and the log-probabilities of the RAW
  * logits for the drawn tokens and the top k (lsamp_logprobs, :167-176), all
- * enqueued on `stream` in that order.  Graph-capturable like its parts. */
+ * enqueued on `stream`.  When the draw runs the one-pass top-k kernel (AUTO
+ * mode, 16-bit logits, `sample.params_host` showing argmax or CBv2 top-k <=
+ * LSAMP_TOPK_MAX_K rows) that kernel writes the log-probabilities in the same
+ * pass over the logits (launch info `fused` = 3); otherwise they are a second
+ * pass (lsamp_logprobs).  Ids are the same either way and values agree to
+ * float rounding of the log-sum-exp.  Graph-capturable like its parts. */
 typedef struct lsamp_step_args {
   lsamp_sample_args sample;          /* the draw; its penalty arguments usually
                                         point at `table` (row_ptr[r] = r * capacity,

@@ -182,7 +182,8 @@ static bool topk_eligible(const lsamp_sample_args* a) {
 
 lsamp_status lsamp::sample_step(const WorkspaceViews& v, const DeviceShape& d, int32_t mode,
                                 const lsamp_sample_args* a, void* stream, void* const* ev,
-                                lsamp_launch_info* last) {
+                                lsamp_launch_info* last, const TopkLp* lp, bool* lp_done) {
+  if (lp_done) *lp_done = false;
   if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
   if (a->semantics != LSAMP_SEM_MLXLM && a->semantics != LSAMP_SEM_CBV2)
     return fail(LSAMP_ERR_INVALID_ARGUMENT, "unknown semantics %d", a->semantics);
@@ -277,16 +278,23 @@ lsamp_status lsamp::sample_step(const WorkspaceViews& v, const DeviceShape& d, i
     P.mask_bits = a->vocab;
     P.mask_tail = LSAMP_MASK_TAIL_KEEP;
   }
-  last->fused = topk ? 2 : P.fused;
+  // raw log-probabilities in the same launch: the top-k kernel, 16-bit logits
+  const bool lp_fused = topk && lp && lp->k >= 0 && a->dtype != LSAMP_DTYPE_F32;
+  TopkLp lpk{};
+  lpk.k = -1;
+  if (lp_fused) lpk = *lp;
+  last->fused = topk ? (lp_fused ? 3 : 2) : P.fused;
   last->slices = P.slices;
   last->slice_len = P.slice_len;
   last->rows_per_round = P.rows_per_round;
   last->grid = topk ? (P.rows + 7) / 8 * 8 * P.slices
                     : P.fused ? (P.rows < P.rows_per_round ? P.rows : P.rows_per_round) * P.slices
                               : P.rows * P.slices;
-  const int err = topk ? launch_topk(P, v.topk, stream, ev) : launch_sample(v.ws, P, stream, ev);
+  const int err =
+      topk ? launch_topk(P, v.topk, lpk, stream, ev) : launch_sample(v.ws, P, stream, ev);
   if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                             hipGetErrorString((hipError_t)err));
+  if (lp_done) *lp_done = lp_fused;
   return ok();
 }
 
@@ -457,7 +465,10 @@ lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, dou
   return ok();
 }
 
-lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* stream) {
+// lsamp_sample, and lsamp_step's draw with its raw log-probabilities (`lp`,
+// done in the same launch when *lp_done comes back true).
+static lsamp_status sample_call(lsamp_context* ctx, const lsamp_sample_args* a, void* stream,
+                                const TopkLp* lp, bool* lp_done) {
   if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
   DeviceGuard guard(ctx->device);
   void* const* ev = nullptr;
@@ -468,9 +479,13 @@ lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* 
       ev = reinterpret_cast<void* const*>(ctx->events + 3 * ctx->timed);
   }
   const lsamp_status st =
-      sample_step(ctx->views, ctx->shape, ctx->mode, a, stream, ev, &ctx->last);
+      sample_step(ctx->views, ctx->shape, ctx->mode, a, stream, ev, &ctx->last, lp, lp_done);
   if (st == LSAMP_OK && ev) ++ctx->timed;
   return st;
+}
+
+lsamp_status lsamp_sample(lsamp_context* ctx, const lsamp_sample_args* a, void* stream) {
+  return sample_call(ctx, a, stream, nullptr, nullptr);
 }
 
 lsamp_status lsamp_step(lsamp_context* ctx, const lsamp_step_args* a, void* stream) {
@@ -501,7 +516,16 @@ lsamp_status lsamp_step(lsamp_context* ctx, const lsamp_step_args* a, void* stre
     if (la.top_k > 0 && (!la.top_values || !la.top_ids))
       return fail(LSAMP_ERR_INVALID_ARGUMENT, "top_logprobs and top_ids are required");
   }
-  lsamp_status st = lsamp_sample(ctx, &sa, stream);
+  // the top-k kernel writes the raw log-probabilities in the same pass over
+  // the logits when it takes the step; otherwise they are a second pass
+  TopkLp lp{};
+  lp.k = a->logprobs_top_k;
+  lp.chosen = la.chosen;
+  lp.values = la.top_values;
+  lp.ids = la.top_ids;
+  bool lp_done = false;
+  lsamp_status st =
+      sample_call(ctx, &sa, stream, a->logprobs_top_k >= 0 ? &lp : nullptr, &lp_done);
   if (st != LSAMP_OK) return st;
   if (a->table) {
     lsamp_commit_args c{};
@@ -512,7 +536,7 @@ lsamp_status lsamp_step(lsamp_context* ctx, const lsamp_step_args* a, void* stre
     st = lsamp_commit(ctx, &c, stream);
     if (st != LSAMP_OK) return st;
   }
-  if (a->logprobs_top_k >= 0) return lsamp_logprobs(ctx, &la, stream);
+  if (a->logprobs_top_k >= 0 && !lp_done) return lsamp_logprobs(ctx, &la, stream);
   return ok();
 }
 

@@ -174,8 +174,14 @@ struct Workspace {
 // payload of tagged 64-bit words: tag (epoch + 1) in the high half, data in
 // the low half, so every word shows on its own whether it is this step's.
 constexpr int kTopkMaxK = 64;
+constexpr int kTopkMaxLp = 32;                     // raw log-probabilities per row
+static_assert(kTopkMaxLp == kRankMaxK, "lsamp_step's log-prob limit either way");
 constexpr int kTopkHead = 8;                       // header words per slice
-constexpr int kTopkWords = kTopkHead + 2 * kTopkMaxK;  // + (value, id) per key
+constexpr int kTopkWordsBase = kTopkHead + 2 * kTopkMaxK;  // + (value, id) per key
+// + (value, id) per raw key, written when the step also asks for raw
+// log-probabilities (the payload stride is the larger size either way)
+constexpr int kTopkRawWords = 2 * kTopkMaxLp;
+constexpr int kTopkWords = kTopkWordsBase + kTopkRawWords;
 struct TopkWs {
   uint64_t* pub;     // [max_rows][kMaxSlices][kTopkWords]
   uint32_t* ticket;  // [max_rows]
@@ -323,7 +329,19 @@ struct VerifyPlan {
 
 // The one-pass top-k kernel over a plan whose rows all qualify (see TopkWs);
 // `events` as launch_sample's.  Returns a hipError_t as int.
-int launch_topk(const SamplePlan& plan, const TopkWs& tw, void* stream, void* const* events);
+// Raw log-probabilities the top-k kernel can write in the same pass over the
+// logits (lsamp_step's log-prob outputs; LogitsPipelineV2.process :307-314
+// with CBv2Logprobs.gather :534-549): the chosen token's x - logsumexp(x) and
+// the k best tokens' by the raw order (value descending, lower id on ties,
+// NaN last).  k < 0: none.
+struct TopkLp {
+  int32_t k;       // -1, or 0 .. kTopkMaxLp
+  float* chosen;   // [rows]
+  float* values;   // [rows, k]
+  int32_t* ids;    // [rows, k]
+};
+int launch_topk(const SamplePlan& plan, const TopkWs& tw, const TopkLp& lp, void* stream,
+                void* const* events);
 // Work-groups of the top-k kernel that fit on one CU.
 int topk_blocks_per_cu(int dtype);
 
@@ -471,9 +489,13 @@ inline DeviceShape query_device_shape(int32_t cus) {
 // Validation, planning and launch of one sampling step (lsamp_sample) over a
 // workspace; records the launch shape in *last.  Sets the thread's last
 // error and returns its status.
+// `lp` (or NULL): raw log-probabilities wanted with the draw.  When the step
+// runs the top-k kernel it writes them in the same launch and *lp_done is
+// set; otherwise the caller computes them with lsamp_logprobs.
 lsamp_status sample_step(const WorkspaceViews& v, const DeviceShape& d, int32_t mode,
                          const lsamp_sample_args* a, void* stream, void* const* events,
-                         lsamp_launch_info* last);
+                         lsamp_launch_info* last, const TopkLp* lp = nullptr,
+                         bool* lp_done = nullptr);
 // The thread's last-error string (xgrammar_c.h:63-69 convention).
 lsamp_status set_error(lsamp_status st, const char* fmt, ...);
 lsamp_status clear_error();

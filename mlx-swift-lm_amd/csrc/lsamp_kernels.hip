@@ -1344,7 +1344,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   // built while the slice streams in and the pass over the slice starts on
   // each quad as it lands.
   const lsamp_row_params prm = load_params(P, row);
-  EntryPrefetch ep;
+  EntryPrefetch<> ep;
   entry_bounds(P, row, ep);
   const RowCtx c = make_ctx(P.semantics, prm);
   const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
@@ -1380,7 +1380,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     L.tmo = 0;
   }
   SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
-  EntryMarks em;
+  EntryMarks<> em;
   float emax = kNegInf;  // this thread's patched entry values
   mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
   if (!aligned || (end32 & (N - 1)) != 0) {

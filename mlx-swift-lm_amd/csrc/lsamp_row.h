@@ -200,19 +200,24 @@ struct SliceEntries {
   int32_t* count;   // LDS counter
 };
 
-// The row's first kEntPrefetch * kThreads penalty entries, one per thread and
-// pass, requested right behind the slice's logits (the CSR bounds come
-// through scalar loads, so they do not wait for the slice).
-constexpr int kEntPrefetch = 2;
+// The row's first KP * kThreads penalty entries, one per thread and pass,
+// requested right behind the slice's logits (the CSR bounds come through
+// scalar loads, so they do not wait for the slice).  Entries past them are
+// loaded after the whole slice (loads complete in order), so a kernel with
+// registers to spare prefetches more.
+constexpr int kEntPrefetch = 2;  // the default depth: 1,024 entries
+template <int KP = kEntPrefetch>
 struct EntryPrefetch {
+  static constexpr int K = KP;
   int32_t e0, e1;
-  lsamp_penalty_entry ent[kEntPrefetch];  // zero past the row's entries
+  lsamp_penalty_entry ent[KP];  // zero past the row's entries
   __device__ bool has(int tid, int k) const { return e0 + tid + k * kThreads < e1; }
 };
 
 // The row's CSR bounds (scalar loads; the row's parameters are requested
 // just before, so that both arrive in one round).
-__device__ __forceinline__ void entry_bounds(const SamplePlan& P, int row, EntryPrefetch& ep) {
+template <int KP>
+__device__ __forceinline__ void entry_bounds(const SamplePlan& P, int row, EntryPrefetch<KP>& ep) {
   ep.e0 = 0;
   ep.e1 = 0;
   if (P.row_ptr && P.entries) {
@@ -229,7 +234,9 @@ __device__ __forceinline__ void entry_bounds(const SamplePlan& P, int row, Entry
   }
 }
 
-__device__ __forceinline__ void prefetch_entries(const SamplePlan& P, int tid, EntryPrefetch& ep) {
+template <int KP>
+__device__ __forceinline__ void prefetch_entries(const SamplePlan& P, int tid,
+                                                 EntryPrefetch<KP>& ep) {
   static_assert(sizeof(lsamp_penalty_entry) == 16, "one 16-byte load per entry");
   // one buffer descriptor over the row's entries: lanes past them read zero,
   // and no branch holds a load back
@@ -237,7 +244,7 @@ __device__ __forceinline__ void prefetch_entries(const SamplePlan& P, int tid, E
       const_cast<lsamp_penalty_entry*>(P.entries) + ep.e0, 0,
       (ep.e1 - ep.e0) * (int)sizeof(lsamp_penalty_entry), kBufferWord3);
 #pragma unroll
-  for (int k = 0; k < kEntPrefetch; ++k) {
+  for (int k = 0; k < KP; ++k) {
     const auto w = __builtin_amdgcn_raw_buffer_load_b128(rs, (tid + k * kThreads) * 16, 0, 0);
     ep.ent[k] = __builtin_bit_cast(lsamp_penalty_entry, make_uint4(w[0], w[1], w[2], w[3]));
   }
@@ -249,9 +256,10 @@ __device__ __forceinline__ void prefetch_entries(const SamplePlan& P, int tid, E
 // prefetched entries are requested here and arrive while the pass runs.
 // finish_slice_entries patches them into the table.  Both steps fold the
 // patched values of the calling thread's entries into `emax`.
+template <int KP = kEntPrefetch>
 struct EntryMarks {
-  int slot[kEntPrefetch];
-  float xr[kEntPrefetch];
+  int slot[KP];
+  float xr[KP];
 };
 
 // Wave-aggregated append to an LDS list: returns this lane's slot or -1.
@@ -275,12 +283,12 @@ __device__ __forceinline__ float patched_entry(const SamplePlan& P, const RowCtx
   return x != x ? kNegInf : x;
 }
 
-template <int DT>
+template <int DT, int KP>
 __device__ __forceinline__ void mark_slice_entries(const SamplePlan& P, const RowCtx& c,
                                                    const lsamp_row_params& prm, const uint32_t* mrow,
                                                    const char* rowp, int64_t base, int64_t end,
-                                                   SliceEntries& se, const EntryPrefetch& ep,
-                                                   int tid, EntryMarks& em, float& emax) {
+                                                   SliceEntries& se, const EntryPrefetch<KP>& ep,
+                                                   int tid, EntryMarks<KP>& em, float& emax) {
   for (int i = tid; i < kSliceWords; i += kThreads) se.pen[i] = 0u;
   if (tid == 0) *se.count = 0;
   lds_barrier();
@@ -294,7 +302,7 @@ __device__ __forceinline__ void mark_slice_entries(const SamplePlan& P, const Ro
   // the slice's first token when there is no entry, so that nothing waits
   // for it before it is used.
 #pragma unroll
-  for (int k = 0; k < kEntPrefetch; ++k) {
+  for (int k = 0; k < KP; ++k) {
     const int32_t t = ep.ent[k].token;
     const bool in = ep.has(tid, k) && t >= base && t < end;
     if (in) {
@@ -305,7 +313,7 @@ __device__ __forceinline__ void mark_slice_entries(const SamplePlan& P, const Ro
     em.xr[k] = load_scalar<DT>(rowp, in ? t : base);
   }
   // the rest of a long history
-  for (int32_t e = ep.e0 + tid + kEntPrefetch * kThreads; e < ep.e1; e += kThreads) {
+  for (int32_t e = ep.e0 + tid + KP * kThreads; e < ep.e1; e += kThreads) {
     const lsamp_penalty_entry ent = gload16(P.entries + e);
     if (ent.token >= base && ent.token < end) {
       const int idx = mark(ent.token);
@@ -320,14 +328,14 @@ __device__ __forceinline__ void mark_slice_entries(const SamplePlan& P, const Ro
   lds_barrier();  // the bitmap is complete
 }
 
-template <int DT>
+template <int DT, int KP>
 __device__ __forceinline__ void finish_slice_entries(const SamplePlan& P, const RowCtx& c,
                                                      const lsamp_row_params& prm,
                                                      const uint32_t* mrow, SliceEntries& se,
-                                                     const EntryPrefetch& ep, const EntryMarks& em,
-                                                     float& emax) {
+                                                     const EntryPrefetch<KP>& ep,
+                                                     const EntryMarks<KP>& em, float& emax) {
 #pragma unroll
-  for (int k = 0; k < kEntPrefetch; ++k) {
+  for (int k = 0; k < KP; ++k) {
     if (em.slot[k] >= 0 && em.slot[k] < kSliceEntryCap) {
       const float x = patched_entry<DT>(P, c, prm, mrow, em.xr[k], ep.ent[k]);
       se.x[em.slot[k]] = x;

@@ -47,6 +47,8 @@ using namespace dev;
 using namespace rowops;
 
 constexpr int kCandCap = 1024;   // candidate keys a slice keeps in LDS
+constexpr int kRStageCap = 256;  // raw quads staged for the raw candidate scan
+constexpr int kRCandCap = 256;   // raw candidates a slice keeps
 constexpr int kTkTauBins = 1024;  // thread-maximum histogram
 constexpr int kSpin = 1 << 20;   // polls before the finalizer gives a slice up
 // lsamp_set_spin_test: > 0 makes the finalizer's wait unreachable (no word
@@ -62,13 +64,19 @@ constexpr int kTopkFirstQuads = LSAMP_TOPK_FIRST_QUADS;  // slab quads requested
 static_assert(kTopkWords <= kThreads, "one payload word per thread");
 static_assert(kMaxSlices * kTopkMaxK <= kThreads, "one merged key per thread");
 
-// Header words of a slice's payload.
-enum : int { kHMax = 0, kHZHi, kHZLo, kHNpub, kHFlags, kHNinf };
+
+// Header words of a slice's payload.  kHNpub holds the slice's key count and,
+// in the high half, its raw key count; kHRMax / kHRZ the raw logits' largest
+// finite value and their sum of exp(x - that value) (raw log-probabilities).
+enum : int { kHMax = 0, kHZHi, kHZLo, kHNpub, kHFlags, kHNinf, kHRMax, kHRZ };
 // Slice flags (header word kHFlags).
 constexpr uint32_t kFNonfinite = 1u;   // a raw logit is NaN or +-inf
 constexpr uint32_t kFLive = 2u;        // a token survived masking (finite or +inf)
 constexpr uint32_t kFPosInf = 4u;      // a transformed logit is +inf
 constexpr uint32_t kFEntOverflow = 8u; // more penalty entries than the slice table holds
+constexpr uint32_t kFRawNaN = 16u;     // a raw logit is NaN
+constexpr uint32_t kFRawPosInf = 32u;  // a raw logit is +inf
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct TopkLds {
   uint32_t pen[kSliceWords];
@@ -77,6 +85,7 @@ struct TopkLds {
   uint64_t cand[kCandCap];
   int32_t racc[kCandCap];
   uint64_t best[kMaxSlices * kTopkMaxK];  // slice s's sorted keys at s * kTopkMaxK
+  uint64_t rbest[kMaxSlices * kTopkMaxLp];  // slice s's sorted raw keys at s * kTopkMaxLp
   uint64_t merged[kTopkMaxK];             // the row's best keys, sorted
   uint32_t hist[kTkTauBins];
   // the row's slice headers (finalizer)
@@ -85,12 +94,23 @@ struct TopkLds {
   int32_t hnpub[kMaxSlices];
   uint32_t hflags[kMaxSlices];
   int32_t hninf[kMaxSlices];
+  float hrmax[kMaxSlices];
+  float hrz[kMaxSlices];
   // reductions
   float redf[kWaves];
   float redf2[kWaves];
   uint32_t redu[kWaves];
   int32_t redi[kWaves];
   uint64_t redz[kWaves];
+  float rredf[kWaves];    // raw: the wave's largest finite logit
+  float rtop[kWaves];     // raw: each wave's c-th largest finite thread maximum
+  uint32_t rstage[4 * kRStageCap];  // raw: the quads that may hold candidates
+  int32_t rstage_at[kRStageCap];  // their first token ids
+  uint64_t rcand[kRCandCap];      // raw candidates (raw pairs, then keys)
+  int32_t rracc[kRCandCap];       // their ranks (the parts sort)
+  int32_t nstage;
+  int32_t nrcand;
+  double rredz[kWaves];   // raw: the wave's sum of exp(x - slice raw maximum)
   int32_t misc[8];
   uint64_t prefix;
   int32_t ecount;
@@ -118,6 +138,38 @@ __device__ __forceinline__ uint64_t raw_cand(float x, int32_t id) {
 __device__ __forceinline__ uint64_t cand_key_of(const RowCtx& c, uint64_t r) {
   return elem_key(c, __uint_as_float((uint32_t)(r >> 32)), (int32_t)(uint32_t)r);
 }
+// Key of a raw logit in the raw order of log-probabilities (value
+// descending, lower id on ties, +0 and -0 tied, NaN last): NaN has value
+// key 0, below every other value's.
+__device__ __forceinline__ uint64_t raw_key(float x, int32_t id) {
+  return ((uint64_t)(x != x ? 0u : key_hi(x)) << 32) | (uint64_t)(0xffffffffu - (uint32_t)id);
+}
+__device__ __forceinline__ uint64_t raw_key_of(uint64_t r) {
+  return raw_key(__uint_as_float((uint32_t)(r >> 32)), (int32_t)(uint32_t)r);
+}
+
+// The exclusion bits of a thread's quads (N bits a quad, packed), kept when
+// the registers keep the raw logits (the variant that also ranks them).
+// (A vector type, not an array: read with a quad index known only at run
+// time, an array would be placed in scratch memory.)
+template <int DT>
+struct ExBits {
+  static constexpr int N = Vec<DT>::N;
+  static constexpr int PER = 32 / N;  // quads per word
+  static constexpr int W = (Slab<DT>::Q + PER - 1) / PER;
+  static_assert(W == 4, "four words");
+  typedef uint32_t words_t __attribute__((ext_vector_type(4)));
+  words_t w;
+  __device__ __forceinline__ void clear() { w = words_t{0u, 0u, 0u, 0u}; }
+  __device__ __forceinline__ void set(int g, uint32_t ex) {  // g known at compile time
+    w[g / PER] |= ex << ((g % PER) * N);
+  }
+  __device__ __forceinline__ uint32_t get(int g) const {  // any uniform g
+    const int i = g / PER;
+    const uint32_t x = i < 2 ? (i == 0 ? w.x : w.y) : (i == 2 ? w.z : w.w);
+    return (x >> ((g % PER) * N)) & ((1u << N) - 1u);
+  }
+};
 
 // The exact K-th largest key among a slice's tokens x >= t, for a slice
 // whose candidates overflow (many equal values): a radix select over the
@@ -190,9 +242,84 @@ __device__ __noinline__ uint64_t kth_key_mem(const RowCtx c, const char* rowp,
   return prefix;
 }
 
+// The slice's K best raw keys (every token, NaN included), for a slice whose
+// threshold left too few or too many candidates (NaN, +inf or many equal
+// logits): a radix select of the exact K-th key over the slice read again
+// from memory (L2), then every key at or above it listed as a raw pair in
+// L.cand.  Returns how many were listed (min(K, slice length)).  Called by
+// the whole work-group.
 template <int DT>
-__device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, int row, int slice,
-                                          TopkLds& L) {
+__device__ __noinline__ int raw_select_mem(const char* rowp, int32_t base32, int32_t end32, int K,
+                                           uint64_t* dst, int32_t* cnt, TopkLds& L) {
+  const int tid = (int)threadIdx.x;
+  const int len = end32 - base32;
+  if (K > len) K = len;
+  uint64_t prefix = 0ull;
+  int need = K;
+#pragma unroll 1
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    const uint64_t hmask = shift == 56 ? 0ull : ~0ull << (shift + 8);
+    for (int i = tid; i < 256; i += kThreads) L.hist[i] = 0u;
+    __syncthreads();
+#pragma unroll 1
+    for (int32_t i = base32 + tid; i < end32; i += kThreads) {
+      const uint64_t key = raw_key(load_scalar<DT>(rowp, i), i);
+      if ((key & hmask) == prefix) atomicAdd(&L.hist[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // digits from the top: lane l holds digits 255 - 4l .. 252 - 4l
+      uint32_t cb[4];
+      uint32_t cs = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        cb[i] = L.hist[255 - (4 * tid + i)];
+        cs += cb[i];
+      }
+      const uint32_t ic = wave_incl_scan(cs);
+      const uint64_t hit = __ballot(ic >= (uint32_t)need);
+      const int f = hit ? __builtin_ctzll(hit) : 63;
+      uint32_t acc = read_lane(ic - cs, f);
+      int digit = 0, above = 0;
+      if (tid == f) {
+        for (int i = 0; i < 4; ++i) {
+          if (acc + cb[i] >= (uint32_t)need) {
+            digit = 255 - (4 * tid + i);
+            above = (int)acc;
+            break;
+          }
+          acc += cb[i];
+        }
+      }
+      digit = read_lane(digit, f);
+      above = read_lane(above, f);
+      if (tid == 0) {
+        L.misc[0] = digit;
+        L.misc[1] = above;
+      }
+    }
+    __syncthreads();
+    prefix |= (uint64_t)(uint32_t)L.misc[0] << shift;
+    need -= L.misc[1];
+  }
+  // the keys >= the K-th: exactly K of them (keys are distinct)
+  if (tid == 0) *cnt = 0;
+  __syncthreads();
+#pragma unroll 1
+  for (int32_t i0 = base32; i0 < end32; i0 += kThreads) {
+    const int32_t i = i0 + tid;
+    const float x = i < end32 ? load_scalar<DT>(rowp, i) : 0.0f;
+    const bool hit = i < end32 && raw_key(x, i) >= prefix;
+    const int slot = wave_append(hit, cnt);
+    if (hit && slot < K) dst[slot] = raw_cand(x, i);
+  }
+  __syncthreads();
+  return K;
+}
+
+template <int DT, bool LP>
+__device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, const TopkLp& LPo,
+                                          int row, int slice, TopkLds& L) {
   constexpr int N = Vec<DT>::N;
   constexpr int Q = Slab<DT>::Q;
   constexpr uint32_t FULL = (1u << N) - 1u;
@@ -240,7 +367,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   // (the parameters first: the bounds are used as soon as they arrive, and
   // one wait then covers both)
   const lsamp_row_params prm = load_params(P, row);
-  EntryPrefetch ep;
+  EntryPrefetch<> ep;
   entry_bounds(P, row, ep);
   prefetch_entries(P, tid, ep);
 #if LSAMP_TOPK_REST_AFTER_MARK == 0
@@ -272,12 +399,16 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   if (tid == 0) {
     L.ncand = 0;
     L.lost = 0;
+    L.nstage = 0;
+    L.nrcand = 0;
   }
   for (int i = tid; i < kCandCap; i += kThreads) L.racc[i] = 0;
+  if constexpr (LP)
+    for (int i = tid; i < kRCandCap; i += kThreads) L.rracc[i] = 0;
 
   // ---------------------------------------------------------- B: entries
   SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
-  EntryMarks em;
+  EntryMarks<decltype(ep)::K> em;
   float emax = kNegInf;
   mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
 #if LSAMP_TOPK_REST_AFTER_MARK != 0
@@ -306,6 +437,9 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   // slice and NaNs become -inf in the registers.  The thread's maximum, its
   // quads' maxima and its sum of exp((x - m) / T_f) (anchored at a quad
   // maximum, re-anchored by an exact power of two) are taken as quads land.
+  // (With raw log-probabilities (LP) the registers keep the raw logits, the
+  // exclusions are kept as bits, and the raw logits' maximum, quad maxima
+  // and sum of exp(x) are taken too, past the slice's end excluded only.)
   const float lgz = (float)(1.4426950408889634 / c.tf);
   const uint32_t* penw = L.pen + ((tid * N) >> 5);
   constexpr int kQuadWords = kThreads * N / 32;
@@ -329,17 +463,52 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   // penalized or not
   uint32_t rawhi = 0u;
   constexpr uint32_t kInfHalf = DT == LSAMP_DTYPE_BF16 ? 0x7f80u : 0x7c00u;
-  for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
+  // (LP) raw statistics and the exclusion bits
+  float rmax = kNegInf, zr = 0.0f, nbr = __FLT_MAX__;
+  bool rnan = false;
+  uint32_t rqp[LP ? Q / 2 : 1];
+#pragma unroll
+  for (int i = 0; i < (LP ? Q / 2 : 1); ++i) rqp[i] = 0xff80ff80u;
+  ExBits<DT> exb;
+  exb.clear();
+  for_quads_static(S, nq, [&](int g, uint4& vin) -> bool {
     const int32_t i0 = base32 + (tid + g * kThreads) * N;
     const uint32_t pcur = pw;
     if (g + 1 < Q) pw = penw[(g + 1) * kQuadWords];
     uint32_t ex = (pcur >> pen_shift) & FULL;
+    uint32_t tl = 0u;
     if (g >= nq_tail) {
       // the quads that can reach past this slice's end: every earlier one is
       // whole for every thread (the last slice of a row is shorter)
       const int32_t rem = lim - g * (kThreads * N);
-      ex |= (~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem))) & FULL;
+      tl = (~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem))) & FULL;
+      ex |= tl;
     }
+    if constexpr (LP) {
+      uint4 vr = vin;
+      if (g >= nq_tail) exclude_elems<DT>(vr, tl);
+      float rq = vec_max_nn<DT>(vr);
+      if (rq != rq) {
+        // a NaN in the quad (rare): the largest of the others
+        rq = kNegInf;
+#pragma unroll
+        for (int e = 0; e < N; ++e) rq = __builtin_fmaxf(rq, vec_elem<DT>(vr, e));
+      }
+      rmax = __builtin_fmaxf(rmax, rq);
+      if (g & 1)
+        rqp[g / 2] = (rqp[g / 2] & 0xffffu) | (hi16_up(rq) << 16);
+      else
+        rqp[g / 2] = (rqp[g / 2] & 0xffff0000u) | hi16_up(rq);
+      if (__builtin_fmaf(rq, kLog2e, nbr) > 64.0f) {
+        const float nn = -__builtin_ceilf(__builtin_amdgcn_fmed3f(rq * kLog2e, -0x1p20f, 0x1p20f));
+        zr = __builtin_ldexpf(zr, (int)__builtin_fmaxf(nn - nbr, -512.0f));
+        nbr = nn;
+      }
+#pragma unroll
+      for (int e = 0; e < N; ++e)
+        zr += __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(vr, e), kLog2e, nbr));
+    }
+    uint4 v = vin;
     if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
     if constexpr (N == 8) {
       constexpr uint32_t M = 0x7fff7fffu;
@@ -352,7 +521,10 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
 #pragma unroll
         for (int e = 0; e < N; ++e) {
           const float x = vec_elem<DT>(v, e);
-          if (x != x) ex |= 1u << e;
+          if (x != x) {
+            ex |= 1u << e;
+            rnan = true;
+          }
         }
       }
     }
@@ -370,6 +542,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
           ninf += x == kPosInf ? 1 : 0;
         }
         exclude_elems<DT>(v, nan);
+        ex |= nan;
         qm = vec_max_nn<DT>(v);
         nf_acc = 0x80008000u;
       }
@@ -394,10 +567,17 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
       for (int e = 0; e < N; ++e)
         zt += __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(v, e), lgz, nbz));
     }
-    return true;
+    if constexpr (LP) {
+      exb.set(g, ex);
+      return false;  // the registers keep the raw logits
+    } else {
+      vin = v;
+      return true;
+    }
   });
   if constexpr (N == 8) {
     if ((rawhi & 0xffffu) >= kInfHalf || (rawhi >> 16) >= kInfHalf) nf_acc = 0x80008000u;
+    rnan = (rawhi & 0xffffu) > kInfHalf || (rawhi >> 16) > kInfHalf;
   }
   const bool zref = nbz < __FLT_MAX__;
   finish_slice_entries<DT>(P, c, prm, mrow, se, ep, em, emax);
@@ -413,13 +593,35 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   {
     const float hi = wave_max(tmax);
     const float lo = wave_min(tmax > kNegInf ? tmax : kPosInf);
-    const uint32_t nf = __ballot(nonfinite_seen<DT>(nf_acc)) != 0ull ? kFNonfinite : 0u;
+    uint32_t nf = __ballot(nonfinite_seen<DT>(nf_acc)) != 0ull ? kFNonfinite : 0u;
     const int32_t ni = wave_sum(ninf);
+    float rhi = kNegInf, rct = kNegInf;
+    if constexpr (LP) {
+      // raw: the largest finite logit, NaN and +inf seen, and the wave's
+      // c-th largest finite thread maximum, c = ceil(LPo.k / 8): the waves'
+      // 8c largest are >= the smallest of these, so that bounds the slice's
+      // LPo.k-th largest thread maximum (and token) from below
+      const float rf = rmax < kPosInf ? rmax : kNegInf;
+      rhi = wave_max(rf);
+      nf |= (__ballot(rnan) ? kFRawNaN : 0u) | (__ballot(rmax == kPosInf) ? kFRawPosInf : 0u);
+      const int cth = (LPo.k + kWaves - 1) / kWaves;
+      float v = rf;
+      rct = rhi;
+      for (int i = 1; i < cth; ++i) {
+        const uint64_t at = __ballot(v == rct);  // drop one lane holding it
+        if (at && l == __builtin_ctzll(at)) v = kNegInf;
+        rct = wave_max(v);
+      }
+    }
     if (l == 0) {
       L.redf[wv] = hi;
       L.redf2[wv] = lo;
       L.redu[wv] = nf;
       L.redi[wv] = ni;
+      if constexpr (LP) {
+        L.rredf[wv] = rhi;
+        L.rtop[wv] = rct;
+      }
     }
   }
   __syncthreads();
@@ -432,6 +634,27 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     tlo = __builtin_fminf(tlo, L.redf2[i]);
     sflags |= L.redu[i];
     sninf += L.redi[i];
+  }
+  // (LP) the slice's largest finite raw logit, the raw threshold and the
+  // raw sum of exp(x - rsmax) (double, fixed order over the waves).  The
+  // threshold is the smallest of the waves' c-th largest finite thread
+  // maxima, c = ceil(LPo.k / 8): the waves' 8c largest are at or above it,
+  // so at least LPo.k tokens are.
+  float rsmax = kNegInf, rtau = kPosInf;
+  if constexpr (LP) {
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      rsmax = __builtin_fmaxf(rsmax, L.rredf[i]);
+      rtau = __builtin_fminf(rtau, L.rtop[i]);
+    }
+    double rz = 0.0;
+    if (rsmax > kNegInf && nbr < __FLT_MAX__) {
+      const float bh = rsmax * kLog2e;
+      const float bl = __builtin_fmaf(rsmax, kLog2e, -bh);
+      rz = (double)zr * (double)__builtin_amdgcn_exp2f((-nbr - bh) - bl);
+    }
+    rz = wave_sum(rz);
+    if (l == 0) L.rredz[wv] = rz;
   }
   const bool posinf = smax == kPosInf;
   const bool has_finite = smax > kNegInf && !posinf;
@@ -472,15 +695,16 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   // min-p: a kept token has y >= y_max + ln(min_p) >= y_smax + ln(min_p); in
   // x-space, with a hundredth of a nat to spare for the rounding of x / T
   const float tau_m = m_on ? smax + (float)c.tf * (__builtin_logf(mp) - 0.01f) : kNegInf;
-  // the k-th largest thread maximum, from a histogram of the maxima below
-  // the slice maximum (half a bin of slack covers the bin index's rounding)
-  auto tau_hist = [&]() -> float {
+  // the K-th largest thread maximum, from a histogram of the maxima within
+  // dcap below the slice maximum hmax (half a bin of slack covers the bin
+  // index's rounding); lo: the smallest thread maximum above -inf
+  auto tau_hist = [&](float hmax, float lo, float mine, float dcap, int K) -> float {
     for (int i = tid; i < kTkTauBins; i += kThreads) L.hist[i] = 0u;
     __syncthreads();
-    const float D = __builtin_fminf(smax - tlo, (float)(32.0 * c.tf));
+    const float D = __builtin_fminf(hmax - lo, dcap);
     const float sc = D > 0.0f ? (float)(kTkTauBins - 1) / D : 0.0f;
-    if (tmax > kNegInf) {
-      const float fb = (smax - tmax) * sc;
+    if (mine > kNegInf) {
+      const float fb = (hmax - mine) * sc;
       const int b = fb < (float)(kTkTauBins - 1) ? (int)fb : kTkTauBins - 1;
       atomicAdd(&L.hist[b], 1u);
     }
@@ -517,7 +741,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     const int bs = L.misc[6];
     return bs >= kTkTauBins
                ? kNegInf
-               : ((bs == kTkTauBins - 1 || sc == 0.0f) ? tlo : smax - ((float)bs + 1.5f) / sc);
+               : ((bs == kTkTauBins - 1 || sc == 0.0f) ? lo : hmax - ((float)bs + 1.5f) / sc);
   };
 
   // ---------------------------------------------------------- F: candidates
@@ -535,8 +759,10 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
       const float qm = __uint_as_float(g & 1 ? w & 0xffff0000u : w << 16);
       if (__ballot(qm >= t) != 0ull) sel |= 1u << g;
     }
-    for_quads_sel(S, sel, [&](int g, uint4& v) -> bool {
+    for_quads_sel(S, sel, [&](int g, uint4& vq) -> bool {
       const int32_t i0 = base32 + (tid + g * kThreads) * N;
+      uint4 v = vq;
+      if constexpr (LP) exclude_elems<DT>(v, exb.get(g));  // (raw registers)
       uint32_t hits = 0u;
 #pragma unroll
       for (int e = 0; e < N; ++e) hits |= (vec_elem<DT>(v, e) >= t ? 1u : 0u) << e;
@@ -578,7 +804,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   } else if (m_on) {
     t0 = tau_m;
   } else {
-    t0 = tau_hist();
+    t0 = tau_hist(smax, tlo, tmax, (float)(32.0 * c.tf), K);
   }
   float tc = margin(t0);
   bool by_key = false, hist_tried = !(m_on && !posinf && K > 1);
@@ -592,7 +818,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     if (n <= kCandCap) break;
     if (!hist_tried) {
       hist_tried = true;
-      tc = margin(__builtin_fmaxf(tau_hist(), tau_m));
+      tc = margin(__builtin_fmaxf(tau_hist(smax, tlo, tmax, (float)(32.0 * c.tf), K), tau_m));
     } else {
       kmin = kth_key_mem<DT>(c, rowp, mrow, P.mask_words, P.mask_bits, P.mask_tail, base32,
                              end32, n_ent, tc, K, L);
@@ -605,60 +831,197 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
 
   // ---------------------------------------------------------- G: sort
   // rank of a key = the keys above it (keys are distinct: ids are); the
-  // comparisons of a key are split over `parts` threads
+  // comparisons of a key are split over `parts` threads.  The n raw pairs in
+  // L.cand become keys (keyof); the best npub go to dst in order.
+  // (src: the candidates, ranks accumulated in racc, which starts at zero)
+  // (wide: the comparisons split over every thread even for a wave's worth)
+  auto sort_into = [&](int n, int npub, uint64_t* dst, auto keyof, uint64_t* src,
+                       int32_t* racc, bool wide) {
+    if (n > 0 && n <= 64 && !wide) {
+      // a wave's worth: lane i turns candidate i into its key, then ranks it
+      // against all of them (broadcast reads, eight at a time), no atomics
+      if (tid < 64) {
+        const uint64_t key = tid < n ? keyof(src[tid]) : 0ull;
+        if (tid < n) src[tid] = key;
+        __builtin_amdgcn_wave_barrier();
+        int r = 0;
+        for (int j0 = 0; j0 < n; j0 += 8) {
+          uint64_t cj[8];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) cj[q] = src[j0 + q];
+#pragma unroll
+          for (int q = 0; q < 8; ++q) r += (j0 + q < n && cj[q] > key) ? 1 : 0;
+        }
+        if (tid < n && r < npub) dst[r] = key;
+      }
+    } else if (n > 0) {
+      for (int i = tid; i < n; i += kThreads) src[i] = keyof(src[i]);
+      __syncthreads();
+      const int parts = n <= kThreads / 2 ? kThreads / n : 1;
+      if (parts > 1) {
+        const int i = tid % n, part = tid / n;
+        if (part < parts) {
+          const uint64_t key = src[i];
+          const int j0 = (n * part) / parts, j1 = (n * (part + 1)) / parts;
+          int r = 0;
+          for (int j = j0; j < j1; ++j) r += src[j] > key ? 1 : 0;
+          if (r) atomicAdd(&racc[i], r);
+        }
+        __syncthreads();
+        for (int i2 = tid; i2 < n; i2 += kThreads) {
+          const int r = racc[i2];
+          if (r < npub) dst[r] = src[i2];
+        }
+      } else {
+        for (int i = tid; i < n; i += kThreads) {
+          const uint64_t key = src[i];
+          int r = 0;
+          for (int j = 0; j < n; ++j) r += src[j] > key ? 1 : 0;
+          if (r < npub) dst[r] = key;
+        }
+      }
+    }
+  };
   const int npub = n < K ? n : K;
   uint64_t* mine = L.best + slice * kTopkMaxK;
-  if (n > 0 && n <= 64) {
-    // a wave's worth: lane i turns candidate i into its key, then ranks it
-    // against all of them (broadcast reads, eight at a time), no atomics
-    if (tid < 64) {
-      const uint64_t key = tid < n ? cand_key_of(c, L.cand[tid]) : 0ull;
-      if (tid < n) L.cand[tid] = key;
-      __builtin_amdgcn_wave_barrier();
-      int r = 0;
-      for (int j0 = 0; j0 < n; j0 += 8) {
-        uint64_t cj[8];
+  sort_into(n, npub, mine, [&](uint64_t r) { return cand_key_of(c, r); }, L.cand, L.racc, false);
+
+  // ---------------------------------------------------------- payload words
+  if (tid == 0) {
+    L.tag = epoch + 1u;
+    L.last = ticket + 1u == (uint32_t)G ? 1 : 0;
+  }
+  uint64_t zs = 0ull;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) cj[q] = L.cand[j0 + q];
+  for (int i = 0; i < kWaves; ++i) zs += L.redz[i];
+  const double zsum = (double)zs * 0x1p-40;
+  int nraw = 0;  // (LP) the slice's raw keys, sorted in rbest
+  double rzs = 0.0;
+  if constexpr (LP) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) r += (j0 + q < n && cj[q] > key) ? 1 : 0;
-      }
-      if (tid < n && r < npub) mine[r] = key;
+    for (int i = 0; i < kWaves; ++i) rzs += L.rredz[i];
+  }
+  auto word = [&](int w) -> uint32_t {
+    if (LP && w >= kTopkWordsBase) {
+      const int p = (w - kTopkWordsBase) >> 1;
+      if (p >= nraw) return 0u;
+      const uint64_t key = L.rbest[slice * kTopkMaxLp + p];
+      return (w - kTopkWordsBase) & 1 ? (uint32_t)key : (uint32_t)(key >> 32);
     }
-  } else if (n > 0) {
-    for (int i = tid; i < n; i += kThreads) L.cand[i] = cand_key_of(c, L.cand[i]);
-    __syncthreads();
-    const int parts = n <= kThreads / 2 ? kThreads / n : 1;
-    if (parts > 1) {
-      const int i = tid % n, part = tid / n;
-      if (part < parts) {
-        const uint64_t key = L.cand[i];
-        const int j0 = (n * part) / parts, j1 = (n * (part + 1)) / parts;
-        int r = 0;
-        for (int j = j0; j < j1; ++j) r += L.cand[j] > key ? 1 : 0;
-        if (r) atomicAdd(&L.racc[i], r);
+    if (w >= kTopkHead) {
+      const int p = (w - kTopkHead) >> 1;
+      if (p >= npub) return 0u;
+      const uint64_t key = mine[p];
+      return (w - kTopkHead) & 1 ? (uint32_t)key : (uint32_t)(key >> 32);
+    }
+    const uint64_t zb = __builtin_bit_cast(uint64_t, zsum);
+    switch (w) {
+      case kHMax: return __float_as_uint(smax);
+      case kHZHi: return (uint32_t)(zb >> 32);
+      case kHZLo: return (uint32_t)zb;
+      case kHNpub: return (uint32_t)npub;
+      case kHFlags: return sflags;
+      case kHNinf: return (uint32_t)sninf;
+      case kHRMax: return LP ? __float_as_uint(rsmax) : 0u;
+      case kHRZ: return LP ? __float_as_uint((float)rzs) : 0u;
+      default: return 0u;
+    }
+  };
+  uint64_t* const pub = T.pub + ((size_t)row * kMaxSlices + slice) * kTopkWords;
+  // (LP with raw keys) the slice's payload, which the draw needs, goes out
+  // before its raw keys are ranked; with keep bytes requested it waits for
+  // them (the finalizer marks kept tokens once every slice cleared its range)
+  const bool early = LP && LPo.k > 0 && !P.keep;
+
+  // ---------------------------------------------------------- raw top-k (LP)
+  // The slice's best LPo.k raw keys: the tokens at or above the LPo.k-th
+  // largest raw thread maximum (gated by the raw quad maxima); a slice with
+  // +inf, or whose threshold leaves too few or too many, takes the exact
+  // select over memory.
+  if constexpr (LP) {
+    const int Kr = LPo.k;
+    if (Kr > 0) {
+      const bool rfin = (sflags & kFRawPosInf) == 0u;
+      const float tr = rfin ? rtau : kNegInf;
+      if (tr > kNegInf) {
+        // the quads whose raw maximum reaches tr are staged in LDS (the
+        // thread's qualifying quads, one slot range a wave: a scan of the
+        // counts and one LDS atomic), while wave 0 may still be sorting the
+        // slice's keys; then all threads scan the staged elements
+        uint32_t qsel = 0u;
+#pragma unroll
+        for (int g = 0; g < Q; ++g) {
+          const uint32_t w = rqp[g / 2];
+          const float rq = __uint_as_float(g & 1 ? w & 0xffff0000u : w << 16);
+          qsel |= (g < nq && rq >= tr ? 1u : 0u) << g;
+        }
+        const uint32_t qc = (uint32_t)__builtin_popcount(qsel);
+        const uint32_t qi = wave_incl_scan(qc);
+        const uint32_t qt = read_lane(qi, 63);
+        int qb = 0;
+        if (l == 0 && qt) qb = atomicAdd(&L.nstage, (int)qt);
+        int slot = read_lane(qb, 0) + (int)(qi - qc);
+#pragma unroll
+        for (int g = 0; g < Q; ++g) {
+          if ((qsel >> g) & 1u) {
+            if (slot < kRStageCap) {
+              const uint4 qv = quad_get(S.bank[g / kQuadsPerBank], g % kQuadsPerBank);
+              L.rstage[4 * slot] = qv.x;
+              L.rstage[4 * slot + 1] = qv.y;
+              L.rstage[4 * slot + 2] = qv.z;
+              L.rstage[4 * slot + 3] = qv.w;
+              L.rstage_at[slot] = base32 + (tid + g * kThreads) * N;
+            }
+            ++slot;
+          }
+        }
       }
-      __syncthreads();
-      for (int i2 = tid; i2 < n; i2 += kThreads) {
-        const int r = L.racc[i2];
-        if (r < npub) mine[r] = L.cand[i2];
+      __syncthreads();  // staged (and the slice's keys are sorted)
+      if (early && L.last == 0 && tid < kTopkWordsBase)
+        st_coherent(&pub[tid], ((uint64_t)L.tag << 32) | word(tid));
+      int nr = 0;
+      if (tr > kNegInf) {
+        const int ns = L.nstage;
+        if (ns <= kRStageCap) {
+          for (int j = tid; j < ns * N; j += kThreads) {
+            const int q = j / N, e = j - q * N;
+            const uint32_t w = L.rstage[4 * q + e * 4 / N];
+            float x;
+            if constexpr (DT == LSAMP_DTYPE_F32)
+              x = __uint_as_float(w);
+            else if constexpr (DT == LSAMP_DTYPE_BF16)
+              x = __uint_as_float((e & 1) ? w & 0xffff0000u : w << 16);
+            else
+              x = half_bits_to_f32((e & 1) ? w >> 16 : w & 0xffffu);
+            const int32_t id = L.rstage_at[q] + e;
+            const bool hit = x >= tr && id < end32;
+            const int cs = wave_append(hit, &L.nrcand);
+            if (hit && cs < kRCandCap) L.rcand[cs] = raw_cand(x, id);
+          }
+        }
+        __syncthreads();
+        nr = ns <= kRStageCap ? L.nrcand : kRCandCap + 1;
       }
-    } else {
-      for (int i = tid; i < n; i += kThreads) {
-        const uint64_t key = L.cand[i];
-        int r = 0;
-        for (int j = 0; j < n; ++j) r += L.cand[j] > key ? 1 : 0;
-        if (r < npub) mine[r] = key;
+      if (nr < Kr || nr > kRCandCap) {
+        __syncthreads();  // every thread has read the counts
+        nr = raw_select_mem<DT>(rowp, base32, end32, Kr, L.rcand, &L.nrcand, L);
       }
+      // the slice's best min(k, n) raw keys in order (the comparisons split
+      // over every thread: a wave alone is a long dependent chain)
+      nraw = nr < Kr ? nr : Kr;
+      sort_into(nr, nraw, L.rbest + slice * kTopkMaxLp, [](uint64_t r) { return raw_key_of(r); },
+                L.rcand, L.rracc, true);
     }
   }
 
   // ---------------------------------------------------------- parity outputs
   if (P.processed) {
     float* out = P.processed + (size_t)row * (size_t)V;
-    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+    for_quads(S, nq, [&](int g, uint4& vq) -> bool {
       const int32_t i0 = base32 + (tid + g * kThreads) * N;
       if (i0 >= end32) return false;
+      uint4 v = vq;
+      if constexpr (LP) exclude_elems<DT>(v, exb.get(g));
       const int32_t li0 = i0 - base32;
       const uint32_t pen = (L.pen[li0 >> 5] >> (uint32_t)(li0 & 31)) & FULL;
 #pragma unroll
@@ -676,8 +1039,10 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     // finalizer marks the kept tokens after every slice has cleared its range
     uint8_t* kr = P.keep + (size_t)row * (size_t)V;
     const bool inf_keep = posinf && c.kind == LSAMP_KIND_FILTERED && !bad_row;
-    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+    for_quads(S, nq, [&](int g, uint4& vq) -> bool {
       const int32_t i0 = base32 + (tid + g * kThreads) * N;
+      uint4 v = vq;
+      if constexpr (LP) exclude_elems<DT>(v, exb.get(g));
 #pragma unroll
       for (int e = 0; e < N; ++e)
         if (i0 + e < end32) kr[i0 + e] = (inf_keep && vec_elem<DT>(v, e) == kPosInf) ? 1 : 0;
@@ -691,38 +1056,14 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   }
 
   // ---------------------------------------------------------- H: publish
-  if (tid == 0) {
-    L.tag = epoch + 1u;
-    L.last = ticket + 1u == (uint32_t)G ? 1 : 0;
-  }
   __syncthreads();
   const uint32_t tag = L.tag;
   const bool last = L.last != 0;
-  uint64_t zs = 0ull;
-#pragma unroll
-  for (int i = 0; i < kWaves; ++i) zs += L.redz[i];
-  const double zsum = (double)zs * 0x1p-40;
-  auto word = [&](int w) -> uint32_t {
-    if (w >= kTopkHead) {
-      const int p = (w - kTopkHead) >> 1;
-      if (p >= npub) return 0u;
-      const uint64_t key = mine[p];
-      return (w - kTopkHead) & 1 ? (uint32_t)key : (uint32_t)(key >> 32);
-    }
-    const uint64_t zb = __builtin_bit_cast(uint64_t, zsum);
-    switch (w) {
-      case kHMax: return __float_as_uint(smax);
-      case kHZHi: return (uint32_t)(zb >> 32);
-      case kHZLo: return (uint32_t)zb;
-      case kHNpub: return (uint32_t)npub;
-      case kHFlags: return sflags;
-      case kHNinf: return (uint32_t)sninf;
-      default: return 0u;
-    }
-  };
   if (!last) {
-    uint64_t* pub = T.pub + ((size_t)row * kMaxSlices + slice) * kTopkWords;
-    if (tid < kTopkWords) st_coherent(&pub[tid], ((uint64_t)tag << 32) | word(tid));
+    // the payload (unless it went out early) and the raw keys
+    const int w0 = early ? kTopkWordsBase : 0;
+    const int w1 = LP && LPo.k > 0 ? kTopkWordsBase + 2 * nraw : kTopkWordsBase;
+    if (tid >= w0 && tid < w1) st_coherent(&pub[tid], ((uint64_t)tag << 32) | word(tid));
     return;
   }
 
@@ -743,11 +1084,13 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
       case kHNpub: L.hnpub[slice] = (int32_t)w; break;
       case kHFlags: L.hflags[slice] = w; break;
       case kHNinf: L.hninf[slice] = (int32_t)w; break;
+      case kHRMax: L.hrmax[slice] = __uint_as_float(w); break;
+      case kHRZ: L.hrz[slice] = __uint_as_float(w); break;
       default: break;
     }
   }
   if (tid == 0) L.hz[slice] = zsum;
-  if (tid < kTopkWords) {
+  if (tid < kTopkWordsBase) {
     // every slice's word in one round trip, then only the missing ones again
     const uint64_t* pub0 = T.pub + (size_t)row * kMaxSlices * kTopkWords + tid;
     uint64_t w8[kMaxSlices];
@@ -783,11 +1126,16 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
       } else if (tid == kHZLo) {
         reinterpret_cast<uint32_t*>(&L.hz[s])[0] = d;
       } else if (tid == kHNpub) {
-        L.hnpub[s] = (int32_t)d;
+        // (clamped: a slice given up on leaves an old word)
+        L.hnpub[s] = d < (uint32_t)kTopkMaxK ? (int32_t)d : kTopkMaxK;
       } else if (tid == kHFlags) {
         L.hflags[s] = d;
       } else if (tid == kHNinf) {
         L.hninf[s] = (int32_t)d;
+      } else if (LP && tid == kHRMax) {
+        L.hrmax[s] = __uint_as_float(d);
+      } else if (LP && tid == kHRZ) {
+        L.hrz[s] = __uint_as_float(d);
       }
     }
   }
@@ -812,6 +1160,112 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     total += npub_s[s];
     ninf_row += in ? L.hninf[s] : 0;
   }
+  // (LP) The row's raw log-sum-exp from the slices' raw headers (NaN when a
+  // logit is NaN, +inf when one is +inf, -inf when all are -inf); every
+  // thread computes it.
+  double lse = 0.0;
+  if constexpr (LP) {
+    float mx = kNegInf;
+    uint32_t rf = 0u;
+#pragma unroll
+    for (int s = 0; s < kMaxSlices; ++s) {
+      const bool in = s < G;
+      rf |= in ? L.hflags[s] : 0u;
+      mx = __builtin_fmaxf(mx, in ? L.hrmax[s] : kNegInf);
+    }
+    if (rf & kFRawNaN) {
+      lse = __builtin_nan("");
+    } else if (rf & kFRawPosInf) {
+      lse = __builtin_huge_val();
+    } else if (mx == kNegInf) {
+      lse = -__builtin_huge_val();
+    } else {
+      double z = 0.0;
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) {
+        const float hx = L.hrmax[s];
+        z += (s < G && hx > kNegInf)
+                 ? (double)L.hrz[s] * (double)__builtin_amdgcn_exp2f((hx - mx) * kLog2e)
+                 : 0.0;
+      }
+      lse = (double)mx + (double)__builtin_logf((float)z);
+    }
+  }
+  // (LP) The raw keys, by waves 1..4 once the row's keys are merged, while
+  // wave 0 draws: each of those waves reads every other slice's raw list
+  // (lane l polls word l; each slice lists min(k, its length) keys, sorted;
+  // the waves store the same values), then each lane ranks the key of one
+  // list slot by counting the keys above it; the ranks below k write their
+  // outputs.  A list given up on (bounded
+  // polls) leaves the row's raw outputs NaN / -1 and raises the sticky
+  // status bit.
+  auto raw_merge = [&]() {
+    const int Kr = LPo.k;
+    if (Kr > 0 && wv >= 1 && wv <= kMaxSlices * kTopkMaxLp / 64) {
+      int nr_s[kMaxSlices];
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) {
+        const int64_t len = s == G - 1 ? V - (int64_t)s * P.slice_len : (int64_t)P.slice_len;
+        nr_s[s] = s < G ? (len < Kr ? (int)len : Kr) : 0;
+      }
+      const uint64_t* praw = T.pub + (size_t)row * kMaxSlices * kTopkWords + kTopkWordsBase + l;
+      uint64_t w8[kMaxSlices];
+      bool want[kMaxSlices];
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) {
+        want[s] = s < G && s != slice && l < 2 * nr_s[s];
+        w8[s] = want[s] ? ld_coherent(praw + s * kTopkWords) : ((uint64_t)tag << 32);
+      }
+      const int lim = spin_test > 0 ? spin_test : kSpin;
+      bool rlost = false;
+      for (int it = 0;; ++it) {
+        bool all = spin_test <= 0;
+#pragma unroll
+        for (int s = 0; s < kMaxSlices; ++s) all = all && (uint32_t)(w8[s] >> 32) == tag;
+        if (all) break;
+        if (it >= lim) {
+          rlost = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int s = 0; s < kMaxSlices; ++s)
+          if ((uint32_t)(w8[s] >> 32) != tag) w8[s] = ld_coherent(praw + s * kTopkWords);
+      }
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) {
+        if (want[s]) {
+          uint32_t* half = reinterpret_cast<uint32_t*>(&L.rbest[s * kTopkMaxLp + (l >> 1)]);
+          half[l & 1 ? 0 : 1] = (uint32_t)w8[s];
+        }
+      }
+      const bool gone = __ballot(rlost) != 0ull || L.lost != 0;
+      if (gone && wv == 1 && l == 0) atomicOr(T.status, kStatusSpinTimeout);
+      __builtin_amdgcn_wave_barrier();
+      // this lane's list slot j, ranked by counting the keys above it in
+      // every list (broadcast reads, eight at a time)
+      const int j = (wv - 1) * 64 + l, sj = j / kTopkMaxLp, pj = j - sj * kTopkMaxLp;
+      if (sj < G && pj < nr_s[sj]) {
+        const uint64_t key = L.rbest[j];
+        int r = 0;
+        for (int s2 = 0; s2 < G; ++s2) {
+          const uint64_t* lst = L.rbest + s2 * kTopkMaxLp;
+          for (int p0 = 0; p0 < nr_s[s2]; p0 += 8) {
+            uint64_t kj[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) kj[q] = lst[p0 + q];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) r += (p0 + q < nr_s[s2] && kj[q] > key) ? 1 : 0;
+          }
+        }
+        if (r < Kr) {
+          const size_t o = (size_t)row * (size_t)Kr + (size_t)r;
+          LPo.ids[o] = gone ? -1 : key_id(key);
+          LPo.values[o] = gone ? __builtin_nanf("") : (float)((double)key_y(key) - lse);
+        }
+      }
+    }
+  };
   // The row's best keys in order, in L.merged.  At most 64 keys in all
   // (every slice's list short, as min-p makes them): one wave ranks them.
   // More: each slice's wave counts, for each of its keys, the keys above it
@@ -819,6 +1273,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   static_assert(kTopkMaxK == 64, "one wave per slice list");
   if (total <= 64) {
     if (tid >= 64) {
+      if constexpr (LP) raw_merge();
       if (tid == 64) {
         gmem(T.ticket)[row] = 0u;
         gmem(T.epoch)[row] = tag;
@@ -868,6 +1323,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     }
     __syncthreads();
     if (tid >= 64) {
+      if constexpr (LP) raw_merge();
       if (tid == 64) {
         gmem(T.ticket)[row] = 0u;
         gmem(T.epoch)[row] = tag;
@@ -897,6 +1353,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   uint8_t* kr = P.keep ? P.keep + (size_t)row * (size_t)V : nullptr;
 
   int32_t token = -1;
+  float cx = 0.0f;      // (LP) the chosen token's raw logit
+  bool cx_ok = false;
   uint64_t W = 0ull, probe_w = 0ull;
   int32_t kept_c = 0;
   float cmin = kPosInf;
@@ -946,6 +1404,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     const uint64_t key = in ? L.merged[l] : 0ull;
     const float y = key_y(key);
     const int32_t id = key_id(key);
+    // (LP) each listed token's raw logit, requested now, read after the draw
+    const float rawx = LP && in ? load_scalar<DT>(rowp, id) : 0.0f;
     const double P_lim = top_p_limit(P, c, prm, z);
     const bool p_on = P_lim >= 0.0;
     const int32_t k_lim = c.kind == LSAMP_KIND_ARGMAX ? 1 : prm.top_k;
@@ -987,6 +1447,13 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     const uint64_t target = W ? scaled_target(uniform_u32(u), W) : 0ull;
     const uint64_t hm = __ballot(wo != 0ull && cum > target && cum - wo <= target);
     token = hm ? read_lane(io, __builtin_ctzll(hm)) : -1;
+    if constexpr (LP) {
+      const uint64_t hc = __ballot(in && id == token);
+      if (hc) {
+        cx = read_lane(rawx, __builtin_ctzll(hc));
+        cx_ok = true;
+      }
+    }
     const uint64_t hp = __ballot(keep && probe >= 0 && id == probe);
     probe_w = hp ? read_lane(w, __builtin_ctzll(hp)) : 0ull;
     if (P.stats) {
@@ -996,6 +1463,11 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     }
     if (kr && in && keep) kr[id] = 1;
     if (token < 0 || W == 0ull) flags |= LSAMP_ROW_EMPTY;
+  }
+  if constexpr (LP) {
+    if (token >= 0 && !cx_ok) cx = load_scalar<DT>(rowp, token);
+    if (l == 0)
+      LPo.chosen[row] = token >= 0 ? (float)((double)cx - lse) : __builtin_nanf("");
   }
   if (l == 0) {
     if (lost) atomicOr(T.status, kStatusSpinTimeout);
@@ -1019,8 +1491,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   }
 }
 
-template <int DT>
-__global__ __launch_bounds__(kThreads) void k_topk(SamplePlan Pk, TopkWs Tk) {
+template <int DT, bool LP>
+__global__ __launch_bounds__(kThreads) void k_topk(SamplePlan Pk, TopkWs Tk, TopkLp Lk) {
   __shared__ TopkLds L;
   const SamplePlan& P = Pk;
   const TopkWs& T = Tk;
@@ -1029,17 +1501,29 @@ __global__ __launch_bounds__(kThreads) void k_topk(SamplePlan Pk, TopkWs Tk) {
   const int loc = b >> 3;
   const int row = (b & 7) + 8 * (loc / P.slices);
   const int slice = loc % P.slices;
-  if (row < P.rows) topk_task<DT>(P, T, row, slice, L);
+  if (row < P.rows) topk_task<DT, LP>(P, T, Lk, row, slice, L);
 }
 
 template <int DT>
-int launch_topk_dt(const SamplePlan& P, const TopkWs& T, hipStream_t st, void* const* events) {
+int launch_topk_dt(const SamplePlan& P, const TopkWs& T, const TopkLp& lp, hipStream_t st,
+                   void* const* events) {
   auto mark = [&](int i) {
     if (events) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), st);
   };
   const int rows8 = (P.rows + 7) / 8 * 8;
+  const dim3 grid((unsigned)(rows8 * P.slices));
   mark(0);
-  hipLaunchKernelGGL(k_topk<DT>, dim3((unsigned)(rows8 * P.slices)), dim3(kThreads), 0, st, P, T);
+  // (raw log-probabilities in the same pass for 16-bit logits only: the fp32
+  // slab leaves no registers for them, and lsamp_step then ranks the raw
+  // logits in a second pass)
+  if constexpr (DT != LSAMP_DTYPE_F32) {
+    if (lp.k >= 0)
+      hipLaunchKernelGGL((k_topk<DT, true>), grid, dim3(kThreads), 0, st, P, T, lp);
+    else
+      hipLaunchKernelGGL((k_topk<DT, false>), grid, dim3(kThreads), 0, st, P, T, lp);
+  } else {
+    hipLaunchKernelGGL((k_topk<DT, false>), grid, dim3(kThreads), 0, st, P, T, lp);
+  }
   mark(1);
   mark(2);
   return (int)hipGetLastError();
@@ -1048,18 +1532,21 @@ int launch_topk_dt(const SamplePlan& P, const TopkWs& T, hipStream_t st, void* c
 template <int DT>
 int topk_blocks_dt() {
   int n = 0;
-  return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_topk<DT>, kThreads, 0) == hipSuccess ? n
-                                                                                                   : 0;
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_topk<DT, false>, kThreads, 0) ==
+                 hipSuccess
+             ? n
+             : 0;
 }
 
 }  // namespace
 
-int launch_topk(const SamplePlan& P, const TopkWs& T, void* stream, void* const* events) {
+int launch_topk(const SamplePlan& P, const TopkWs& T, const TopkLp& lp, void* stream,
+                void* const* events) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (P.dtype) {
-    case LSAMP_DTYPE_F32: return launch_topk_dt<LSAMP_DTYPE_F32>(P, T, st, events);
-    case LSAMP_DTYPE_BF16: return launch_topk_dt<LSAMP_DTYPE_BF16>(P, T, st, events);
-    default: return launch_topk_dt<LSAMP_DTYPE_F16>(P, T, st, events);
+    case LSAMP_DTYPE_F32: return launch_topk_dt<LSAMP_DTYPE_F32>(P, T, lp, st, events);
+    case LSAMP_DTYPE_BF16: return launch_topk_dt<LSAMP_DTYPE_BF16>(P, T, lp, st, events);
+    default: return launch_topk_dt<LSAMP_DTYPE_F16>(P, T, lp, st, events);
   }
 }
 

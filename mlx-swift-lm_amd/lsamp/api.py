@@ -479,9 +479,12 @@ class PreparedStep:
     """A fully bound lsamp_step call (draw -> commit -> log-probabilities)."""
 
     def __init__(self, ctx: Context, logits, params, *, table, uniforms, philox_keys,
-                 logprobs_top_k, **sample_kw):
+                 logprobs_top_k, draw_from_table: bool = True, **sample_kw):
+        """`draw_from_table` False: the draw reads the penalty entries given
+        in `sample_kw` (row_ptr / entries) and only the commit goes to `table`."""
         self.ctx = ctx
-        self.sample = ctx.prepare_sample(logits, params, semantics=_ffi.SEM_CBV2, table=table,
+        self.sample = ctx.prepare_sample(logits, params, semantics=_ffi.SEM_CBV2,
+                                         table=table if draw_from_table else None,
                                          uniforms=uniforms, philox_keys=philox_keys, **sample_kw)
         rows = logits.shape[0]
         dev = logits.device

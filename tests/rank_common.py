@@ -81,7 +81,9 @@ def close_logprobs(a, b, tol=LOGPROB_TOL):
     fin = np.isfinite(a) & np.isfinite(b)
     same_nonfinite = (~np.isfinite(a)) & (~np.isfinite(b)) & (
         (np.isnan(a) & np.isnan(b)) | (a == b))
-    return bool(np.all(same_nonfinite | (fin & (np.abs(a - b) <= tol))))
+    with np.errstate(invalid="ignore"):  # (inf - inf where both are non-finite)
+        near = fin & (np.abs(a - b) <= tol)
+    return bool(np.all(same_nonfinite | near))
 
 
 def torch_view(storage, dtype, rows, vocab, row_stride, col_stride, offset=0, device="cuda"):

@@ -3,15 +3,23 @@
 penalty table, and the raw log-probabilities of the drawn tokens and the top
 k, against the same three steps made by separate calls with the penalty
 entries rebuilt on the host, and replayed from a HIP graph.
+
+When the draw runs the one-pass top-k kernel (16-bit logits, CBv2 top-k
+rows), that kernel ranks the raw logits in the same pass (launch kind 3);
+its log-probabilities are checked against the oracle's raw ranking
+(LogitsPipelineV2.process :307-314, CBv2Logprobs.gather :534-549) and against
+lsamp_logprobs: ids identical, values within the log-probability tolerance.
 """
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
+import oracle as O
 from lsamp import _ffi
 from lsamp import workloads as W
 from lsamp.history import Cbv2RowState, csr
+from rank_common import BF16, F16, close_logprobs, to_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -56,15 +64,17 @@ def test_step_equals_separate_calls(ctx):
     for step in range(6):
         u = rng.random(rows, dtype=np.float32)
         out = ctx.step(lt, params, table=table, uniforms=u, logprobs_top_k=5)
+        # (the step's draw ranked the raw logits in its own pass)
+        assert ctx.last_launch()["fused"] == 3
         rp, en = csr([h.entries() for h in host])
         ref = ctx.sample(lt, params, semantics=_ffi.SEM_CBV2, row_ptr=rp, entries=en, uniforms=u)
         lp = ctx.logprobs(lt, tokens=ref["tokens"], top_k=5)
         torch.cuda.synchronize()
         tok = out["tokens"].cpu().numpy()
         assert np.array_equal(tok, ref["tokens"].cpu().numpy()), f"step {step}"
-        assert np.array_equal(out["chosen"].cpu().numpy(), lp["chosen"].cpu().numpy())
+        assert close_logprobs(out["chosen"].cpu().numpy(), lp["chosen"].cpu().numpy())
         assert np.array_equal(out["top_ids"].cpu().numpy(), lp["top_ids"].cpu().numpy())
-        assert np.array_equal(out["top_values"].cpu().numpy(), lp["top_values"].cpu().numpy())
+        assert close_logprobs(out["top_values"].cpu().numpy(), lp["top_values"].cpu().numpy())
         assert not out["commit_flags"].cpu().numpy().any()
         for r in range(rows):
             host[r].commit(int(tok[r]))
@@ -103,3 +113,77 @@ def test_step_replays_from_a_graph(ctx):
     ra, rb = eager_t.host_rows(), graph_t.host_rows()
     for r in range(rows):
         assert ra[r][0].tolist() == rb[r][0].tolist()
+
+
+NAN, INF = float("nan"), float("inf")
+
+
+def special_rows(x, rng):
+    """Rows 1..8 of a batch get the raw ranking's edge cases."""
+    V = x.shape[1]
+    x[1, rng.choice(V, 5, replace=False)] = NAN            # NaN: log-sum-exp NaN
+    x[2, rng.choice(V, 3, replace=False)] = INF            # +inf: log-sum-exp +inf
+    x[3].fill(-INF)                                         # all -inf but two
+    x[3, rng.choice(V, 2, replace=False)] = -3.0
+    x[4].fill(1.5)                                          # every token tied
+    x[5, [7, V // 2, V - 1]] = 50.0                         # ties across slices
+    x[6].fill(NAN)                                          # all NaN (an EMPTY draw)
+    np.minimum(x[7], 0.0, out=x[7])                         # signed zeros
+    x[7, rng.choice(V, 40, replace=False)] = -0.0
+    x[8, :V // 3] += 40.0                                   # one slice holds the top
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("vocab,k", [(151936, 0), (151936, 1), (151936, 20), (151936, 32),
+                                     (40003, 20), (1001, 32)])
+def test_step_logprobs_in_the_sampling_pass(ctx, dtype, vocab, k):
+    """The top-k kernel's raw log-probabilities (launch kind 3) against the
+    oracle's raw ranking and lsamp_logprobs: the raw logits before penalties,
+    the grammar mask and the temperature; NaN, +inf, all -inf, tied, signed
+    zero rows; rows that are not 16-byte aligned (odd vocabularies)."""
+    import torch
+    from lsamp.api import PenaltyTable
+    rng = np.random.default_rng(vocab + 7 * k + dtype)
+    rows = 12
+    x = rng.normal(0.0, 3.0, (rows, vocab)).astype(np.float32)
+    special_rows(x, rng)
+    bits = to_bits(x, dtype)
+    tdt = torch.bfloat16 if dtype == BF16 else torch.float16
+    lt = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(tdt).cuda()
+    p = W.resolve_cbv2(temperature=0.8, top_k=50, top_p=0.95, min_p=0.05, presence_penalty=0.5,
+                       frequency_penalty=0.3, repetition_penalty=1.2, repetition_context_size=8,
+                       vocab=vocab)
+    params = W._params([p] * rows)
+    prompts = [rng.integers(0, vocab, 30).tolist() for _ in range(rows)]
+    table = PenaltyTable(states_v(prompts, vocab), capacity=256, window_capacity=8)
+    # a grammar mask on the even rows (the raw log-probabilities ignore it)
+    words = (vocab + 31) // 32
+    mask = np.full((rows, words), 0xFFFFFFFF, np.uint32)
+    mask[::2] = rng.integers(0, 1 << 32, (rows // 2 + rows % 2, words), dtype=np.uint64).astype(np.uint32)
+    u = rng.random(rows, dtype=np.float32)
+    out = ctx.step(lt, params, table=table, uniforms=u, logprobs_top_k=k, bitmask=mask,
+                   mask_bits=vocab)
+    torch.cuda.synchronize()
+    assert ctx.last_launch()["fused"] == 3
+    tok = out["tokens"].cpu().numpy()
+    assert (tok[6] == -1), "an all-NaN row draws nothing"
+    ref = O.rank(np.ascontiguousarray(bits).reshape(-1), dtype=dtype, k=k, raw_values=False,
+                 rows=rows, vocab=vocab, row_stride=vocab, col_stride=1, tokens=tok)
+    if k:
+        ids = out["top_ids"].cpu().numpy()
+        bad = np.nonzero((ids != ref["ids"]).any(axis=1))[0]
+        assert bad.size == 0, f"ids differ in rows {bad}: {ids[bad[:2]]} vs {ref['ids'][bad[:2]]}"
+        assert close_logprobs(out["top_values"].cpu().numpy(), ref["values"])
+    assert close_logprobs(out["chosen"].cpu().numpy(), ref["chosen"])
+    # and the second-pass entry point on the same tokens agrees
+    lp = ctx.logprobs(lt, tokens=out["tokens"], top_k=k)
+    torch.cuda.synchronize()
+    if k:
+        assert np.array_equal(out["top_ids"].cpu().numpy(), lp["top_ids"].cpu().numpy())
+        assert close_logprobs(out["top_values"].cpu().numpy(), lp["top_values"].cpu().numpy())
+    assert close_logprobs(out["chosen"].cpu().numpy(), lp["chosen"].cpu().numpy())
+
+
+def states_v(prompts, vocab):
+    return [Cbv2RowState(pr, [], 8, repetition_on=True, counts_on=True, vocab=vocab)
+            for pr in prompts]
