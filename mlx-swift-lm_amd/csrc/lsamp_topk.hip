@@ -504,16 +504,27 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
         zr = __builtin_ldexpf(zr, (int)__builtin_fmaxf(nn - nbr, -512.0f));
         nbr = nn;
       }
+      float t[N];
 #pragma unroll
       for (int e = 0; e < N; ++e)
-        zr += __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(vr, e), kLog2e, nbr));
+        t[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(vr, e), kLog2e, nbr));
+#pragma unroll
+      for (int w = 1; w < N; w *= 2)
+#pragma unroll
+        for (int e = 0; e < N; e += 2 * w) t[e] += t[e + w];
+      zr += t[0];
     }
-    uint4 v = vin;
+    // (the registers are masked in place, unless LP keeps them raw)
+    uint4 vcopy = vin;
+    uint4& v = LP ? vcopy : vin;
     if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
     if constexpr (N == 8) {
       constexpr uint32_t M = 0x7fff7fffu;
       const uint32_t hw = pk_max_u16(pk_max_u16(v.x & M, v.y & M), pk_max_u16(v.z & M, v.w & M));
       rawhi = pk_max_u16(rawhi, hw);
+      // (the raw magnitudes are taken before the words are overwritten: with
+      // the order left open the compiler keeps a copy of the quad)
+      asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w) : "v"(rawhi));
     } else {
       const uint32_t probe = nonfinite_probe<DT>(v);
       nf_acc |= probe;
@@ -529,7 +540,17 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
       }
     }
     exclude_elems<DT>(v, ex);
-    float qm = vec_max_nn<DT>(v);
+    // the quad's elements, unpacked once for its maximum and its exp-sum
+    float f[N];
+#pragma unroll
+    for (int e = 0; e < N; ++e) f[e] = vec_elem<DT>(v, e);
+    auto fmax_of = [&]() {
+      float m = f[0];
+#pragma unroll
+      for (int e = 1; e < N; ++e) m = __builtin_elementwise_maximum(m, f[e]);
+      return m;
+    };
+    float qm = fmax_of();
     if constexpr (N == 8) {
       // a NaN (the maximum propagates it) or +inf in the quad: NaNs out,
       // +inf tokens counted (rare)
@@ -537,13 +558,14 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
         uint32_t nan = 0u;
 #pragma unroll
         for (int e = 0; e < N; ++e) {
-          const float x = vec_elem<DT>(v, e);
-          nan |= (x != x ? 1u : 0u) << e;
-          ninf += x == kPosInf ? 1 : 0;
+          nan |= (f[e] != f[e] ? 1u : 0u) << e;
+          ninf += f[e] == kPosInf ? 1 : 0;
         }
         exclude_elems<DT>(v, nan);
         ex |= nan;
-        qm = vec_max_nn<DT>(v);
+#pragma unroll
+        for (int e = 0; e < N; ++e) f[e] = vec_elem<DT>(v, e);
+        qm = fmax_of();
         nf_acc = 0x80008000u;
       }
     } else {
@@ -563,16 +585,21 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
         zt = __builtin_ldexpf(zt, (int)__builtin_fmaxf(nn - nbz, -512.0f));
         nbz = nn;
       }
+      // (a pairwise sum per quad: one dependent add a quad on zt)
+      float t[N];
 #pragma unroll
-      for (int e = 0; e < N; ++e)
-        zt += __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(v, e), lgz, nbz));
+      for (int e = 0; e < N; ++e) t[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(f[e], lgz, nbz));
+#pragma unroll
+      for (int w = 1; w < N; w *= 2)
+#pragma unroll
+        for (int e = 0; e < N; e += 2 * w) t[e] += t[e + w];
+      zt += t[0];
     }
     if constexpr (LP) {
       exb.set(g, ex);
       return false;  // the registers keep the raw logits
     } else {
-      vin = v;
-      return true;
+      return true;   // (masked in place)
     }
   });
   if constexpr (N == 8) {
