@@ -939,6 +939,7 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   Q.tokens = a->tokens;
   Q.accept_mask = a->accept_mask;
   Q.penalized = penalized ? 1 : 0;
+  Q.parts = a->mode == LSAMP_VERIFY_RESIDUAL ? (int32_t)verify_parts((size_t)a->vocab) : 1;
   DeviceGuard guard(ctx->device);
   int err = penalized ? launch_window_entries(E, stream) : 0;
   if (err == 0) err = launch_sample(ctx->ws, P, stream, nullptr);

@@ -33,6 +33,11 @@ constexpr int kMassFracBits = 29;
 // Candidates (tokens in the cut bin) per row, and per work-group in LDS.
 constexpr int kCandCap = 4096;
 constexpr int kWgCandCap = 2048;
+// MTP verify residual draw: a work-group covers a part of kVerifyPart tokens
+// of the rejected position's rows, a wave kVerifySpan of them.
+constexpr int kVerifySpan = 2048;
+constexpr int kVerifyPart = kWaves * kVerifySpan;  // 16,384
+static_assert(kVerifySpan <= 65536, "queue entries are 16-bit offsets");
 // Short-list rows (argmax, or top-k <= kShortMaxK): each slice lists the
 // tokens at or above a threshold taken from its threads' maxima (the quads
 // holding them staged whole in LDS, at most kQStage per thread) and
@@ -146,10 +151,17 @@ struct RankSlice {
   int32_t pad;
 };
 
+// A part's sums of the residual draw's two weights.
+struct VerifyPart {
+  uint64_t res;  // max(0, p_t - p_d) at 2^-52
+  uint64_t tgt;  // the target's kept weight
+};
+
 struct Workspace {
   int32_t max_rows;
   int32_t max_vocab;
   int32_t max_chunks;
+  int32_t max_parts;        // verify parts per sequence (kVerifyPart tokens each)
   SliceSummary* summaries;  // [max_rows][kMaxSlices]
   RowInfo* rows;            // [max_rows]
   uint64_t* chunk_w;        // [max_rows][max_chunks]
@@ -164,6 +176,8 @@ struct Workspace {
   lsamp_row_stats* vstats;  // [max_rows]
   int32_t* vtokens;         // [max_rows]
   uint32_t* vflags;         // [max_rows]
+  VerifyPart* vpart;        // [max_rows][max_parts] per sequence
+  uint32_t* vticket;        // [max_rows] per sequence: parts done (zeroed range)
 };
 
 // The one-pass top-k kernel (lsamp_topk.hip) takes steps whose rows are all
@@ -195,11 +209,12 @@ struct TopkWs {
 // the one range [zero_begin, zero_end); the kernels return them to zero at
 // the end of every step.
 struct WorkspaceLayout {
-  size_t sum, rows, chunk, cand, klist, part, status, cc, as, asel, tticket;
-  size_t vstats, vtok, vfl, rpart, arank, vrp, vrl, smask, tpub, tepoch;
+  size_t sum, rows, chunk, cand, klist, part, status, cc, as, asel, tticket, vtick;
+  size_t vstats, vtok, vfl, vpart, rpart, arank, vrp, vrl, smask, tpub, tepoch;
   size_t zero_begin, zero_end, total;
 };
 constexpr size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+constexpr size_t verify_parts(size_t vocab) { return (vocab + kVerifyPart - 1) / kVerifyPart; }
 constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
   const size_t chunks = (max_vocab + kChunk - 1) / kChunk;
   const size_t words = (max_vocab + 31) / 32;
@@ -217,10 +232,12 @@ constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
   L.as = off;     off = align256(off + R * sizeof(uint32_t));
   L.asel = off;   off = align256(off + R * sizeof(uint32_t));
   L.tticket = off; off = align256(off + R * sizeof(uint32_t));
+  L.vtick = off;  off = align256(off + R * sizeof(uint32_t));
   L.zero_end = off;
   L.vstats = off; off = align256(off + R * sizeof(lsamp_row_stats));
   L.vtok = off;   off = align256(off + R * sizeof(int32_t));
   L.vfl = off;    off = align256(off + R * sizeof(uint32_t));
+  L.vpart = off;  off = align256(off + R * verify_parts(max_vocab) * sizeof(VerifyPart));
   L.rpart = off;  off = align256(off + R * kRankMaxSlices * sizeof(RankSlice));
   L.arank = off;  off = align256(off + R * sizeof(uint32_t));
   L.vrp = off;    off = align256(off + R * sizeof(int32_t));
@@ -325,6 +342,7 @@ struct VerifyPlan {
   int32_t* tokens;
   uint8_t* accept_mask;
   int32_t penalized;   // penalty-aware call: rows with a penalty accept exactly
+  int32_t parts;       // work-groups per sequence (RESIDUAL: verify_parts(vocab))
 };
 
 // The one-pass top-k kernel over a plan whose rows all qualify (see TopkWs);
@@ -454,6 +472,9 @@ inline WorkspaceViews bind_workspace(char* b, int32_t max_rows, int32_t max_voca
   ws.vstats = reinterpret_cast<lsamp_row_stats*>(b + L.vstats);
   ws.vtokens = reinterpret_cast<int32_t*>(b + L.vtok);
   ws.vflags = reinterpret_cast<uint32_t*>(b + L.vfl);
+  ws.max_parts = (int32_t)verify_parts((size_t)max_vocab);
+  ws.vpart = reinterpret_cast<VerifyPart*>(b + L.vpart);
+  ws.vticket = reinterpret_cast<uint32_t*>(b + L.vtick);
   v.rank_part = reinterpret_cast<RankSlice*>(b + L.rpart);
   v.arrive_rank = reinterpret_cast<uint32_t*>(b + L.arank);
   v.vrow_ptr = reinterpret_cast<int32_t*>(b + L.vrp);

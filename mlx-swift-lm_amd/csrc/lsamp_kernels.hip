@@ -2114,7 +2114,8 @@ int launch_dt(const Workspace& ws, const SamplePlan& P, hipStream_t st, void* co
 
 // ============================================================ MTP verify
 // Is (y, id) among the n kept candidates of a row (sorted by cand_key,
-// descending)?  Binary search in global memory; called for cut-bin tokens only.
+// descending)?  Binary search (in LDS when the row's candidates were staged
+// there); called for cut-bin tokens only.
 __device__ __forceinline__ bool in_kept_list(const Candidate* rc, int n, uint64_t key) {
   int lo = 0, hi = n - 1;
   while (lo <= hi) {
@@ -2126,101 +2127,279 @@ __device__ __forceinline__ bool in_kept_list(const Candidate* rc, int n, uint64_
   return false;
 }
 
-// Kept weight of token i in a sampled row, from the row's decision (RowInfo),
-// its kept candidates and its logit.
-template <int DT>
-__device__ __forceinline__ uint64_t kept_weight_of(const RowCtx& c, const RowInfo& info,
-                                                   const ClassRule& rule, const Candidate* rc,
-                                                   const char* rowp, int32_t i) {
-  float x = load_scalar<DT>(rowp, i);
+// Kept weight of token i (transformed logit x) in a sampled row, from the
+// row's decision (its ClassRule and filter-space maximum) and its kept
+// candidates.
+__device__ __forceinline__ uint64_t kept_weight_of(const RowCtx& c, const ClassRule& rule,
+                                                   const Candidate* kl, int nk, float y_max,
+                                                   float x, int32_t i) {
   if (x != x) x = kNegInf;
   const int cls = classify(rule, x);
   if (cls == kDrop) return 0ull;
   const float y = to_filter(c, x);
-  if (cls == kCand && !in_kept_list(rc, info.kept_cands, cand_key(y, i))) return 0ull;
-  const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
+  if (cls == kCand && !in_kept_list(kl, nk, cand_key(y, i))) return 0ull;
   return weight(y, y_max, c.scale);
 }
 
-// One work-group per sequence.  Rows were sampled into ws.v* by launch_sample:
-// target (s, j) at row s*W + j, draft (s, j) at row S*W + s*(W-1) + j; each
-// row's draw used uniform [s, j] and probed draft token [s, j].
+__device__ __forceinline__ bool aligned16(const void* p) {
+  return ((uintptr_t)p & 15u) == 0u;
+}
+
+// The two rows of a residual draw (target and draft at the rejected
+// position), resolved once per work-group.
+struct ResidualRows {
+  RowCtx c;
+  ClassRule qt, qd;
+  const Candidate* ct;  // kept cut-bin candidates (in LDS when they fit)
+  const Candidate* cd;
+  int32_t nct, ncd;
+  float ymt, ymd;       // filter-space maxima
+  uint64_t Wt, Wd;      // kept weights
+  const char* trow;
+  const char* drow;
+  int32_t V;
+  bool vec;             // the target row is 16-byte aligned
+};
+
+// Token i's kept target weight, and (with_draft) its residual weight
+// max(0, p_t - p_d) with both probabilities quantized to 2^-52.
+__device__ __forceinline__ void residual_weights(const ResidualRows& r, float xt, float xd,
+                                                 int32_t i, bool with_draft, uint64_t& wt,
+                                                 uint64_t& wr) {
+  wt = kept_weight_of(r.c, r.qt, r.ct, r.nct, r.ymt, xt, i);
+  wr = 0ull;
+  if (!with_draft || wt == 0ull) return;
+  const uint64_t wd = kept_weight_of(r.c, r.qd, r.cd, r.ncd, r.ymd, xd, i);
+  const uint64_t a = (uint64_t)((double)wt / (double)r.Wt * 4503599627370496.0);
+  const uint64_t b = r.Wd ? (uint64_t)((double)wd / (double)r.Wd * 4503599627370496.0) : 0ull;
+  wr = a > b ? a - b : 0ull;
+}
+
+constexpr int kVerifyCandLds = 1024;  // kept candidates of a row staged in LDS
+constexpr int kVerifyBatch = 4;       // queue entries a lane evaluates per round trip
+
+// Screen a wave's span of the target row (kVerifySpan tokens from q0, 64
+// lanes x N-token vectors per step, coalesced): every token the target's bin
+// screen does not drop (kept and cut-bin tokens; every token when the row has
+// no finite screen) goes to the wave's LDS queue as its offset from q0, in id
+// order.  Returns the count.  Most tokens cost a multiply and a compare.
+template <int DT>
+__device__ __forceinline__ int residual_screen(const ResidualRows& r, int32_t q0,
+                                               uint16_t* queue, int lane) {
+  constexpr int N = Vec<DT>::N;
+  constexpr int kSteps = kVerifySpan / (64 * N);
+  uint4 tv[kSteps];
+#pragma unroll
+  for (int k = 0; k < kSteps; ++k)
+    tv[k] = load_vec<DT>(r.trow, (int64_t)q0 + (k * 64 + lane) * N, r.V, r.vec);
+  int n = 0;
+#pragma unroll
+  for (int k = 0; k < kSteps; ++k) {
+    const int off0 = (k * 64 + lane) * N;
+    uint32_t m = 0u;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const float x = vec_elem<DT>(tv[k], e);
+      const bool drop = x * r.qt.c32 < r.qt.screen || q0 + off0 + e >= r.V;
+      m |= drop ? 0u : 1u << e;
+    }
+    // exclusive prefix of the lanes' counts (at most 8: four ballots)
+    const int cnt = __builtin_popcount(m);
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint64_t bl = __ballot((cnt >> b) & 1);
+      off += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bl >> 32),
+                                            __builtin_amdgcn_mbcnt_lo((uint32_t)bl, 0u))
+             << b;
+      tot += __builtin_popcountll(bl) << b;
+    }
+    int o = n + off;
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+      if ((m >> e) & 1u) queue[o++] = (uint16_t)(off0 + e);
+    n += tot;
+  }
+  return n;
+}
+
+// The ids and logits of queue entries g0 + b*64 + lane (b < kVerifyBatch):
+// all loads of a batch go out together.
+template <int DT>
+__device__ __forceinline__ void residual_batch(const ResidualRows& r, int32_t q0,
+                                               const uint16_t* queue, int n, int g0, int lane,
+                                               bool with_draft, int32_t (&id)[kVerifyBatch],
+                                               float (&xt)[kVerifyBatch],
+                                               float (&xd)[kVerifyBatch]) {
+#pragma unroll
+  for (int b = 0; b < kVerifyBatch; ++b) {
+    const int idx = g0 + b * 64 + lane;
+    id[b] = idx < n ? q0 + (int32_t)queue[idx] : -1;
+  }
+#pragma unroll
+  for (int b = 0; b < kVerifyBatch; ++b) {
+    xt[b] = id[b] >= 0 ? load_scalar<DT>(r.trow, id[b]) : kNegInf;
+    xd[b] = with_draft && id[b] >= 0 ? load_scalar<DT>(r.drow, id[b]) : kNegInf;
+  }
+}
+
+// This lane's sums over the queued tokens of the target's kept weight and of
+// the residual weight (with_draft).
+template <int DT>
+__device__ __forceinline__ void residual_sums(const ResidualRows& r, int32_t q0,
+                                              const uint16_t* queue, int n, int lane,
+                                              bool with_draft, uint64_t& st, uint64_t& sr) {
+  st = 0ull;
+  sr = 0ull;
+  for (int g0 = 0; g0 < n; g0 += 64 * kVerifyBatch) {
+    int32_t id[kVerifyBatch];
+    float xt[kVerifyBatch], xd[kVerifyBatch];
+    residual_batch<DT>(r, q0, queue, n, g0, lane, with_draft, id, xt, xd);
+#pragma unroll
+    for (int b = 0; b < kVerifyBatch; ++b) {
+      uint64_t wt = 0ull, wr = 0ull;
+      if (id[b] >= 0) residual_weights(r, xt[b], xd[b], id[b], with_draft, wt, wr);
+      st += wt;
+      sr += wr;
+    }
+  }
+}
+
+// The queued token whose run of the draw weight (residual, or the target's
+// own) holds t, counted from the wave's first token, in id order; -1 if none.
+template <int DT>
+__device__ __forceinline__ int32_t residual_find(const ResidualRows& r, int32_t q0,
+                                                 const uint16_t* queue, int n, int lane,
+                                                 bool use_res, uint64_t t) {
+  uint64_t cum = 0ull;
+  int32_t found = -1;
+  for (int g0 = 0; g0 < n; g0 += 64 * kVerifyBatch) {
+    int32_t id[kVerifyBatch];
+    float xt[kVerifyBatch], xd[kVerifyBatch];
+    residual_batch<DT>(r, q0, queue, n, g0, lane, use_res, id, xt, xd);
+#pragma unroll
+    for (int b = 0; b < kVerifyBatch; ++b) {
+      uint64_t wt = 0ull, wr = 0ull;
+      if (id[b] >= 0) residual_weights(r, xt[b], xd[b], id[b], use_res, wt, wr);
+      const uint64_t w = use_res ? wr : wt;
+      const uint64_t incl = wave_incl_scan(w);
+      const uint64_t before = cum + incl - w;
+      if (w && before <= t && t < before + w) found = id[b];
+      cum += read_lane(incl, 63);
+    }
+  }
+  const uint64_t hm = __ballot(found >= 0);
+  return hm ? read_lane(found, __builtin_ctzll(hm)) : -1;
+}
+
+// Rows were sampled into ws.v* by launch_sample: target (s, j) at row s*W + j,
+// draft (s, j) at row S*W + s*(W-1) + j; each row's draw used uniform [s, j]
+// and probed draft token [s, j].  Grid: (parts, sequences).  Part 0 of a
+// sequence writes its outcome; in RESIDUAL mode, a sequence with a rejected
+// position draws from the residual there with all its parts: each part sums
+// both weights over its kVerifyPart tokens and publishes the sums, and the
+// last part to arrive picks the part whose run holds the draw, walks that
+// part again and writes the token.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, VerifyPlan Q) {
-  __shared__ int32_t s_rej;
-  __shared__ uint64_t s_red[kWaves];
-  __shared__ int32_t s_tok;
-  const int s = blockIdx.x;
-  const int tid = threadIdx.x;
+  __shared__ Candidate s_ct[kVerifyCandLds];
+  __shared__ Candidate s_cd[kVerifyCandLds];
+  __shared__ uint16_t s_queue[kWaves][kVerifySpan];
+  __shared__ uint64_t s_wt[kWaves], s_wr[kWaves];
+  __shared__ int32_t s_rej, s_last, s_part, s_res, s_tok;
+  __shared__ uint64_t s_target;
+  const int part = blockIdx.x, s = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = Q.window, D = W - 1, S = Q.sequences;
   const int32_t V = Q.vocab;
   int32_t* tok = Q.tokens + (size_t)s * W;
-  if (tid == 0) {
-    const lsamp_row_params prm = Q.params[s];
-    const bool greedy = make_ctx(Q.semantics, prm).kind == LSAMP_KIND_ARGMAX;
-    // greedy rows, and rows with a presence or frequency penalty when the
-    // penalties are applied, accept exactly (DefaultSamplerV2.swift:496-502,
-    // CBv2MTPVerifyPenalties.applies, EngineLoopV2.swift:241-243)
-    const bool exact_row = greedy || (Q.penalized && (prm.presence_penalty != 0.0f ||
-                                                      prm.frequency_penalty != 0.0f));
-    const int32_t* drafts = Q.draft_tokens + (size_t)s * D;
-    const float* u = Q.uniforms + (size_t)s * W;
-    uint8_t* am = Q.accept_mask ? Q.accept_mask + (size_t)s * D : nullptr;
-    bool failed = false;  // a row whose keep set could not be resolved
-    for (int j = 0; j < W; ++j) {
-      tok[j] = -1;
-      if (ws.vflags[s * W + j] & (LSAMP_ROW_OVERFLOW | LSAMP_ROW_TIMEOUT)) failed = true;
-      if (Q.mode == LSAMP_VERIFY_RESIDUAL && j < D &&
-          (ws.vflags[S * W + s * D + j] & (LSAMP_ROW_OVERFLOW | LSAMP_ROW_TIMEOUT)))
-        failed = true;
-    }
-    if (am)
-      for (int j = 0; j < D; ++j) am[j] = 0;
-    int rej = -1;
-    if (failed) {
-      Q.accepted[s] = 0;
-    } else if (Q.mode == LSAMP_VERIFY_RESIDUAL) {
-      int j = 0;
-      for (; j < D; ++j) {
-        const lsamp_row_stats& st = ws.vstats[s * W + j];
-        const lsamp_row_stats& sd = ws.vstats[S * W + s * D + j];
-        const double pt = st.kept_weight ? (double)st.probe_weight / (double)st.kept_weight : 0.0;
-        const double pd = sd.kept_weight ? (double)sd.probe_weight / (double)sd.kept_weight : 0.0;
-        const bool accept = pd > 0.0 ? ((double)u[j] < pt / pd) : (pt > 0.0);
-        if (!accept) break;
-        tok[j] = drafts[j];
-        if (am) am[j] = 1;
-      }
-      Q.accepted[s] = j;
-      if (j == D)
-        tok[D] = ws.vtokens[s * W + D];  // the bonus: the target row's own draw
-      else
-        rej = j;
-    } else {
-      int prefix = 0;
-      bool still = true;
-      for (int j = 0; j < W; ++j) {
-        tok[j] = ws.vtokens[s * W + j];
-        if (j >= D) continue;
-        bool accept;
-        if (Q.mode == LSAMP_VERIFY_EXACT || exact_row) {
-          accept = tok[j] == drafts[j];
-        } else {
-          // p(draft) > min(1, delta * e^-H) on the filtered, tempered row
-          const lsamp_row_stats& st = ws.vstats[s * W + j];
-          const double p = st.kept_weight ? (double)st.probe_weight / (double)st.kept_weight : 0.0;
-          const double fl = fmin(1.0, (double)Q.typical_delta * exp(-(double)st.kept_entropy));
-          accept = p > fl;
+  const int32_t* drafts = Q.draft_tokens + (size_t)s * D;
+  const float* u = Q.uniforms + (size_t)s * W;
+  uint8_t* am = Q.accept_mask ? Q.accept_mask + (size_t)s * D : nullptr;
+  constexpr uint32_t kBad = LSAMP_ROW_OVERFLOW | LSAMP_ROW_TIMEOUT;
+  if (Q.mode == LSAMP_VERIFY_RESIDUAL) {
+    // wave 0, a position per lane: accept j iff u_j * p_d < p_t (p_d = 0:
+    // iff p_t > 0); a row whose keep set could not be resolved fails the
+    // whole window
+    if (tid < 64) {
+      bool failed = false;
+      int jr = D;  // the first rejected position (D: every draft accepted)
+      for (int j0 = 0; j0 < W; j0 += 64) {
+        const int jj = j0 + lane;
+        bool bad = false, rej = false;
+        if (jj < W) bad = (ws.vflags[s * W + jj] & kBad) != 0u;
+        if (jj < D) {
+          bad = bad || (ws.vflags[S * W + s * D + jj] & kBad) != 0u;
+          const lsamp_row_stats& st = ws.vstats[s * W + jj];
+          const lsamp_row_stats& sd = ws.vstats[S * W + s * D + jj];
+          const double pt = st.kept_weight ? (double)st.probe_weight / (double)st.kept_weight : 0.0;
+          const double pd = sd.kept_weight ? (double)sd.probe_weight / (double)sd.kept_weight : 0.0;
+          rej = !(pd > 0.0 ? ((double)u[jj] < pt / pd) : (pt > 0.0));
         }
-        if (am) am[j] = accept ? 1 : 0;
-        if (still && accept)
-          ++prefix;
-        else
-          still = false;
+        failed = failed || __ballot(bad) != 0ull;
+        const uint64_t rm = __ballot(rej);
+        if (rm && jr == D) jr = j0 + __builtin_ctzll(rm);
       }
-      Q.accepted[s] = prefix;
+      if (part == 0) {
+        for (int j0 = 0; j0 < W; j0 += 64) {
+          const int jj = j0 + lane;
+          // (the rejected position's token is the residual draw's)
+          if (jj < W && (failed || jj != jr || jr == D))
+            tok[jj] = failed     ? -1
+                      : jj < jr  ? drafts[jj]
+                      : jj == jr ? ws.vtokens[s * W + D]  // (jr == D here: the bonus)
+                                 : -1;
+          if (am && jj < D) am[jj] = !failed && jj < jr ? 1 : 0;
+        }
+        if (lane == 0) Q.accepted[s] = failed ? 0 : jr;
+      }
+      if (lane == 0) s_rej = failed || jr == D ? -1 : jr;
     }
-    s_rej = rej;
+  } else if (tid == 0) {
+    s_rej = -1;
+    if (part == 0) {
+      const lsamp_row_params prm = Q.params[s];
+      const bool greedy = make_ctx(Q.semantics, prm).kind == LSAMP_KIND_ARGMAX;
+      // greedy rows, and rows with a presence or frequency penalty when the
+      // penalties are applied, accept exactly (DefaultSamplerV2.swift:496-502,
+      // CBv2MTPVerifyPenalties.applies, EngineLoopV2.swift:241-243)
+      const bool exact_row = greedy || (Q.penalized && (prm.presence_penalty != 0.0f ||
+                                                        prm.frequency_penalty != 0.0f));
+      bool failed = false;  // a row whose keep set could not be resolved
+      for (int j = 0; j < W; ++j) {
+        tok[j] = -1;
+        if (ws.vflags[s * W + j] & kBad) failed = true;
+      }
+      if (am)
+        for (int j = 0; j < D; ++j) am[j] = 0;
+      if (failed) {
+        Q.accepted[s] = 0;
+      } else {
+        int prefix = 0;
+        bool still = true;
+        for (int j = 0; j < W; ++j) {
+          tok[j] = ws.vtokens[s * W + j];
+          if (j >= D) continue;
+          bool accept;
+          if (Q.mode == LSAMP_VERIFY_EXACT || exact_row) {
+            accept = tok[j] == drafts[j];
+          } else {
+            // p(draft) > min(1, delta * e^-H) on the filtered, tempered row
+            const lsamp_row_stats& st = ws.vstats[s * W + j];
+            const double p =
+                st.kept_weight ? (double)st.probe_weight / (double)st.kept_weight : 0.0;
+            const double fl = fmin(1.0, (double)Q.typical_delta * exp(-(double)st.kept_entropy));
+            accept = p > fl;
+          }
+          if (am) am[j] = accept ? 1 : 0;
+          if (still && accept)
+            ++prefix;
+          else
+            still = false;
+        }
+        Q.accepted[s] = prefix;
+      }
+    }
   }
   __syncthreads();
   const int j = s_rej;
@@ -2228,61 +2407,148 @@ __global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, Verify
 
   // residual draw at the first rejected position: normalize(max(0, p_t - p_d))
   // with both distributions quantized to 2^-52, by inverse CDF in id order
+  // with uniform [s, W-1]; an empty residual draws from the target row itself
   const lsamp_row_params prm = Q.params[s];
-  const RowCtx c = make_ctx(Q.semantics, prm);
+  ResidualRows r;
+  r.c = make_ctx(Q.semantics, prm);
   const int rt = s * W + j, rd = S * W + s * D + j;
   const RowInfo it = ws.rows[rt], id = ws.rows[rd];
-  const ClassRule qt = make_rule(it, c), qd = make_rule(id, c);
-  const Candidate* ct = ws.cands + (size_t)rt * kCandCap;
-  const Candidate* cd = ws.cands + (size_t)rd * kCandCap;
-  const uint64_t Wt = ws.vstats[rt].kept_weight, Wd = ws.vstats[rd].kept_weight;
+  r.qt = make_rule(it, r.c);
+  r.qd = make_rule(id, r.c);
+  r.nct = it.kept_cands;
+  r.ncd = id.kept_cands;
+  {
+    const Candidate* ct = ws.cands + (size_t)rt * kCandCap;
+    const Candidate* cd = ws.cands + (size_t)rd * kCandCap;
+    r.ct = ct;
+    r.cd = cd;
+    if (r.nct <= kVerifyCandLds) {
+      for (int i = tid; i < r.nct; i += kThreads) s_ct[i] = ct[i];
+      r.ct = s_ct;
+    }
+    if (r.ncd <= kVerifyCandLds) {
+      for (int i = tid; i < r.ncd; i += kThreads) s_cd[i] = cd[i];
+      r.cd = s_cd;
+    }
+  }
+  r.ymt = it.mode == kModePosInf ? kPosInf : to_filter(r.c, it.x_max);
+  r.ymd = id.mode == kModePosInf ? kPosInf : to_filter(r.c, id.x_max);
+  r.Wt = ws.vstats[rt].kept_weight;
+  r.Wd = ws.vstats[rd].kept_weight;
   const size_t es = DT == LSAMP_DTYPE_F32 ? 4 : 2;
-  const char* trow = reinterpret_cast<const char*>(Q.target) + (size_t)rt * V * es;
-  const char* drow = reinterpret_cast<const char*>(Q.draft) + (size_t)(s * D + j) * V * es;
-  auto res_of = [&](int32_t i, bool use_residual) -> uint64_t {
-    const uint64_t wt = kept_weight_of<DT>(c, it, qt, ct, trow, i);
-    if (!use_residual) return wt;
-    if (wt == 0ull) return 0ull;
-    const uint64_t wd = kept_weight_of<DT>(c, id, qd, cd, drow, i);
-    const uint64_t a = (uint64_t)((double)wt / (double)Wt * 4503599627370496.0);
-    const uint64_t b = Wd ? (uint64_t)((double)wd / (double)Wd * 4503599627370496.0) : 0ull;
-    return a > b ? a - b : 0ull;
-  };
-  const int32_t per = (V + kThreads - 1) / kThreads;
-  const int32_t i0 = tid * per, i1 = i0 + per < V ? i0 + per : V;
-  const float ur = Q.uniforms[(size_t)s * W + D];
-  int tokout = -1;
-  for (int pass = 0; pass < 2 && tokout < 0; ++pass) {
-    // pass 0: the residual; pass 1 (only when it is empty): the target itself
-    const bool use_residual = pass == 0;
-    uint64_t mine = 0ull;
-    for (int32_t i = i0; i < i1; ++i) mine += res_of(i, use_residual);
-    uint64_t tot = 0ull;
-    const uint64_t ex = block_excl_scan(mine, s_red, &tot);
-    if (tot == 0ull) continue;
-    const uint64_t target = scaled_target(uniform_u32(ur), tot);
-    if (tid == 0) s_tok = -1;
-    __syncthreads();
-    if (ex <= target && target < ex + mine) {
-      uint64_t cum = ex;
-      for (int32_t i = i0; i < i1; ++i) {
-        const uint64_t w = res_of(i, use_residual);
-        cum += w;
-        if (w && cum > target) {
-          s_tok = i;
-          break;
+  r.trow = reinterpret_cast<const char*>(Q.target) + (size_t)rt * V * es;
+  r.drow = reinterpret_cast<const char*>(Q.draft) + (size_t)(s * D + j) * V * es;
+  r.V = V;
+  r.vec = aligned16(r.trow);
+  if (tid == 0) s_tok = -1;
+  __syncthreads();
+  uint16_t* queue = s_queue[wv];
+  const int P = Q.parts;
+  {
+    const int32_t q0 = part * kVerifyPart + wv * kVerifySpan;
+    const int n = residual_screen<DT>(r, q0, queue, lane);
+    uint64_t st, sr;
+    residual_sums<DT>(r, q0, queue, n, lane, true, st, sr);
+    st = wave_sum(st);
+    sr = wave_sum(sr);
+    if (lane == 0) {
+      s_wt[wv] = st;
+      s_wr[wv] = sr;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t T = 0ull, R = 0ull;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      T += s_wt[w];
+      R += s_wr[w];
+    }
+    VerifyPart* vp = ws.vpart + (size_t)s * ws.max_parts + part;
+    st_coherent(&vp->res, R);
+    st_coherent(&vp->tgt, T);
+    drain_memory();
+    const uint32_t t =
+        __hip_atomic_fetch_add(&ws.vticket[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = t + 1u == (uint32_t)P;
+    if (last) st_coherent(&ws.vticket[s], 0u);
+    s_last = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // the last part: the draw's kind and target, and the part holding it
+  if (tid < 64) {
+    const VerifyPart* vp = ws.vpart + (size_t)s * ws.max_parts;
+    uint64_t R = 0ull, T = 0ull;
+    for (int p0 = 0; p0 < P; p0 += 64) {
+      const int p = p0 + lane;
+      R += wave_sum(p < P ? ld_coherent(&vp[p].res) : 0ull);
+      T += wave_sum(p < P ? ld_coherent(&vp[p].tgt) : 0ull);
+    }
+    const bool use_res = R != 0ull;
+    const uint64_t tot = use_res ? R : T;
+    int ps = -1;
+    uint64_t rel = 0ull;
+    if (tot) {
+      const uint64_t target = scaled_target(uniform_u32(u[D]), tot);
+      uint64_t cum = 0ull;
+      for (int p0 = 0; p0 < P && ps < 0; p0 += 64) {
+        const int p = p0 + lane;
+        const uint64_t v = p < P ? ld_coherent(use_res ? &vp[p].res : &vp[p].tgt) : 0ull;
+        const uint64_t incl = wave_incl_scan(v);
+        const uint64_t before = cum + incl - v;
+        const uint64_t hm = __ballot(v && before <= target && target < before + v);
+        if (hm) {
+          const int hl = __builtin_ctzll(hm);
+          ps = p0 + hl;
+          rel = target - read_lane(before, hl);
         }
+        cum += read_lane(incl, 63);
       }
     }
-    __syncthreads();
-    tokout = s_tok;
+    if (lane == 0) {
+      s_part = ps;
+      s_target = rel;
+      s_res = use_res ? 1 : 0;
+    }
   }
-  if (tid == 0) tok[j] = tokout;
+  __syncthreads();
+  const int ps = s_part;
+  if (ps >= 0) {
+    const bool use_res = s_res != 0;
+    const uint64_t t = s_target;
+    const int32_t q0 = ps * kVerifyPart + wv * kVerifySpan;
+    const int n = residual_screen<DT>(r, q0, queue, lane);
+    uint64_t st, sr;
+    residual_sums<DT>(r, q0, queue, n, lane, use_res, st, sr);
+    const uint64_t mine = wave_sum(use_res ? sr : st);
+    if (lane == 0) s_wt[wv] = mine;
+    __syncthreads();
+    uint64_t cum = 0ull, wb = 0ull;
+    int wsel = -1;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const uint64_t v = s_wt[w];
+      if (wsel < 0 && v && cum <= t && t < cum + v) {
+        wsel = w;
+        wb = cum;
+      }
+      cum += v;
+    }
+    if (wv == wsel) {
+      const int32_t f = residual_find<DT>(r, q0, queue, n, lane, use_res, t - wb);
+      if (lane == 0) s_tok = f;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) tok[j] = s_tok;
 }
 
 template <int DT>
 int launch_verify_dt(const Workspace& ws, const VerifyPlan& Q, hipStream_t st) {
-  hipLaunchKernelGGL(k_verify_finish<DT>, dim3((unsigned)Q.sequences), dim3(kThreads), 0, st, ws, Q);
+  hipLaunchKernelGGL(k_verify_finish<DT>, dim3((unsigned)Q.parts, (unsigned)Q.sequences),
+                     dim3(kThreads), 0, st, ws, Q);
   return (int)hipGetLastError();
 }
 

@@ -139,3 +139,29 @@ def test_config5_full(ctx):
                     cfg["params"], cfg["uniforms"], cfg["dtype"])
     check(g, o, "config5")
     print(f"config5: accepted {g['accepted'].tolist()}")
+
+
+@pytest.mark.parametrize("dtype,V,pkw", [
+    (_ffi.DTYPE_BF16, 40003, dict(temperature=0.8, top_p=0.95)),
+    (_ffi.DTYPE_F16, 20000, dict(temperature=1.0, min_p=0.02)),
+    (_ffi.DTYPE_F32, 70001, dict(temperature=0.9, top_k=300)),
+    (_ffi.DTYPE_BF16, 16384, dict(temperature=1.2)),
+])
+def test_residual_across_parts(ctx, dtype, V, pkw):
+    # rows wider than one work-group's part: the residual sums are split over
+    # several parts, the last part to finish draws (ragged last part, every dtype)
+    rng = np.random.default_rng(V)
+    S, Wn = 6, 3
+    t = rng.normal(0, 3, (S, Wn, V)).astype(np.float32)
+    d = (t[:, : Wn - 1] + rng.normal(0, 1.5, (S, Wn - 1, V))).astype(np.float32)
+    if dtype == _ffi.DTYPE_BF16:
+        t, d = W.f32_to_bf16_bits(t), W.f32_to_bf16_bits(d)
+    elif dtype == _ffi.DTYPE_F16:
+        t, d = t.astype(np.float16).view(np.uint16), d.astype(np.float16).view(np.uint16)
+    params = W._params([W.resolve_cbv2(vocab=V, **pkw)] * S)
+    drafts = draw_drafts(d, dtype, params, rng.random((S, Wn - 1), dtype=np.float32))
+    u = rng.random((S, Wn), dtype=np.float32)
+    for rep in range(2):  # twice: the parts' arrival counters return to zero
+        g, o = run_both(ctx, _ffi.VERIFY_RESIDUAL, t, d, drafts, params, u, dtype)
+        check(g, o, f"parts dtype {dtype} V {V} {pkw} rep {rep}")
+    assert (g["accepted"] < Wn - 1).any(), "no rejection: the residual draw was not exercised"
