@@ -188,6 +188,11 @@ struct TaskLds {
   int32_t tmo;  // this task's bounded wait gave up
   uint32_t flags;
 };
+// Select pass: each wave's queue of screened tokens (offset in the slice,
+// value bits) lives in the short-list area, idle in that phase.
+constexpr int kSelQueue = (int)(sizeof(TaskLds::ssrc) / sizeof(uint2) / kWaves);  // 512
+static_assert(kSelQueue >= kThreads / kWaves * 8, "a quad step of a wave fits the queue");
+
 
 
 // ============================================================ merge (stats)
@@ -1913,46 +1918,74 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   };
   const ClassRule rule = make_rule(info, c);
   if (active) {
-    for_quads(S, nq, [&](int g, uint4& v) -> bool {
-      const int32_t i0 = base32 + (tid + g * kThreads) * N;
-      // screen the quad by its largest element; the rare quads that hold a
-      // kept or candidate token are classified element by element
-      const float qm = vec_max_nn<DT>(v);
-      uint64_t part = 0ull;
-      if (qm * rule.c32 >= rule.screen) {
-        uint32_t kb = 0u, cb = 0u;
-#pragma unroll
-        for (int e = 0; e < N; ++e) {
-          const int cls = classify(rule, vec_elem<DT>(v, e));
-          kb |= (uint32_t)(cls == kKept) << e;
-          cb |= (uint32_t)(cls == kCand) << e;
-        }
-        if (kb == FULL) {
-          // every element kept (wide nuclei): static element reads
-#pragma unroll
-          for (int e = 0; e < N; ++e) keep_token(vec_elem<DT>(v, e), i0 + e, part);
-        } else {
-          for (uint32_t bits = kb | cb; bits != 0u; bits &= bits - 1u) {
-            const int e = __builtin_ctz(bits);
-            const float x = vec_elem_dyn<DT>(v, e);
-            if ((kb >> e) & 1u)
-              keep_token(x, i0 + e, part);
-            else
-              cand_token(x, i0 + e);
+    // The bin screen passes the kept and cut-bin tokens only (a few percent
+    // of a top-p row, spread over every wave): they are queued per wave in
+    // LDS, in id order, as (offset in the slice, value bits), and classified
+    // and weighed with every lane busy, so a wave does not pay the per-token
+    // work once for each lane that holds such a token.
+    uint2* q = reinterpret_cast<uint2*>(L.ssrc) + (tid >> 6) * kSelQueue;
+    const int lane = tid & 63;
+    int qn = 0;  // wave-uniform
+    auto flush = [&]() {
+      for (int i0 = 0; i0 < qn; i0 += 64) {
+        const int i = i0 + lane;
+        uint64_t w = 0ull;
+        int ch = -1;
+        if (i < qn) {
+          const uint2 en = q[i];
+          const float x = __uint_as_float(en.y);
+          const int32_t id = base32 + (int32_t)en.x;
+          const int cls = classify(rule, x);
+          if (cls == kKept) {
+            keep_token(x, id, w);
+            ch = (int)(en.x / kChunk);
+          } else if (cls == kCand) {
+            cand_token(x, id);
           }
         }
-      }
-      // chunk sums: a wave's quads lie in one 1024-token chunk
-      if (__ballot(part != 0ull)) {
-        const uint64_t sum = wave_sum(part);
-        if ((tid & 63) == 0) {
-          const int32_t wi0 = ((tid & ~63) + g * kThreads) * N;
-          atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.s.chunk[wi0 / kChunk]),
-                    (unsigned long long)sum);
+        // chunk sums: one atomic per round when its kept tokens share a chunk
+        const int chm = wave_min(ch < 0 ? 0x7fffffff : ch);
+        const bool one = __ballot(ch >= 0 && ch != chm) == 0ull;
+        if (one) {
+          const uint64_t sum = wave_sum(w);
+          if (lane == 0 && sum)
+            atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.s.chunk[chm]),
+                      (unsigned long long)sum);
+        } else if (w) {
+          atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.s.chunk[ch]), (unsigned long long)w);
         }
       }
+      qn = 0;
+    };
+    for_quads(S, nq, [&](int g, uint4& v) -> bool {
+      const int32_t li0 = (tid + g * kThreads) * N;
+      uint32_t m = 0u;
+#pragma unroll
+      for (int e = 0; e < N; ++e)
+        m |= (vec_elem<DT>(v, e) * rule.c32 >= rule.screen ? 1u : 0u) << e;
+      if (__ballot(m != 0u) == 0ull) return false;
+      // the lanes' offsets in the queue: an exclusive prefix of their counts
+      // (at most N <= 8: four ballots)
+      const int cnt = __builtin_popcount(m);
+      int off = 0, tot = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint64_t bl = __ballot((cnt >> b) & 1);
+        off += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bl >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bl, 0u))
+               << b;
+        tot += __builtin_popcountll(bl) << b;
+      }
+      if (qn + tot > kSelQueue) flush();
+      int o = qn + off;
+#pragma unroll
+      for (int e = 0; e < N; ++e)
+        if ((m >> e) & 1u)
+          q[o++] = make_uint2((uint32_t)(li0 + e), __float_as_uint(vec_elem<DT>(v, e)));
+      qn += tot;
       return false;
     });
+    flush();
     if (kout) {
       // keep bytes of tokens outside the entry table (re-read; an output for
       // parity checks only); candidates' bytes are written by the finalize
