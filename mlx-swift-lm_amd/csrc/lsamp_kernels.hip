@@ -437,6 +437,8 @@ struct TailIn {
   int32_t kept_all; //   count
   float u_draw;
   int32_t probe;
+  bool probe_x_set; // probe_x holds the probe's logit (loaded early)
+  float probe_x;
   int32_t n_list;   // lane s < G: kept tokens slice s listed (> kKeptCap: incomplete)
   bool reset;       // clear the row's select counters (histogram path)
   bool fused;
@@ -693,11 +695,12 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
       if (P.entries[e].token == probe) pe = e;
     const uint64_t hp = __ballot(pe >= 0);
     float x;
+    const float xr = t.probe_x_set ? t.probe_x : load_scalar<DT>(rowp, probe);
     if (hp) {
       const int32_t e = read_lane(pe, __builtin_ctzll(hp));
-      x = patch_value(c, prm, load_scalar<DT>(rowp, probe), P.entries[e], DT);
+      x = patch_value(c, prm, xr, P.entries[e], DT);
     } else {
-      x = load_scalar<DT>(rowp, probe);
+      x = xr;
     }
     if (!mask_allows(mrow, P.mask_words, P.mask_bits, P.mask_tail, probe) || x != x) x = kNegInf;
     const int cls = classify(make_rule(info, c), x);
@@ -761,9 +764,15 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   // ---- wave 0 issues every independent load at once
   SelectPartial part{};
   uint64_t rch[kChunksPerLane];
-  uint64_t key0 = 0ull;
+  // candidate tid, read before the count is known (slots past it are ignored)
+  uint64_t key0;
+  {
+    const float cy = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[tid].y)));
+    key0 = cand_key(cy, ld_coherent(&rc[tid].id));
+  }
   float u_draw = 0.0f;
   int32_t probe = -1, total_cand = 0;
+  float probe_x = kNegInf;
   if (wave0) {
     if (l < G) {
       const SelectPartial* sp = ws.partials + (size_t)row * kMaxSlices + l;
@@ -780,10 +789,6 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
       const int ci = kChunksPerLane * l + i;
       rch[i] = ci < nch_row ? ld_coherent(&rowchunks[ci]) : 0ull;
     }
-    // candidate l, read before the count is known (slots past it are ignored)
-    const float cy = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rc[l].y)));
-    const int32_t cid = ld_coherent(&rc[l].id);
-    key0 = cand_key(cy, cid);
     int32_t tc = 0;
     float u = 0.0f;
     int32_t pr = -1;
@@ -799,6 +804,8 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
     total_cand = read_lane(tc, 0);
     u_draw = read_lane(u, 0);
     probe = read_lane(pr, 0);
+    // the probe's logit, requested now: it is needed only at the end
+    if (probe >= 0 && probe < P.vocab) probe_x = load_scalar<DT>(rowp, probe);
   }
   // ---- row-wide partials (wave 0), shared through LDS with the other waves
   double ent_all = 0.0;
@@ -821,7 +828,17 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   nc = L.misc[1];
 
   // ---- sort candidates: value descending, id ascending (-0 == +0)
-  if (nc > 64) {
+  if (nc > 64 && nc <= kThreads) {
+    // rank by counting (keys are distinct: ids are): one barrier
+    if (tid < nc) F.dw[tid] = key0;
+    __syncthreads();
+    if (tid < nc) {
+      int rank = 0;
+      for (int i = 0; i < nc; ++i) rank += F.dw[i] > key0 ? 1 : 0;
+      F.keys[rank] = key0;
+    }
+    __syncthreads();
+  } else if (nc > 64) {
     int n2 = 1;
     while (n2 < nc) n2 <<= 1;
     for (int i = tid; i < n2; i += kThreads) {
@@ -872,6 +889,8 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   t.kept_all = kept_all;
   t.u_draw = u_draw;
   t.probe = probe;
+  t.probe_x_set = true;
+  t.probe_x = probe_x;
   t.n_list = part.n_list;
   t.reset = true;
   t.fused = fused;
@@ -1296,6 +1315,8 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   t.kept_all = 0;
   t.u_draw = u_draw;
   t.probe = probe;
+  t.probe_x_set = false;
+  t.probe_x = 0.0f;
   t.n_list = 0;
   t.reset = false;
   t.fused = P.fused != 0;
