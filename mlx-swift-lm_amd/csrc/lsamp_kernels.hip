@@ -147,6 +147,7 @@ struct FinalLds {
   float cx[kChunk];
   uint8_t cent[kChunk];
   uint8_t cflag[kChunk];
+  uint16_t qoff[kChunk];  // chunk re-read: the slots the bin screen passes
 };
 union PhaseLds {
   uint64_t hist[kHist + 64];  // + one discard word per lane
@@ -645,14 +646,38 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
       const ClassRule rule = make_rule(info, c);
       const uint32_t allow =
           mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, (int32_t)i0, kSlotsPerLane);
+      // every slot's value to LDS; the slots the bin screen passes (kept and
+      // cut-bin tokens) are listed, then classified and weighed a slot per
+      // lane, so the wave does not run the weight once per lane holding one
+      uint32_t m = 0u;
 #pragma unroll
       for (int i = 0; i < kSlotsPerLane; ++i) {
         const int o = kSlotsPerLane * l + i;
-        if (cb + o >= ce) continue;
         float x = F.cent[o] ? F.cx[o]
                             : (((allow >> i) & 1u) ? vec_elem<DT>(lv[i / Vec<DT>::N], i % Vec<DT>::N)
                                                    : kNegInf);
         if (x != x) x = kNegInf;
+        F.cx[o] = x;
+        m |= (cb + o < ce && x * rule.c32 >= rule.screen ? 1u : 0u) << i;
+      }
+      static_assert(kSlotsPerLane <= 16, "slot counts take five ballots");
+      const int cnt = __builtin_popcount(m);
+      int off = 0, tot = 0;
+#pragma unroll
+      for (int b = 0; b < 5; ++b) {
+        const uint64_t bl = __ballot((cnt >> b) & 1);
+        off += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bl >> 32),
+                                              __builtin_amdgcn_mbcnt_lo((uint32_t)bl, 0u))
+               << b;
+        tot += __builtin_popcountll(bl) << b;
+      }
+#pragma unroll
+      for (int i = 0; i < kSlotsPerLane; ++i)
+        if ((m >> i) & 1u) F.qoff[off++] = (uint16_t)(kSlotsPerLane * l + i);
+      __builtin_amdgcn_wave_barrier();
+      for (int j = l; j < tot; j += 64) {
+        const int o = F.qoff[j];
+        const float x = F.cx[o];
         const int cls = classify(rule, x);
         if (cls == kKept || (cls == kCand && F.cflag[o]))
           F.dw[draw_slot(o)] = weight(to_filter(c, x), y_max, c.scale);
