@@ -172,6 +172,7 @@ struct Workspace {
   uint32_t* arrive_stats;   // [max_rows]
   uint32_t* arrive_select;  // [max_rows]
   uint32_t* status;         // [1] sticky error bits (kStatus*)
+  uint32_t* tasks;          // [1] fused kernel over several rounds: tasks taken
   // MTP verification: the sampled rows' outputs
   lsamp_row_stats* vstats;  // [max_rows]
   int32_t* vtokens;         // [max_rows]
@@ -209,7 +210,7 @@ struct TopkWs {
 // the one range [zero_begin, zero_end); the kernels return them to zero at
 // the end of every step.
 struct WorkspaceLayout {
-  size_t sum, rows, chunk, cand, klist, part, status, cc, as, asel, tticket, vtick;
+  size_t sum, rows, chunk, cand, klist, part, status, tasks, cc, as, asel, tticket, vtick;
   size_t vstats, vtok, vfl, vpart, rpart, arank, vrp, vrl, smask, tpub, tepoch;
   size_t zero_begin, zero_end, total;
 };
@@ -228,6 +229,7 @@ constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
   L.part = off;   off = align256(off + R * kMaxSlices * sizeof(SelectPartial));
   L.zero_begin = off;
   L.status = off; off = align256(off + sizeof(uint32_t));
+  L.tasks = off;  off = align256(off + sizeof(uint32_t));
   L.cc = off;     off = align256(off + R * sizeof(uint32_t));
   L.as = off;     off = align256(off + R * sizeof(uint32_t));
   L.asel = off;   off = align256(off + R * sizeof(uint32_t));
@@ -466,6 +468,7 @@ inline WorkspaceViews bind_workspace(char* b, int32_t max_rows, int32_t max_voca
   ws.klist = reinterpret_cast<KeptItem*>(b + L.klist);
   ws.partials = reinterpret_cast<SelectPartial*>(b + L.part);
   ws.status = reinterpret_cast<uint32_t*>(b + L.status);
+  ws.tasks = reinterpret_cast<uint32_t*>(b + L.tasks);
   ws.cand_count = reinterpret_cast<uint32_t*>(b + L.cc);
   ws.arrive_stats = reinterpret_cast<uint32_t*>(b + L.as);
   ws.arrive_select = reinterpret_cast<uint32_t*>(b + L.asel);

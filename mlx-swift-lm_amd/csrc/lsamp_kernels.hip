@@ -188,6 +188,7 @@ struct TaskLds {
   int32_t last;
   int32_t tmo;  // this task's bounded wait gave up
   uint32_t flags;
+  uint32_t task;  // fused kernel over several rounds: the task taken
 };
 // Select pass: each wave's queue of screened tokens (offset in the slice,
 // value bits) lives in the short-list area, idle in that phase.
@@ -2150,11 +2151,31 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
     if (rowslot < P.rows) run_task<DT, kFused>(ws, P, rowslot, slice, L);
     return;
   }
-  for (int r0 = 0; r0 < P.rows; r0 += P.rows_per_round) {
-    const int row = r0 + rowslot;
-    if (row < P.rows) run_task<DT, kFused>(ws, P, row, slice, L);
+  // More tasks than work-groups: each work-group takes the next task (row-
+  // major, slice-minor) from a counter when it has finished the last one, so
+  // fast rows (short lists) and slow ones (wide nuclei) balance over the
+  // grid.  The tasks taken always form a prefix, and a work-group finishes a
+  // task before it takes another, so the slices a row waits for are held by
+  // running work-groups or are next in line for the first one free.
+  const uint32_t total = (uint32_t)(P.rows * G);
+  uint32_t t;
+  for (;;) {
+    if (threadIdx.x == 0)
+      L.task = __hip_atomic_fetch_add(ws.tasks, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    t = L.task;
+    __syncthreads();
+    if (t >= total) break;
+    // (through empty asm: nothing derived from the arguments is hoisted out
+    // of the loop and held across tasks)
+    const Workspace wsr = in_sgprs(ws);
+    const SamplePlan Pr = in_sgprs(P);
+    run_task<DT, kFused>(wsr, Pr, (int)(t / (uint32_t)G), (int)(t % (uint32_t)G), L);
     __syncthreads();
   }
+  // every work-group ends with one failed take: the last of those returns
+  // the counter to zero for the next step
+  if (threadIdx.x == 0 && t == total + gridDim.x - 1u) st_coherent(ws.tasks, 0u);
 }
 
 template <int DT>
