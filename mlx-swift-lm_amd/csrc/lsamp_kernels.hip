@@ -2158,6 +2158,34 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
   // task before it takes another, so the slices a row waits for are held by
   // running work-groups or are next in line for the first one free.
   const uint32_t total = (uint32_t)(P.rows * G);
+  // Rows in the order their tasks are taken: rows bound for the histogram
+  // path (the slow ones) first, short-list rows after, so the grid's last
+  // tasks are short.  Every work-group derives the same order from the
+  // rows' parameters (one load per thread, two block scans).
+  constexpr int kOrderCap = 4096;
+  __shared__ uint16_t order[kOrderCap];
+  const bool ordered = P.rows <= kOrderCap;
+  if (ordered) {
+    int placed_slow = 0, placed_short = 0;
+    for (int r0 = 0; r0 < P.rows; r0 += kThreads) {
+      const int r = r0 + (int)threadIdx.x;
+      int slow = 0;
+      if (r < P.rows) {
+        const lsamp_row_params prm = P.params[params_index(P, r)];
+        slow = short_k(make_ctx(P.semantics, prm), prm, P.vocab) == 0 ? 1 : 0;
+      }
+      const int fast = r < P.rows ? 1 - slow : 0;
+      int n_slow = 0, n_fast = 0;
+      const int es = block_excl_scan(slow, L.redi, &n_slow);
+      const int ef = block_excl_scan(fast, L.redi, &n_fast);
+      // (short-list rows fill the order from its end)
+      if (r < P.rows)
+        order[slow ? placed_slow + es : P.rows - 1 - (placed_short + ef)] = (uint16_t)r;
+      placed_slow += n_slow;
+      placed_short += n_fast;
+    }
+    __syncthreads();
+  }
   uint32_t t;
   for (;;) {
     if (threadIdx.x == 0)
@@ -2170,7 +2198,8 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
     // of the loop and held across tasks)
     const Workspace wsr = in_sgprs(ws);
     const SamplePlan Pr = in_sgprs(P);
-    run_task<DT, kFused>(wsr, Pr, (int)(t / (uint32_t)G), (int)(t % (uint32_t)G), L);
+    const int q = (int)(t / (uint32_t)G);
+    run_task<DT, kFused>(wsr, Pr, ordered ? (int)order[q] : q, (int)(t % (uint32_t)G), L);
     __syncthreads();
   }
   // every work-group ends with one failed take: the last of those returns
