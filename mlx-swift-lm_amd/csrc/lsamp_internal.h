@@ -44,7 +44,7 @@ static_assert(kVerifySpan <= 65536, "queue entries are 16-bit offsets");
 // publishes them all (at most kShortPub, which the row's candidate area
 // holds for every slice).
 constexpr int kShortMaxK = 256;
-constexpr int kQStage = 3;
+constexpr int kQStage = 4;
 constexpr int kShortPub = kCandCap / kMaxSlices;  // 512
 constexpr int kTauBins = 1024;                    // thread-maximum histogram
 // Kept tokens listed per slice (fast draw path); beyond this the draw scans.

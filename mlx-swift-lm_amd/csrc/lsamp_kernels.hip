@@ -2162,7 +2162,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
   // path (the slow ones) first, short-list rows after, so the grid's last
   // tasks are short.  Every work-group derives the same order from the
   // rows' parameters (one load per thread, two block scans).
-  constexpr int kOrderCap = 4096;
+  constexpr int kOrderCap = 1024;
   __shared__ uint16_t order[kOrderCap];
   const bool ordered = P.rows <= kOrderCap;
   if (ordered) {
