@@ -909,6 +909,7 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   P.logits2 = residual ? a->draft_logits : a->target_logits;
   P.rows_split = (int32_t)(S * W);
   P.vwin = (int32_t)W;
+  P.bonus_only = residual ? 1 : 0;
   P.params = a->params;
   P.uniforms = a->uniforms;
   P.probe_tokens = a->draft_tokens;

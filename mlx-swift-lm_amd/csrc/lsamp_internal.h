@@ -307,6 +307,9 @@ struct SamplePlan {
   // row uses params[s], the uniform [s, j] of a [S, vwin] array, and probes
   // the draft token [s, j] of a [S, vwin - 1] array (none at j = vwin - 1).
   int32_t vwin;
+  // MTP verify in RESIDUAL mode: only the last target position's draw is
+  // read (the bonus token); the other rows report their weights, no token
+  int32_t bonus_only;
   const lsamp_row_params* params;
   const int32_t* row_ptr;
   const int32_t* row_len;  // or NULL: rows end at row_ptr[row + 1]

@@ -575,7 +575,9 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
   const uint64_t hitc = __ballot(my_c >= 0);
   int cstar = -1;
   uint64_t ltarget = 0ull;
-  if (W && hitc && !overflow && active) {
+  // (a verify row whose draw nobody reads keeps only its weights)
+  const bool draw = !P.bonus_only || (row < P.rows_split && row % P.vwin == P.vwin - 1);
+  if (W && hitc && !overflow && active && draw) {
     const int f = __builtin_ctzll(hitc);
     cstar = read_lane(my_c, f);
     ltarget = read_lane(my_t, f);
@@ -740,7 +742,7 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
       flags |= LSAMP_ROW_TIMEOUT;
     else if (overflow)
       flags |= LSAMP_ROW_OVERFLOW;
-    if (!overflow && (token < 0 || W == 0ull)) flags |= LSAMP_ROW_EMPTY;
+    if (!overflow && ((draw && token < 0) || W == 0ull)) flags |= LSAMP_ROW_EMPTY;
     const int tok = overflow ? -1 : token;
     P.tokens[row] = tok;
     if (P.row_flags) P.row_flags[row] = flags;
