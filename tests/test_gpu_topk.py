@@ -207,3 +207,32 @@ def test_batched_decode_equals_fused(ctx):
     assert np.array_equal(a["keep"], b["keep"]), "keep sets differ"
     for f in ("kept", "token", "kept_weight", "probe_weight"):
         assert np.array_equal(a["stats"][f], b["stats"][f]), f"stats {f} differ"
+
+
+@pytest.mark.parametrize("dtype", [_ffi.DTYPE_BF16, _ffi.DTYPE_F16])
+def test_top_p_cuts_inside_top_k(ctx, dtype):
+    # peaked rows (a head of 40 tokens spread over the slices) whose top-p
+    # cut falls inside the top-k: the kernel's lower bound of the row's mass
+    # (one exponential a quad) cannot decide the limit there, so the
+    # finalizer waits for the slices' exact sums; Gaussian rows in the same
+    # launch are decided by the bound; some head tokens are penalty entries
+    rng = np.random.default_rng(71 + dtype)
+    R, V = 24, 151936
+    x = rng.normal(0, 2, (R, V)).astype(np.float32)
+    entries = []
+    params = []
+    for r in range(R):
+        head = rng.choice(V, 40, replace=False)
+        if r % 4 != 3:
+            x[r, head] = 12.0 - 0.4 * np.arange(40) + rng.normal(0, 0.05, 40)
+        ent = np.zeros(8, dtype=PENALTY_DTYPE)
+        ent["token"] = np.sort(head[::5])
+        ent["count"] = rng.integers(1, 4, 8)
+        ent["flags"] = _ffi.PEN_PRESENCE
+        entries.append(ent)
+        top_p = [0.3, 0.6, 0.9, 0.95, 0.99, 0.8][r % 6]
+        params.append(W.resolve_cbv2(temperature=[0.7, 1.0, 1.3, 0.7][r // 6], top_k=[50, 64, 20][r % 3],
+                                     top_p=top_p, min_p=0.0 if r % 2 else 0.01,
+                                     presence_penalty=0.4, vocab=V))
+    u = rng.random(R).astype(np.float32)
+    check(ctx, cfg_of(to_bits(x, dtype), dtype, params, u, entries=entries), f"top-p in top-k dt{dtype}")
