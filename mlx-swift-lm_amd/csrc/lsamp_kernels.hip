@@ -1403,6 +1403,12 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   const RowCtx c = make_ctx(P.semantics, prm);
   const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
   prefetch_entries(P, tid, ep);
+  // the slice's grammar-mask words, staged in LDS (the short-list area,
+  // idle until after pass 1) before the pass
+  MaskStage ms;
+  if (mrow) load_mask_stage(mrow, P.mask_words, base32, end32, tid, ms);
+  uint32_t* const mw = reinterpret_cast<uint32_t*>(L.sh.squad);
+  static_assert(sizeof(L.sh.squad) >= kSliceWords * sizeof(uint32_t), "staged mask words fit");
   // The slice's logits: 16-byte vectors all in flight at once, through one
   // buffer descriptor over the slice (the lane's byte offset is fixed and
   // the quad's is a scalar; lanes past the slice end read as zero, by the
@@ -1436,6 +1442,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
   EntryMarks<> em;
   float emax = kNegInf;  // this thread's patched entry values
+  if (mrow) store_mask_stage(ms, P.mask_words, P.mask_bits, P.mask_tail, base32, end32, tid, mw);
   mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
   if (!aligned || (end32 & (N - 1)) != 0) {
     // unaligned rows, or the row's last partial quad: element by element
@@ -1495,7 +1502,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     const int32_t rem = lim - g * (kThreads * N);
     const uint32_t tail = ~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem));
     uint32_t ex = ((pcur >> pen_shift) | tail) & FULL;
-    if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
+    if (mrow) ex |= ~staged_allow_bits(mw, i0 - base32, N) & FULL;
     // (NaNs are rare, behind a branch; entry tokens are in most quads of a
     // wave, so the exclusion runs unconditionally, a no-op without bits)
     if (nonfinite_seen<DT>(probe)) {

@@ -146,6 +146,49 @@ __device__ __forceinline__ uint32_t mask_allow_bits(const uint32_t* mrow, int32_
   return (bits | (tail == LSAMP_MASK_TAIL_KEEP ? (full & ~in_mask) : 0u)) & full;
 }
 
+// The grammar mask of one slice, staged in LDS for the pass over the slice:
+// word w holds the allow bits (what mask_allow_bits gives) of the slice's
+// tokens 32w .. 32w + 31, so the pass reads LDS instead of waiting on a
+// global word for every quad.  Slices start on a multiple of 32 tokens.
+// The raw words are requested ahead of the slice's logits (loads complete
+// in order, so they land first), then converted and stored.
+constexpr int kMaskStage = kMaxSliceLen / 32 / kThreads;  // words per thread
+struct MaskStage {
+  uint32_t w[kMaskStage];  // raw words tid, tid + kThreads, ...
+};
+__device__ __forceinline__ void load_mask_stage(const uint32_t* mrow, int32_t mask_words,
+                                                int32_t base32, int32_t end32, int tid,
+                                                MaskStage& ms) {
+  const int nw = (end32 - base32 + 31) >> 5;
+#pragma unroll
+  for (int k = 0; k < kMaskStage; ++k) {
+    const int lw = tid + k * kThreads;
+    const int32_t wi = (base32 >> 5) + lw;
+    ms.w[k] = (lw < nw && wi < mask_words) ? gmem(mrow)[wi] : 0u;
+  }
+}
+__device__ __forceinline__ void store_mask_stage(const MaskStage& ms, int32_t mask_words,
+                                                 int32_t mask_bits, int32_t tail, int32_t base32,
+                                                 int32_t end32, int tid, uint32_t* mw) {
+  const int nw = (end32 - base32 + 31) >> 5;
+#pragma unroll
+  for (int k = 0; k < kMaskStage; ++k) {
+    const int lw = tid + k * kThreads;
+    if (lw >= nw) continue;
+    const int32_t wi = (base32 >> 5) + lw;
+    const bool word_in = wi < mask_words;
+    int32_t nin = word_in ? mask_bits - wi * 32 : 0;  // leading tokens the mask covers
+    nin = nin < 0 ? 0 : (nin > 32 ? 32 : nin);
+    const uint32_t in_mask = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
+    mw[lw] = (ms.w[k] & in_mask) | (tail == LSAMP_MASK_TAIL_KEEP ? ~in_mask : 0u);
+  }
+}
+// The staged allow bits of the N tokens from slice offset li0 (N-aligned).
+__device__ __forceinline__ uint32_t staged_allow_bits(const uint32_t* mw, int32_t li0, int N) {
+  const uint32_t full = (N == 32) ? 0xffffffffu : ((1u << N) - 1u);
+  return (mw[li0 >> 5] >> (uint32_t)(li0 & 31)) & full;
+}
+
 __device__ __forceinline__ bool mask_allows(const uint32_t* mrow, int32_t mask_words,
                                             int32_t mask_bits, int32_t tail, int32_t i) {
   return mask_allow_bits(mrow, mask_words, mask_bits, tail, i, 1) != 0u;

@@ -370,11 +370,17 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   EntryPrefetch<> ep;
   entry_bounds(P, row, ep);
   prefetch_entries(P, tid, ep);
+  // the slice's grammar-mask words, staged in LDS (the candidate area, idle
+  // until the extraction) before the first pass
+  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
+  MaskStage ms;
+  if (mrow) load_mask_stage(mrow, P.mask_words, base32, end32, tid, ms);
+  uint32_t* const mw = reinterpret_cast<uint32_t*>(L.cand);
+  static_assert(sizeof(L.cand) >= kSliceWords * sizeof(uint32_t), "staged mask words fit");
 #if LSAMP_TOPK_REST_AFTER_MARK == 0
   load_quads(std::integral_constant<int, kFirst>{}, std::integral_constant<int, Q>{});
 #endif
   const RowCtx c = make_ctx(P.semantics, prm);
-  const uint32_t* mrow = P.bitmask ? P.bitmask + (size_t)row * (size_t)P.mask_words : nullptr;
   // (defaults the compiler cannot see as constants: with constant ones it
   // moves the later `+ 1`s into this branch, where they would wait for the
   // atomic at once)
@@ -410,6 +416,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
   EntryMarks<decltype(ep)::K> em;
   float emax = kNegInf;
+  if (mrow) store_mask_stage(ms, P.mask_words, P.mask_bits, P.mask_tail, base32, end32, tid, mw);
   mark_slice_entries<DT>(P, c, prm, mrow, rowp, base, end, se, ep, tid, em, emax);
 #if LSAMP_TOPK_REST_AFTER_MARK != 0
   load_quads(std::integral_constant<int, kFirst>{}, std::integral_constant<int, Q>{});
@@ -517,7 +524,7 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
     // (the registers are masked in place, unless LP keeps them raw)
     uint4 vcopy = vin;
     uint4& v = LP ? vcopy : vin;
-    if (mrow) ex |= ~mask_allow_bits(mrow, P.mask_words, P.mask_bits, P.mask_tail, i0, N) & FULL;
+    if (mrow) ex |= ~staged_allow_bits(mw, i0 - base32, N) & FULL;
     if constexpr (N == 8) {
       constexpr uint32_t M = 0x7fff7fffu;
       const uint32_t hw = pk_max_u16(pk_max_u16(v.x & M, v.y & M), pk_max_u16(v.z & M, v.w & M));
