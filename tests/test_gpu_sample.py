@@ -231,3 +231,33 @@ def test_deterministic_replay(ctx):
         b = run_gpu(ctx, cfg)
         assert np.array_equal(a["tokens"], b["tokens"])
         assert np.array_equal(a["stats"], b["stats"])
+
+
+@pytest.mark.parametrize("dtype", [_ffi.DTYPE_F32, _ffi.DTYPE_BF16])
+def test_mask_ending_inside_a_later_slice(ctx, dtype):
+    # a mask shorter than the vocabulary (100,003 bits: not a whole word)
+    # ends inside a later slice, so the allow words each slice stages before
+    # its first pass change policy mid-word and past the mask; strong tokens
+    # past the mask are kept only under the KEEP tail.  Histogram-path rows
+    # (the fused kernel) and top-k rows (the top-k kernel) both stage them.
+    rng = np.random.default_rng(17 + dtype)
+    V, R, nb = 151936, 4, 100003
+    words = (nb + 31) // 32
+    x = rng.normal(0, 3, (R, V)).astype(np.float32)
+    x[:, 120000:120010] += 9.0
+    x[:, nb - 3:nb + 3] += 8.0  # around the mask's last bit
+    bits = rng.random((R, words * 32)) < 0.3
+    bits[:, nb - 3:nb] = True
+    bm = np.packbits(bits, axis=1, bitorder="little").view(np.uint32).copy()
+    xin = x if dtype == _ffi.DTYPE_F32 else W.f32_to_bf16_bits(x)
+    for tail in (_ffi.MASK_TAIL_KEEP, _ffi.MASK_TAIL_FORBID):
+        for pkw in (dict(temperature=0.8, top_p=0.9), dict(temperature=0.8, top_k=40, top_p=0.95)):
+            p = W.resolve_cbv2(vocab=V, **pkw)
+            cfg = small_cfg(_ffi.SEM_CBV2, xin, [p] * R, rng.random(R, dtype=np.float32),
+                            dtype=dtype, bitmask=bm, mask_bits=nb, mask_tail=tail)
+            g = run_gpu(ctx, cfg)
+            compare(cfg, g, run_oracle(cfg), label=f"mask to {nb} tail {tail} {pkw}")
+            if tail == _ffi.MASK_TAIL_FORBID:
+                assert (g["tokens"] < nb).all(), g["tokens"]
+            else:
+                assert (g["tokens"] >= nb).any(), g["tokens"]
