@@ -76,3 +76,25 @@ def test_status_clear_after_default_mode(ctx):
     cfg = W.config2(rows=16)
     run_gpu(ctx, cfg)
     assert ctx.read_status() == 0
+
+
+def test_fused_equals_split_past_the_row_order():
+    # 1,100 rows: more than the fused kernel orders (histogram-path rows
+    # first) at its start, so its work-groups take the tasks in row order
+    import torch
+    from lsamp.api import Context
+    rng = np.random.default_rng(23)
+    V, B = 8192, 1100
+    c = Context(0, max_rows=B, max_vocab=V)
+    try:
+        x = rng.normal(0, 3, (B, V)).astype(np.float32)
+        params = [W.resolve_cbv2(temperature=[0.0, 0.8, 1.1][r % 3], top_k=[0, 30, 300][(r // 3) % 3],
+                                 top_p=[1.0, 0.9][r % 2], vocab=V) for r in range(B)]
+        cfg = dict(semantics=_ffi.SEM_CBV2, dtype=_ffi.DTYPE_F32, rows=B, vocab=V, logits=x,
+                   params=W._params(params), uniforms=rng.random(B, dtype=np.float32))
+        f, s = _both_modes(c, cfg)
+        _assert_same(f, s, "past the row order")
+        assert c.last_launch()["fused"] == 0  # (the split launch ran last)
+    finally:
+        torch.cuda.synchronize()
+        c.close()
