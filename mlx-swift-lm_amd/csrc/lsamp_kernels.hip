@@ -2195,13 +2195,19 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
     }
     __syncthreads();
   }
-  uint32_t t;
-  for (;;) {
-    if (threadIdx.x == 0)
-      L.task = __hip_atomic_fetch_add(ws.tasks, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    t = L.task;
-    __syncthreads();
+  // The first task of work-group b is task b (the first takes of the grid
+  // would return 0 .. grid - 1 in some order, all at once on one counter);
+  // later takes count from the grid's size.
+  uint32_t t = blockIdx.x;
+  for (bool first = true;; first = false) {
+    if (!first) {
+      if (threadIdx.x == 0)
+        L.task = gridDim.x + __hip_atomic_fetch_add(ws.tasks, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      t = L.task;
+      __syncthreads();
+    }
     if (t >= total) break;
     // (through empty asm: nothing derived from the arguments is hoisted out
     // of the loop and held across tasks)
@@ -2211,8 +2217,9 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
     run_task<DT, kFused>(wsr, Pr, ordered ? (int)order[q] : q, (int)(t % (uint32_t)G), L);
     __syncthreads();
   }
-  // every work-group ends with one failed take: the last of those returns
-  // the counter to zero for the next step
+  // every work-group ends with one failed take (the counter then holds
+  // total - grid + grid): the last of those returns it to zero for the next
+  // step
   if (threadIdx.x == 0 && t == total + gridDim.x - 1u) st_coherent(ws.tasks, 0u);
 }
 
