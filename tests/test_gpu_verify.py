@@ -165,3 +165,20 @@ def test_residual_across_parts(ctx, dtype, V, pkw):
         g, o = run_both(ctx, _ffi.VERIFY_RESIDUAL, t, d, drafts, params, u, dtype)
         check(g, o, f"parts dtype {dtype} V {V} {pkw} rep {rep}")
     assert (g["accepted"] < Wn - 1).any(), "no rejection: the residual draw was not exercised"
+
+
+@pytest.mark.parametrize("S,Wn,V,pkw", [
+    (5, 2, 16385, dict(temperature=0.9, top_p=0.9)),   # one draft; a last part of one token
+    (4, 6, 2049, dict(temperature=1.1)),               # a row inside one wave's first step
+    (3, 6, 40000, dict(temperature=0.7, top_k=30)),    # long windows, later rejections
+])
+def test_residual_window_and_vocab_edges(ctx, S, Wn, V, pkw):
+    rng = np.random.default_rng(V + Wn)
+    t = rng.normal(0, 2.5, (S, Wn, V)).astype(np.float32)
+    d = (t[:, : Wn - 1] + rng.normal(0, 1.5, (S, Wn - 1, V))).astype(np.float32)
+    t, d = W.f32_to_bf16_bits(t), W.f32_to_bf16_bits(d)
+    params = W._params([W.resolve_cbv2(vocab=V, **pkw)] * S)
+    drafts = draw_drafts(d, _ffi.DTYPE_BF16, params, rng.random((S, Wn - 1), dtype=np.float32))
+    u = rng.random((S, Wn), dtype=np.float32)
+    g, o = run_both(ctx, _ffi.VERIFY_RESIDUAL, t, d, drafts, params, u, _ffi.DTYPE_BF16)
+    check(g, o, f"S{S} W{Wn} V{V} {pkw}")
