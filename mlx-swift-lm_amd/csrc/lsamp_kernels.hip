@@ -335,26 +335,35 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
           msum[k] = L.u.m.mass[64 * k + l];
         }
       } else {
-        // deeper batch: read the slices' bins already aligned
+        // deeper batch: read the slices' bins already aligned, four slices'
+        // requests out before the first is used (one round trip a batch up
+        // to four slices)
 #pragma unroll
         for (int k = 0; k < kBlk; ++k) {
           cnt[k] = 0u;
           msum[k] = 0ull;
         }
-        for (int s = 0; s < G; ++s) {
-          const int32_t off = row_top - __shfl(htop, s, 64);
-          if (__shfl(hn, s, 64) <= 0) continue;
-          uint64_t ws4[kBlk];
+        constexpr int kGrp = 4;
+        for (int s0 = 0; s0 < G; s0 += kGrp) {
+          uint64_t wg[kGrp][kBlk];
 #pragma unroll
-          for (int k = 0; k < kBlk; ++k) {
-            const int i = 64 * kBlk * b + 64 * k + l - off;
-            ws4[k] = (i >= 0 && i < kBins) ? ld_coherent(&summ[s].hist[i]) : 0ull;
+          for (int d = 0; d < kGrp; ++d) {
+            const int s = s0 + d;
+            const bool live = s < G && __shfl(hn, s, 64) > 0;
+            const int32_t off = row_top - __shfl(htop, s, 64);
+#pragma unroll
+            for (int k = 0; k < kBlk; ++k) {
+              const int i = 64 * kBlk * b + 64 * k + l - off;
+              wg[d][k] = (live && i >= 0 && i < kBins) ? ld_coherent(&summ[s].hist[i]) : 0ull;
+            }
           }
 #pragma unroll
-          for (int k = 0; k < kBlk; ++k) {
-            cnt[k] += (uint32_t)(ws4[k] >> kCountShift);
-            msum[k] += ws4[k] & kMassMask;
-          }
+          for (int d = 0; d < kGrp; ++d)
+#pragma unroll
+            for (int k = 0; k < kBlk; ++k) {
+              cnt[k] += (uint32_t)(wg[d][k] >> kCountShift);
+              msum[k] += wg[d][k] & kMassMask;
+            }
         }
       }
 #pragma unroll
