@@ -38,6 +38,8 @@ constexpr int kWgCandCap = 2048;
 constexpr int kVerifySpan = 2048;
 constexpr int kVerifyPart = kWaves * kVerifySpan;  // 16,384
 static_assert(kVerifySpan <= 65536, "queue entries are 16-bit offsets");
+// Wave spans of a maximum-vocabulary row.
+constexpr int kMaxVerifySpans = (kMaxVocab + kVerifyPart - 1) / kVerifyPart * kWaves;
 // Short-list rows (argmax, or top-k <= kShortMaxK): each slice lists the
 // tokens at or above a threshold taken from its threads' maxima (the quads
 // holding them staged whole in LDS, at most kQStage per thread) and
@@ -151,8 +153,8 @@ struct RankSlice {
   int32_t pad;
 };
 
-// A part's sums of the residual draw's two weights.
-struct VerifyPart {
+// A wave span's sums of the residual draw's two weights.
+struct VerifySpan {
   uint64_t res;  // max(0, p_t - p_d) at 2^-52
   uint64_t tgt;  // the target's kept weight
 };
@@ -177,7 +179,7 @@ struct Workspace {
   lsamp_row_stats* vstats;  // [max_rows]
   int32_t* vtokens;         // [max_rows]
   uint32_t* vflags;         // [max_rows]
-  VerifyPart* vpart;        // [max_rows][max_parts] per sequence
+  VerifySpan* vspan;        // [max_rows][max_parts][kWaves] per sequence
   uint32_t* vticket;        // [max_rows] per sequence: parts done (zeroed range)
 };
 
@@ -211,7 +213,7 @@ struct TopkWs {
 // the end of every step.
 struct WorkspaceLayout {
   size_t sum, rows, chunk, cand, klist, part, status, tasks, cc, as, asel, tticket, vtick;
-  size_t vstats, vtok, vfl, vpart, rpart, arank, vrp, vrl, smask, tpub, tepoch;
+  size_t vstats, vtok, vfl, vspan, rpart, arank, vrp, vrl, smask, tpub, tepoch;
   size_t zero_begin, zero_end, total;
 };
 constexpr size_t align256(size_t v) { return (v + 255) / 256 * 256; }
@@ -239,7 +241,7 @@ constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
   L.vstats = off; off = align256(off + R * sizeof(lsamp_row_stats));
   L.vtok = off;   off = align256(off + R * sizeof(int32_t));
   L.vfl = off;    off = align256(off + R * sizeof(uint32_t));
-  L.vpart = off;  off = align256(off + R * verify_parts(max_vocab) * sizeof(VerifyPart));
+  L.vspan = off;  off = align256(off + R * verify_parts(max_vocab) * kWaves * sizeof(VerifySpan));
   L.rpart = off;  off = align256(off + R * kRankMaxSlices * sizeof(RankSlice));
   L.arank = off;  off = align256(off + R * sizeof(uint32_t));
   L.vrp = off;    off = align256(off + R * sizeof(int32_t));
@@ -479,7 +481,7 @@ inline WorkspaceViews bind_workspace(char* b, int32_t max_rows, int32_t max_voca
   ws.vtokens = reinterpret_cast<int32_t*>(b + L.vtok);
   ws.vflags = reinterpret_cast<uint32_t*>(b + L.vfl);
   ws.max_parts = (int32_t)verify_parts((size_t)max_vocab);
-  ws.vpart = reinterpret_cast<VerifyPart*>(b + L.vpart);
+  ws.vspan = reinterpret_cast<VerifySpan*>(b + L.vspan);
   ws.vticket = reinterpret_cast<uint32_t*>(b + L.vtick);
   v.rank_part = reinterpret_cast<RankSlice*>(b + L.rpart);
   v.arrive_rank = reinterpret_cast<uint32_t*>(b + L.arank);

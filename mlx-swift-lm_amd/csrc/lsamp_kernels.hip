@@ -2451,17 +2451,16 @@ __device__ __forceinline__ int32_t residual_find(const ResidualRows& r, int32_t 
 // and probed draft token [s, j].  Grid: (parts, sequences).  Part 0 of a
 // sequence writes its outcome; in RESIDUAL mode, a sequence with a rejected
 // position draws from the residual there with all its parts: each part sums
-// both weights over its kVerifyPart tokens and publishes the sums, and the
-// last part to arrive picks the part whose run holds the draw, walks that
-// part again and writes the token.
+// both weights over each wave's kVerifySpan tokens and publishes the eight
+// spans' sums, and the last part to arrive picks the span whose run holds the
+// draw, walks that span again with one wave and writes the token.
 template <int DT>
 __global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, VerifyPlan Q) {
   __shared__ Candidate s_ct[kVerifyCandLds];
   __shared__ Candidate s_cd[kVerifyCandLds];
   __shared__ uint16_t s_queue[kWaves][kVerifySpan];
   __shared__ uint64_t s_wt[kWaves], s_wr[kWaves];
-  __shared__ int32_t s_rej, s_last, s_part, s_res, s_tok;
-  __shared__ uint64_t s_target;
+  __shared__ int32_t s_rej, s_last;
   const int part = blockIdx.x, s = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int W = Q.window, D = W - 1, S = Q.sequences;
@@ -2594,7 +2593,6 @@ __global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, Verify
   r.drow = reinterpret_cast<const char*>(Q.draft) + (size_t)(s * D + j) * V * es;
   r.V = V;
   r.vec = aligned16(r.trow);
-  if (tid == 0) s_tok = -1;
   __syncthreads();
   uint16_t* queue = s_queue[wv];
   const int P = Q.parts;
@@ -2611,92 +2609,75 @@ __global__ __launch_bounds__(kThreads) void k_verify_finish(Workspace ws, Verify
     }
   }
   __syncthreads();
-  if (tid == 0) {
-    uint64_t T = 0ull, R = 0ull;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      T += s_wt[w];
-      R += s_wr[w];
-    }
-    VerifyPart* vp = ws.vpart + (size_t)s * ws.max_parts + part;
-    st_coherent(&vp->res, R);
-    st_coherent(&vp->tgt, T);
-    drain_memory();
-    const uint32_t t =
-        __hip_atomic_fetch_add(&ws.vticket[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = t + 1u == (uint32_t)P;
-    if (last) st_coherent(&ws.vticket[s], 0u);
-    s_last = last ? 1 : 0;
-  }
-  __syncthreads();
-  if (!s_last) return;
-
-  // the last part: the draw's kind and target, and the part holding it
+  // publish the wave spans' sums (wave 0 stores them all, so that its own
+  // wait covers every store), then take the sequence's ticket
   if (tid < 64) {
-    const VerifyPart* vp = ws.vpart + (size_t)s * ws.max_parts;
-    uint64_t R = 0ull, T = 0ull;
-    for (int p0 = 0; p0 < P; p0 += 64) {
-      const int p = p0 + lane;
-      R += wave_sum(p < P ? ld_coherent(&vp[p].res) : 0ull);
-      T += wave_sum(p < P ? ld_coherent(&vp[p].tgt) : 0ull);
+    VerifySpan* vs = ws.vspan + ((size_t)s * ws.max_parts + part) * kWaves;
+    if (lane < kWaves) {
+      st_coherent(&vs[lane].res, s_wr[lane]);
+      st_coherent(&vs[lane].tgt, s_wt[lane]);
     }
-    const bool use_res = R != 0ull;
-    const uint64_t tot = use_res ? R : T;
-    int ps = -1;
-    uint64_t rel = 0ull;
-    if (tot) {
-      const uint64_t target = scaled_target(uniform_u32(u[D]), tot);
-      uint64_t cum = 0ull;
-      for (int p0 = 0; p0 < P && ps < 0; p0 += 64) {
-        const int p = p0 + lane;
-        const uint64_t v = p < P ? ld_coherent(use_res ? &vp[p].res : &vp[p].tgt) : 0ull;
-        const uint64_t incl = wave_incl_scan(v);
-        const uint64_t before = cum + incl - v;
-        const uint64_t hm = __ballot(v && before <= target && target < before + v);
-        if (hm) {
-          const int hl = __builtin_ctzll(hm);
-          ps = p0 + hl;
-          rel = target - read_lane(before, hl);
-        }
-        cum += read_lane(incl, 63);
-      }
-    }
+    drain_memory();
     if (lane == 0) {
-      s_part = ps;
-      s_target = rel;
-      s_res = use_res ? 1 : 0;
+      const uint32_t t =
+          __hip_atomic_fetch_add(&ws.vticket[s], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = t + 1u == (uint32_t)P;
+      if (last) st_coherent(&ws.vticket[s], 0u);
+      s_last = last ? 1 : 0;
     }
   }
   __syncthreads();
-  const int ps = s_part;
-  if (ps >= 0) {
-    const bool use_res = s_res != 0;
-    const uint64_t t = s_target;
-    const int32_t q0 = ps * kVerifyPart + wv * kVerifySpan;
-    const int n = residual_screen<DT>(r, q0, queue, lane);
-    uint64_t st, sr;
-    residual_sums<DT>(r, q0, queue, n, lane, use_res, st, sr);
-    const uint64_t mine = wave_sum(use_res ? sr : st);
-    if (lane == 0) s_wt[wv] = mine;
-    __syncthreads();
-    uint64_t cum = 0ull, wb = 0ull;
-    int wsel = -1;
+  if (!s_last || wv != 0) return;
+
+  // the last part, wave 0: the draw's kind and target from every span's sums
+  // (span e covers tokens from e * kVerifySpan, so the spans run in id
+  // order), then the token inside the span whose run holds the target
+  constexpr int kE = (kMaxVerifySpans + 63) / 64;
+  const VerifySpan* vs = ws.vspan + (size_t)s * ws.max_parts * kWaves;
+  const int E = P * kWaves;
+  uint64_t vr[kE], vt[kE];
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const uint64_t v = s_wt[w];
-      if (wsel < 0 && v && cum <= t && t < cum + v) {
-        wsel = w;
-        wb = cum;
-      }
-      cum += v;
-    }
-    if (wv == wsel) {
-      const int32_t f = residual_find<DT>(r, q0, queue, n, lane, use_res, t - wb);
-      if (lane == 0) s_tok = f;
-    }
-    __syncthreads();
+  for (int k = 0; k < kE; ++k) {
+    const int e = k * 64 + lane;
+    vr[k] = e < E ? ld_coherent(&vs[e].res) : 0ull;
+    vt[k] = e < E ? ld_coherent(&vs[e].tgt) : 0ull;
   }
-  if (tid == 0) tok[j] = s_tok;
+  uint64_t R = 0ull, T = 0ull;
+#pragma unroll
+  for (int k = 0; k < kE; ++k) {
+    R += vr[k];
+    T += vt[k];
+  }
+  R = wave_sum(R);
+  T = wave_sum(T);
+  const bool use_res = R != 0ull;
+  const uint64_t tot = use_res ? R : T;
+  int32_t f = -1;
+  if (tot) {
+    const uint64_t target = scaled_target(uniform_u32(u[D]), tot);
+    uint64_t cum = 0ull, rel = 0ull;
+    int es = -1;
+#pragma unroll
+    for (int k = 0; k < kE; ++k) {
+      if (k * 64 >= E) break;
+      const uint64_t v = use_res ? vr[k] : vt[k];
+      const uint64_t incl = wave_incl_scan(v);
+      const uint64_t before = cum + incl - v;
+      const uint64_t hm = __ballot(v && before <= target && target < before + v);
+      if (hm && es < 0) {
+        const int hl = __builtin_ctzll(hm);
+        es = k * 64 + hl;
+        rel = target - read_lane(before, hl);
+      }
+      cum += read_lane(incl, 63);
+    }
+    if (es >= 0) {
+      const int32_t q0 = es * kVerifySpan;
+      const int n = residual_screen<DT>(r, q0, s_queue[0], lane);
+      f = residual_find<DT>(r, q0, s_queue[0], n, lane, use_res, rel);
+    }
+  }
+  if (lane == 0) tok[j] = f;
 }
 
 template <int DT>
