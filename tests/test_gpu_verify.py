@@ -182,3 +182,34 @@ def test_residual_window_and_vocab_edges(ctx, S, Wn, V, pkw):
     u = rng.random((S, Wn), dtype=np.float32)
     g, o = run_both(ctx, _ffi.VERIFY_RESIDUAL, t, d, drafts, params, u, _ffi.DTYPE_BF16)
     check(g, o, f"S{S} W{Wn} V{V} {pkw}")
+
+
+@pytest.mark.parametrize("sigma,pkw", [(1.0, dict(temperature=1.5)),
+                                        (3.0, dict(temperature=1.0, top_p=0.9))])
+def test_residual_at_the_maximum_vocabulary(sigma, pkw):
+    # V = 524,288: 32 parts of eight 2,048-token spans each, so the finishing
+    # wave scans all 256 spans' sums (four per lane); these rows put the
+    # residual draw past token 262,144, in the spans of the third and fourth
+    # lane rounds.  (Top-p over flat N(0, 1) rows would leave more than 4,096
+    # tokens in the cut bin at this width: such rows fail closed by design.)
+    import torch
+    from lsamp.api import Context
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    V, S, Wn = 524288, 6, 3
+    rng = np.random.default_rng(524288 + len(pkw))
+    t = rng.normal(0, sigma, (S, Wn, V)).astype(np.float32)
+    d = (t[:, : Wn - 1] + rng.normal(0, 1.5, (S, Wn - 1, V))).astype(np.float32)
+    t, d = W.f32_to_bf16_bits(t), W.f32_to_bf16_bits(d)
+    params = W._params([W.resolve_cbv2(vocab=V, **pkw)] * S)
+    drafts = draw_drafts(d, _ffi.DTYPE_BF16, params, rng.random((S, Wn - 1), dtype=np.float32))
+    u = rng.random((S, Wn), dtype=np.float32)
+    c = Context(0, max_rows=S * (2 * Wn - 1), max_vocab=V)
+    try:
+        for rep in range(2):
+            g, o = run_both(c, _ffi.VERIFY_RESIDUAL, t, d, drafts, params, u, _ffi.DTYPE_BF16)
+            check(g, o, f"V {V} {pkw} rep {rep}")
+    finally:
+        c.close()
+    rej = [s for s in range(S) if o["accepted"][s] < Wn - 1]
+    assert rej, "no rejection: the residual draw was not exercised"
+    assert max(int(o["tokens"][s][o["accepted"][s]]) for s in rej) >= 262144
