@@ -433,8 +433,12 @@ typedef struct lsamp_logprobs_args {
  * (LogitsPipelineV2.process :307-314, Evaluate.swift:800-806), gathered for
  * the sampled token and the top_k best tokens (CBv2Logprobs.gather,
  * LogitsPipelineV2.swift:534-549; DeferredTokenLogProbabilities,
- * Evaluate.swift:818-853).  The log-sum-exp is NaN when a logit is NaN,
- * +inf when one is +inf, -inf when all are -inf. */
+ * Evaluate.swift:818-853).  A row with a NaN or +inf logit, or with every
+ * logit -inf, has no finite log-sum-exp and defines no log-probabilities: it
+ * fails closed with LSAMP_ROW_NONFINITE, top_ids -1 and NaN values and chosen
+ * log-probability, as the reference fails a non-finite row
+ * (CBv2NonFiniteLogits.swift:8-34).  A row holding -inf beside finite logits
+ * is flagged NONFINITE and keeps its (finite or -inf) log-probabilities. */
 lsamp_status lsamp_logprobs(lsamp_context* ctx, const lsamp_logprobs_args* args, void* stream);
 
 /* ---- device-side penalty state ---------------------------------------------

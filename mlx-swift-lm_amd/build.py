@@ -18,6 +18,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(PKG)
@@ -49,17 +50,24 @@ def run(cmd):
     subprocess.run(cmd, check=True)
 
 
-def build_lib(verbose_asm: bool = False) -> str:
+def build_lib(verbose_asm: bool = False, jobs: int = 0) -> str:
+    """Compile every source (in parallel, `jobs` at once; 0 = up to 8) and
+    link liblsamp.so."""
     os.makedirs(LIB_DIR, exist_ok=True)
-    objs = []
+    cmds, objs = [], []
     for src in SOURCES_HIP:
         obj = os.path.join(LIB_DIR, src.replace(".hip", ".o"))
-        run([HIPCC, "-x", "hip", *COMMON, *DEVICE, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC, "-x", "hip", *COMMON, *DEVICE, "-c", os.path.join(CSRC, src), "-o", obj])
         objs.append(obj)
     for src in SOURCES_CPP:
         obj = os.path.join(LIB_DIR, src.replace(".cpp", ".o"))
-        run([HIPCC, *COMMON, "-D__HIP_PLATFORM_AMD__", "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([HIPCC, *COMMON, "-D__HIP_PLATFORM_AMD__", "-c", os.path.join(CSRC, src),
+                     "-o", obj])
         objs.append(obj)
+    jobs = jobs or min(len(cmds), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        for f in [pool.submit(run, c) for c in cmds]:
+            f.result()
     tmp = LIB + ".tmp"
     run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)

@@ -499,11 +499,12 @@ __global__ __launch_bounds__(kThreads) void k_rank(RankPlan P) {
       L.lse = lse;
       uint32_t of = (rflags & kRankNonfinite) ? LSAMP_ROW_NONFINITE : 0u;
       if (P.tokens) {
+        // a row whose log-sum-exp is not finite fails closed (NaN)
         float c = __builtin_nanf("");
-        if (tok >= 0 && tok < P.vocab)
-          c = (float)((double)bits_value<DT>(L.tok_bits) - lse);
-        else
+        if (tok < 0 || tok >= P.vocab)
           of |= LSAMP_ROW_TOKEN_RANGE;
+        else if (__builtin_isfinite(lse))
+          c = (float)((double)bits_value<DT>(L.tok_bits) - lse);
         P.chosen[row] = c;
       }
       if (P.row_flags) P.row_flags[row] = of;
@@ -512,10 +513,16 @@ __global__ __launch_bounds__(kThreads) void k_rank(RankPlan P) {
   }
   __syncthreads();
   if (tid < k) {
+    // Log-probabilities of a row whose log-sum-exp is not finite (a NaN or
+    // +inf logit, or every logit -inf) are undefined: the row fails closed
+    // with ids -1 and NaN values, as the reference fails a non-finite row
+    // (CBv2NonFiniteLogits.swift:8-34).  The exact top-2 ranks it as is.
     const uint64_t v = L.out[tid];
     const float x = sort_key_value<DT>(v);
-    P.ids[(size_t)row * k + tid] = key_id(v);
-    P.values[(size_t)row * k + tid] = P.raw_values ? x : (float)((double)x - L.lse);
+    const bool closed = !P.raw_values && !__builtin_isfinite(L.lse);
+    P.ids[(size_t)row * k + tid] = closed ? -1 : key_id(v);
+    P.values[(size_t)row * k + tid] =
+        P.raw_values ? x : closed ? __builtin_nanf("") : (float)((double)x - L.lse);
   }
 }
 

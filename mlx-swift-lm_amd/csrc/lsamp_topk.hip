@@ -1293,9 +1293,12 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
           }
         }
         if (r < Kr) {
+          // a row whose log-sum-exp is not finite fails closed, as a list
+          // given up on does (CBv2NonFiniteLogits.swift:8-34)
+          const bool closed = gone || !__builtin_isfinite(lse);
           const size_t o = (size_t)row * (size_t)Kr + (size_t)r;
-          LPo.ids[o] = gone ? -1 : key_id(key);
-          LPo.values[o] = gone ? __builtin_nanf("") : (float)((double)key_y(key) - lse);
+          LPo.ids[o] = closed ? -1 : key_id(key);
+          LPo.values[o] = closed ? __builtin_nanf("") : (float)((double)key_y(key) - lse);
         }
       }
     }
@@ -1501,7 +1504,8 @@ __device__ __forceinline__ void topk_task(const SamplePlan& P, const TopkWs& T, 
   if constexpr (LP) {
     if (token >= 0 && !cx_ok) cx = load_scalar<DT>(rowp, token);
     if (l == 0)
-      LPo.chosen[row] = token >= 0 ? (float)((double)cx - lse) : __builtin_nanf("");
+      LPo.chosen[row] = token >= 0 && __builtin_isfinite(lse) ? (float)((double)cx - lse)
+                                                              : __builtin_nanf("");
   }
   if (l == 0) {
     if (lost) atomicOr(T.status, kStatusSpinTimeout);

@@ -1078,18 +1078,26 @@ int32_t lso_rank(const lso_rank_args* a) {
     uint32_t nonfinite = 0;
     const double lse = row_lse(row, a->dtype, V, a->col_stride, &nonfinite);
     uint32_t flags = nonfinite ? LSAMP_ROW_NONFINITE : 0u;
+    /* A row whose log-sum-exp is not finite (a NaN or +inf logit, or every
+     * logit -inf) defines no log-probabilities.  The reference fails such a
+     * row closed: CBv2NonFiniteLogits.flags (CBv2NonFiniteLogits.swift:30-34)
+     * marks it and the request finishes with an error, committing nothing
+     * from it (:8-14).  Here it carries LSAMP_ROW_NONFINITE, ids -1 and NaN
+     * values.  The exact top-2 (raw values) still ranks such rows. */
+    const int closed = !a->raw_values && !isfinite(lse);
     for (int32_t j = 0; j < k; ++j) {
-      if (a->ids) a->ids[(size_t)r * k + j] = ti[j];
+      if (a->ids) a->ids[(size_t)r * k + j] = closed ? -1 : ti[j];
       if (a->values)
-        a->values[(size_t)r * k + j] = a->raw_values ? tv[j] : (float)((double)tv[j] - lse);
+        a->values[(size_t)r * k + j] =
+            a->raw_values ? tv[j] : closed ? NAN : (float)((double)tv[j] - lse);
     }
     if (a->tokens) {
       const int32_t t = a->tokens[r];
       float c = NAN;
-      if (t >= 0 && t < V)
-        c = (float)((double)load_logit(row, a->dtype, (int64_t)t * a->col_stride) - lse);
-      else
+      if (t < 0 || t >= V)
         flags |= LSAMP_ROW_TOKEN_RANGE;
+      else if (!closed)
+        c = (float)((double)load_logit(row, a->dtype, (int64_t)t * a->col_stride) - lse);
       if (a->chosen) a->chosen[r] = c;
     }
     if (a->row_flags) a->row_flags[r] = flags;

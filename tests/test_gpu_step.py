@@ -174,6 +174,9 @@ def test_step_logprobs_in_the_sampling_pass(ctx, dtype, vocab, k):
         bad = np.nonzero((ids != ref["ids"]).any(axis=1))[0]
         assert bad.size == 0, f"ids differ in rows {bad}: {ids[bad[:2]]} vs {ref['ids'][bad[:2]]}"
         assert close_logprobs(out["top_values"].cpu().numpy(), ref["values"])
+        # NaN, +inf and all-NaN rows have no finite log-sum-exp: they fail closed
+        assert (ids[[1, 2, 6]] == -1).all() and (ids[[0, 3, 4, 5, 7, 8]] >= 0).all()
+        assert np.isnan(out["top_values"].cpu().numpy()[[1, 2, 6]]).all()
     assert close_logprobs(out["chosen"].cpu().numpy(), ref["chosen"])
     # and the second-pass entry point on the same tokens agrees
     lp = ctx.logprobs(lt, tokens=out["tokens"], top_k=k)

@@ -159,15 +159,41 @@ def test_nonfinite_rows_and_token_range():
                   [-INF, -INF, -INF, -INF],
                   [0.5, 0.25, -1.0, 3.0]], np.float32)
     r = O.rank(x, dtype=F32, k=2, raw_values=False, tokens=[2, 1, 0, 4])
-    assert math.isnan(r["lse"][0]) and np.isnan(r["values"][0]).all() and math.isnan(r["chosen"][0])
-    assert r["lse"][1] == INF and math.isnan(r["chosen"][1])     # inf - inf
-    assert r["ids"][1].tolist() == [1, 2] and math.isnan(r["values"][1, 0])
-    assert r["values"][1, 1] == -INF
-    assert r["lse"][2] == -INF and math.isnan(r["chosen"][2])
+    assert math.isnan(r["lse"][0])
+    assert r["lse"][1] == INF
+    assert r["lse"][2] == -INF
+    # rows whose log-sum-exp is not finite fail closed (CBv2NonFiniteLogits.swift:8-34):
+    # no ids, NaN values and chosen log-probability, the NONFINITE flag
+    for i in range(3):
+        assert r["ids"][i].tolist() == [-1, -1], i
+        assert np.isnan(r["values"][i]).all() and math.isnan(r["chosen"][i]), i
+    assert r["ids"][3].tolist() == [3, 0]
     assert math.isnan(r["chosen"][3])                           # token 4 is out of range
     F = _ffi
     assert r["row_flags"].tolist() == [F.ROW_NONFINITE, F.ROW_NONFINITE, F.ROW_NONFINITE,
                                        F.ROW_TOKEN_RANGE]
+
+
+def test_nonfinite_row_with_finite_lse_keeps_its_logprobs():
+    """A row holding -inf beside finite logits has a finite log-sum-exp: it is
+    flagged NONFINITE (CBv2NonFiniteLogits.swift:30-34 flags any +-inf) but its
+    log-probabilities are defined and written (-inf for the -inf token)."""
+    x = np.array([[1.0, -INF, 0.0, -2.0]], np.float32)
+    r = O.rank(x, dtype=F32, k=4, raw_values=False, tokens=[1])
+    lse = math.log(math.exp(1.0) + 1.0 + math.exp(-2.0))
+    assert r["ids"][0].tolist() == [0, 2, 3, 1]
+    assert np.allclose(r["values"][0, :3], np.array([1.0, 0.0, -2.0]) - lse, atol=1e-7)
+    assert r["values"][0, 3] == -INF and r["chosen"][0] == -INF
+    assert r["row_flags"].tolist() == [_ffi.ROW_NONFINITE]
+
+
+def test_top2_still_ranks_nonfinite_rows():
+    """The exact top-2 (raw values) is not a log-probability: it ranks NaN and
+    infinite rows by the reference order (CBv2TopTwo.swift:29-47)."""
+    x = np.array([[0.0, NAN, 1.0, 2.0], [0.0, INF, 1.0, -INF], [-INF, -INF, -INF, -INF]],
+                 np.float32)
+    r = O.rank(x, dtype=F32, k=2, raw_values=True)
+    assert r["ids"].tolist() == [[3, 2], [1, 2], [0, 1]]
 
 
 @pytest.mark.parametrize("dtype", [BF16, F16])
