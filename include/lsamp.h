@@ -344,12 +344,7 @@ lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode);
 #define LSAMP_STATUS_PENALTY_CAPACITY 2u
 lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
 
-/* Test hook of the bounded waits (the fused arrangement's and the top-k
- * kernel's finalizer), process-wide on `device`: polls > 0 makes every wait's
- * target unreachable and gives it up after `polls` polls, so the fail-closed
- * path (LSAMP_ROW_TIMEOUT) runs while every kernel exits normally; 0 restores
- * normal waits.  Synchronous; not for use while other calls are in flight. */
-lsamp_status lsamp_set_spin_test(int32_t device, int32_t polls);
+/* (The test hook of the bounded waits is declared apart, in lsamp_testing.h.) */
 
 /* Launch shape of the context's last lsamp_sample call (diagnostics; no
  * device work): top-k with raw log-probabilities (3, lsamp_step), top-k (2),
@@ -440,6 +435,39 @@ typedef struct lsamp_logprobs_args {
  * (CBv2NonFiniteLogits.swift:8-34).  A row holding -inf beside finite logits
  * is flagged NONFINITE and keeps its (finite or -inf) log-probabilities. */
 lsamp_status lsamp_logprobs(lsamp_context* ctx, const lsamp_logprobs_args* args, void* stream);
+
+/* ---- the mlx-lm penalty processor on its own ------------------------------
+ * PenaltyProcessor.process (Evaluate.swift:687-693) as a separate pass, for a
+ * processor chain in which another processor runs between the penalties and
+ * the sampler (GenerationComponents.swift:112-141 composes penalty, then the
+ * custom processor, then suppression).  lsamp_sample applies the same
+ * penalties inside the sampling pass; use this entry point only when the
+ * penalized logits themselves are needed. */
+typedef struct lsamp_penalize_args {
+  int32_t rows;       /* >= 1                                                  */
+  int32_t vocab;      /* >= 1                                                  */
+  int32_t dtype;      /* lsamp_dtype of logits                                 */
+  int64_t row_stride; /* elements between logits rows (>= vocab)              */
+  const void* logits; /* [rows, vocab] device                                  */
+  const lsamp_row_params* params; /* [rows] device: repetition / presence /
+                                     frequency penalties (mlx-lm semantics)   */
+  const int32_t* penalty_row_ptr; /* [rows + 1] device (CSR), or the row starts
+                                     with penalty_row_len                     */
+  const int32_t* penalty_row_len; /* [rows] device or NULL                     */
+  const lsamp_penalty_entry* penalty_entries;
+  int32_t out_dtype;  /* the logits' dtype, or LSAMP_DTYPE_F32: MLX promotes
+                         to float32 when a frequency penalty is on
+                         (FrequencyPenaltyContext's float32 histogram,
+                         Evaluate.swift:649-658)                              */
+  void* out;          /* [rows, vocab] device, contiguous, out_dtype           */
+} lsamp_penalize_args;
+
+/* RepetitionContext, then PresencePenaltyContext in the logits' dtype with the
+ * penalty rounded to it, then FrequencyPenaltyContext in float32
+ * (Evaluate.swift:586-658), every other logit copied unchanged.  Entries
+ * follow lsamp_sample's rules (LSAMP_PEN_REPETITION, LSAMP_PEN_PRESENCE,
+ * count = occurrences in the frequency window). */
+lsamp_status lsamp_penalize(lsamp_context* ctx, const lsamp_penalize_args* args, void* stream);
 
 /* ---- device-side penalty state ---------------------------------------------
  * The incremental state of LogitsPipelineV2 (outputCounts, repWindow,

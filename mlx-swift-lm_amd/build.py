@@ -40,7 +40,7 @@ DEVICE = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 SOURCES_HIP = ["lsamp_kernels.hip", "lsamp_topk.hip", "lsamp_rank.hip", "lsamp_commit.hip",
-               "lsamp_mask.hip", "lsamp_noalloc.hip"]
+               "lsamp_mask.hip", "lsamp_noalloc.hip", "lsamp_penalize.hip"]
 SOURCES_CPP = ["lsamp_api.cpp"]
 HEADERS = ["lsamp_internal.h", "lsamp_device.h"]
 

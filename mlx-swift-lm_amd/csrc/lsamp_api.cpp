@@ -13,6 +13,7 @@
 #include <string>
 
 #include "lsamp_internal.h"
+#include "../../include/lsamp_testing.h"
 
 using namespace lsamp;
 
@@ -322,6 +323,7 @@ int64_t lsamp_abi_sizeof(const char* name) {
   if (!strcmp(name, "lsamp_commit_args")) return (int64_t)sizeof(lsamp_commit_args);
   if (!strcmp(name, "lsamp_mask_assemble_args")) return (int64_t)sizeof(lsamp_mask_assemble_args);
   if (!strcmp(name, "lsamp_logprobs_args")) return (int64_t)sizeof(lsamp_logprobs_args);
+  if (!strcmp(name, "lsamp_penalize_args")) return (int64_t)sizeof(lsamp_penalize_args);
   return -1;
 }
 
@@ -406,7 +408,7 @@ lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits) {
   return ok();
 }
 
-lsamp_status lsamp_set_spin_test(int32_t device, int32_t polls) {
+lsamp_status lsamp_test_set_spin_limit(int32_t device, int32_t polls) {
   if (polls < 0) return fail(LSAMP_ERR_INVALID_ARGUMENT, "polls %d is negative", polls);
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev)
@@ -618,6 +620,44 @@ lsamp_status lsamp_commit(lsamp_context* ctx, const lsamp_commit_args* a, void* 
     return fail(LSAMP_ERR_INVALID_ARGUMENT, "every table array and tokens are required");
   DeviceGuard guard(ctx->device);
   const int err = launch_commit(*a, stream);
+  if (err != 0)
+    return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
+  return ok();
+}
+
+// ------------------------------------------------------- penalty processor
+
+lsamp_status lsamp_penalize(lsamp_context* ctx, const lsamp_penalize_args* a, void* stream) {
+  if (!ctx) return fail(LSAMP_ERR_INVALID_ARGUMENT, "context is NULL");
+  if (!a) return fail(LSAMP_ERR_INVALID_ARGUMENT, "args is NULL");
+  if (a->rows <= 0 || a->vocab <= 0)
+    return fail(LSAMP_ERR_SHAPE, "rows %d / vocab %d must be positive", a->rows, a->vocab);
+  if (a->row_stride < a->vocab)
+    return fail(LSAMP_ERR_SHAPE, "row_stride %lld is below vocab %d", (long long)a->row_stride,
+                a->vocab);
+  if (a->dtype < LSAMP_DTYPE_F32 || a->dtype > LSAMP_DTYPE_F16)
+    return fail(LSAMP_ERR_DTYPE, "dtype %d is not a logits dtype", a->dtype);
+  if (a->out_dtype != a->dtype && a->out_dtype != LSAMP_DTYPE_F32)
+    return fail(LSAMP_ERR_DTYPE, "out_dtype %d must be the logits dtype %d or float32",
+                a->out_dtype, a->dtype);
+  if (!a->logits || !a->params || !a->out)
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "logits, params and out are required");
+  if ((a->penalty_entries != nullptr) != (a->penalty_row_ptr != nullptr))
+    return fail(LSAMP_ERR_INVALID_ARGUMENT, "penalty_row_ptr and penalty_entries go together");
+  PenalizePlan P{};
+  P.rows = a->rows;
+  P.vocab = a->vocab;
+  P.dtype = a->dtype;
+  P.out_dtype = a->out_dtype;
+  P.row_stride = a->row_stride;
+  P.logits = a->logits;
+  P.params = a->params;
+  P.row_ptr = a->penalty_row_ptr;
+  P.row_len = a->penalty_row_len;
+  P.entries = a->penalty_entries;
+  P.out = a->out;
+  DeviceGuard guard(ctx->device);
+  const int err = launch_penalize(P, stream);
   if (err != 0)
     return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));
   return ok();

@@ -280,7 +280,7 @@ struct RankPlan {
 
 // Sticky device status bits.
 constexpr uint32_t kStatusSpinTimeout = 1u;  // a fused-kernel barrier wait timed out
-// Test hook of the fused kernel's bounded waits (set by lsamp_set_spin_test):
+// Test hook of the fused kernel's bounded waits (set by lsamp_test_set_spin_limit):
 // 0 = normal; n > 0 = every wait's target is unreachable and it gives up after
 // n polls, so the fail-closed path runs while every kernel still exits.
 int set_spin_test(int32_t polls);
@@ -383,6 +383,22 @@ int launch_verify_finish(const Workspace& ws, const VerifyPlan& plan, void* stre
 int launch_rank(const RankPlan& plan, void* stream);
 // Incremental penalty-state update after a draw (lsamp_commit.hip).
 int launch_commit(const lsamp_commit_args& args, void* stream);
+
+// lsamp_penalize (lsamp_penalize.hip): the mlx-lm penalty processor's output.
+struct PenalizePlan {
+  int32_t rows;
+  int32_t vocab;
+  int32_t dtype;
+  int32_t out_dtype;
+  int64_t row_stride;
+  const void* logits;
+  const lsamp_row_params* params;
+  const int32_t* row_ptr;
+  const int32_t* row_len;
+  const lsamp_penalty_entry* entries;
+  void* out;
+};
+int launch_penalize(const PenalizePlan& plan, void* stream);
 
 // Per-position penalty entries of a penalty-aware verify window: row s * W + j
 // = sequence s's confirmed counts plus the drafts before chain position

@@ -39,7 +39,7 @@ using namespace dev;
 using namespace rowops;
 
 constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
-// lsamp_set_spin_test: > 0 makes every bounded wait's target unreachable and
+// lsamp_test_set_spin_limit: > 0 makes every bounded wait's target unreachable and
 // its limit this many polls (the waits' fail-closed path, under test)
 __device__ int32_t g_spin_test = 0;
 

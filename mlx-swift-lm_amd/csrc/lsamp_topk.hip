@@ -51,7 +51,7 @@ constexpr int kRStageCap = 256;  // raw quads staged for the raw candidate scan
 constexpr int kRCandCap = 256;   // raw candidates a slice keeps
 constexpr int kTkTauBins = 1024;  // thread-maximum histogram
 constexpr int kSpin = 1 << 20;   // polls before the finalizer gives a slice up
-// lsamp_set_spin_test: > 0 makes the finalizer's wait unreachable (no word
+// lsamp_test_set_spin_limit: > 0 makes the finalizer's wait unreachable (no word
 // counts as seen) and gives it up after this many polls
 __device__ int32_t g_topk_spin_test = 0;
 #ifndef LSAMP_TOPK_FIRST_QUADS

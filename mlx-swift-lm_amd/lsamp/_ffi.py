@@ -132,6 +132,22 @@ class CommitArgs(Structure):
     ]
 
 
+class PenalizeArgs(Structure):
+    _fields_ = [
+        ("rows", c_int32),
+        ("vocab", c_int32),
+        ("dtype", c_int32),
+        ("row_stride", c_int64),
+        ("logits", c_void_p),
+        ("params", c_void_p),
+        ("penalty_row_ptr", c_void_p),
+        ("penalty_row_len", c_void_p),
+        ("penalty_entries", c_void_p),
+        ("out_dtype", c_int32),
+        ("out", c_void_p),
+    ]
+
+
 class MaskAssembleArgs(Structure):
     _fields_ = [
         ("rows", c_int32),
@@ -301,8 +317,8 @@ def load_library(path: str | None = None):
     lib.lsamp_context_read_status.restype = c_int32
     lib.lsamp_sample_noalloc.argtypes = [POINTER(SampleArgs), c_void_p]
     lib.lsamp_sample_noalloc.restype = c_int32
-    lib.lsamp_set_spin_test.argtypes = [c_int32, c_int32]
-    lib.lsamp_set_spin_test.restype = c_int32
+    lib.lsamp_test_set_spin_limit.argtypes = [c_int32, c_int32]
+    lib.lsamp_test_set_spin_limit.restype = c_int32
     lib.lsamp_context_last_launch.argtypes = [c_void_p, POINTER(LaunchInfo)]
     lib.lsamp_context_last_launch.restype = c_int32
     lib.lsamp_context_set_timing.argtypes = [c_void_p, c_int32]
@@ -318,6 +334,8 @@ def load_library(path: str | None = None):
     lib.lsamp_propose.restype = c_int32
     lib.lsamp_commit.argtypes = [c_void_p, POINTER(CommitArgs), c_void_p]
     lib.lsamp_commit.restype = c_int32
+    lib.lsamp_penalize.argtypes = [c_void_p, POINTER(PenalizeArgs), c_void_p]
+    lib.lsamp_penalize.restype = c_int32
     lib.lsamp_mask_assemble.argtypes = [c_void_p, POINTER(MaskAssembleArgs), c_void_p]
     lib.lsamp_mask_assemble.restype = c_int32
     lib.lsamp_top2.argtypes = [c_void_p, POINTER(Top2Args), c_void_p]

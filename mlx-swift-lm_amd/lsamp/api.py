@@ -232,6 +232,47 @@ class Context:
         p.launch()
         return p.outputs()
 
+    def penalize(self, logits: torch.Tensor, params, *, row_ptr=None, entries=None,
+                 row_len=None, out_dtype: Optional[torch.dtype] = None,
+                 stream: Optional[int] = None) -> torch.Tensor:
+        """PenaltyProcessor.process (Evaluate.swift:687-693) on its own
+        (lsamp_penalize): [rows, vocab] logits in, the penalized logits out,
+        in the logits' dtype or (out_dtype=torch.float32, as a frequency
+        penalty promotes them) in float32."""
+        if logits.dim() != 2:
+            raise ValueError("logits must be [rows, vocab]")
+        rows, V = logits.shape
+        if logits.stride(1) != 1:
+            raise ValueError("logits rows must be contiguous")
+        dev = logits.device
+        out_dtype = logits.dtype if out_dtype is None else out_dtype
+        out = torch.empty((rows, V), dtype=out_dtype, device=dev)
+        pr = params if isinstance(params, torch.Tensor) else to_device_bytes(params_array(params), dev)
+        a = _ffi.PenalizeArgs()
+        a.rows, a.vocab, a.dtype = rows, V, LSAMP_DTYPE[logits.dtype]
+        a.row_stride = logits.stride(0) if rows > 1 else V
+        a.logits = logits.data_ptr()
+        a.params = pr.data_ptr()
+        keep = [pr]
+        if entries is not None:
+            rp = torch.from_numpy(np.ascontiguousarray(row_ptr, np.int32)).to(dev)
+            en = to_device_bytes(np.ascontiguousarray(entries, PENALTY_DTYPE), dev) \
+                if len(entries) else torch.zeros(16, dtype=torch.uint8, device=dev)
+            a.penalty_row_ptr, a.penalty_entries = rp.data_ptr(), en.data_ptr()
+            keep += [rp, en]
+            if row_len is not None:
+                rl = torch.from_numpy(np.ascontiguousarray(row_len, np.int32)).to(dev)
+                a.penalty_row_len = rl.data_ptr()
+                keep.append(rl)
+        a.out_dtype = LSAMP_DTYPE[out_dtype]
+        a.out = out.data_ptr()
+        s = stream if stream is not None else current_stream_handle(dev)
+        st = self.lib.lsamp_penalize(self.handle, ctypes.byref(a), ctypes.c_void_p(s))
+        if st != 0:
+            raise _ffi.LsampError(st, "lsamp_penalize")
+        out._lsamp_keep = keep  # the inputs stay alive until the output is consumed
+        return out
+
     def prepare_logprobs(self, logits: torch.Tensor, *, tokens=None, top_k: int = 0) -> "PreparedRank":
         return PreparedRank(self, logits, top2=False, tokens=tokens, top_k=top_k)
 

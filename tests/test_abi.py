@@ -7,6 +7,7 @@ factory rules and with the oracle's independent restatement.
 from __future__ import annotations
 
 import ctypes
+import glob
 import os
 import re
 
@@ -19,6 +20,7 @@ from lsamp import workloads as W
 
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(REPO, "include", "lsamp.h")
+HEADERS = sorted(glob.glob(os.path.join(REPO, "include", "*.h")))
 
 
 @pytest.fixture(scope="module")
@@ -27,7 +29,7 @@ def lib():
 
 
 def declared_functions():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
     return sorted(set(re.findall(r"\b(lsamp_[a-z0-9_]+)\s*\(", text)))
 
@@ -35,7 +37,8 @@ def declared_functions():
 def test_header_declares_the_entry_points():
     names = declared_functions()
     for required in ("lsamp_context_create", "lsamp_context_destroy", "lsamp_sample",
-                     "lsamp_verify", "lsamp_last_error", "lsamp_version"):
+                     "lsamp_verify", "lsamp_last_error", "lsamp_version", "lsamp_penalize",
+                     "lsamp_test_set_spin_limit"):
         assert required in names
 
 
@@ -49,7 +52,8 @@ def test_library_exports_every_declared_function(lib):
     ("lsamp_row_stats", _ffi.RowStats), ("lsamp_sample_args", _ffi.SampleArgs),
     ("lsamp_verify_args", _ffi.VerifyArgs), ("lsamp_mask_assemble_args", _ffi.MaskAssembleArgs),
     ("lsamp_generate_parameters", _ffi.GenerateParameters),
-    ("lsamp_cbv2_params", _ffi.Cbv2Params), ("lsamp_launch_info", _ffi.LaunchInfo)])
+    ("lsamp_cbv2_params", _ffi.Cbv2Params), ("lsamp_launch_info", _ffi.LaunchInfo),
+    ("lsamp_penalize_args", _ffi.PenalizeArgs)])
 def test_struct_layouts_agree(lib, name, struct):
     assert lib.lsamp_abi_sizeof(name.encode()) == ctypes.sizeof(struct)
 

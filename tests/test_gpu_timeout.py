@@ -1,7 +1,7 @@
 """Fail-closed rows when a bounded wait gives up (the fused arrangement's
 waits, and the top-k kernel's finalizer).
 
-The wait test hook (lsamp_set_spin_test) makes every wait's target
+The wait test hook (lsamp_test_set_spin_limit) makes every wait's target
 unreachable and its limit a few polls, forced from the host: every kernel
 still exits normally.  A row whose path waited must come back as token -1
 with LSAMP_ROW_TIMEOUT (the reference fails closed per row, in the same
@@ -45,12 +45,12 @@ def test_timed_out_rows_fail_closed_and_the_next_step_is_exact(ctx):
     waits = _waits(cfg["params"], cfg["vocab"])
     assert waits.any() and (~waits).any()
     ctx.read_status()  # clear
-    _ffi.check(lib.lsamp_set_spin_test(0, 16), "lsamp_set_spin_test")
+    _ffi.check(lib.lsamp_test_set_spin_limit(0, 16), "lsamp_test_set_spin_limit")
     try:
         g = run_gpu(ctx, cfg)
         status = ctx.read_status()
     finally:
-        _ffi.check(lib.lsamp_set_spin_test(0, 0), "lsamp_set_spin_test")
+        _ffi.check(lib.lsamp_test_set_spin_limit(0, 0), "lsamp_test_set_spin_limit")
     assert ctx.last_launch()["fused"] == 1
     assert status & _ffi.STATUS_SPIN_TIMEOUT
     tmo = (g["row_flags"] & _ffi.ROW_TIMEOUT) != 0
@@ -68,11 +68,11 @@ def test_split_mode_never_waits(ctx):
     cfg = W.config3(rows=16)
     o = run_oracle(cfg, threads=16)
     ctx.set_mode(_ffi.MODE_SPLIT)
-    _ffi.check(lib.lsamp_set_spin_test(0, 16), "lsamp_set_spin_test")
+    _ffi.check(lib.lsamp_test_set_spin_limit(0, 16), "lsamp_test_set_spin_limit")
     try:
         g = run_gpu(ctx, cfg)
     finally:
-        _ffi.check(lib.lsamp_set_spin_test(0, 0), "lsamp_set_spin_test")
+        _ffi.check(lib.lsamp_test_set_spin_limit(0, 0), "lsamp_test_set_spin_limit")
         ctx.set_mode(_ffi.MODE_AUTO)
     compare(cfg, g, o, label="split with the hook on")
     assert not (g["row_flags"] & _ffi.ROW_TIMEOUT).any()
@@ -87,12 +87,12 @@ def test_topk_finalizer_timeout_fails_closed_and_recovers(ctx):
     cfg = W.config2(rows=16)
     o = run_oracle(cfg, threads=16)
     ctx.read_status()  # clear
-    _ffi.check(lib.lsamp_set_spin_test(0, 16), "lsamp_set_spin_test")
+    _ffi.check(lib.lsamp_test_set_spin_limit(0, 16), "lsamp_test_set_spin_limit")
     try:
         g = run_gpu(ctx, cfg)
         status = ctx.read_status()
     finally:
-        _ffi.check(lib.lsamp_set_spin_test(0, 0), "lsamp_set_spin_test")
+        _ffi.check(lib.lsamp_test_set_spin_limit(0, 0), "lsamp_test_set_spin_limit")
     assert ctx.last_launch()["fused"] == 2
     assert status & _ffi.STATUS_SPIN_TIMEOUT
     assert ((g["row_flags"] & _ffi.ROW_TIMEOUT) != 0).all(), g["row_flags"]

@@ -18,7 +18,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from common import compare, run_gpu, run_oracle
+from common import compare, run_gpu, run_oracle, to_torch_logits
 from lsamp import _ffi
 from lsamp import workloads as W
 from lsamp.api import PENALTY_DTYPE
@@ -236,3 +236,37 @@ def test_top_p_cuts_inside_top_k(ctx, dtype):
                                      presence_penalty=0.4, vocab=V))
     u = rng.random(R).astype(np.float32)
     check(ctx, cfg_of(to_bits(x, dtype), dtype, params, u, entries=entries), f"top-p in top-k dt{dtype}")
+
+
+def test_params_host_mismatch_fails_closed(ctx):
+    """The host copy of the parameters chooses the top-k kernel; rows whose
+    device parameters it misdescribes (top-k 0, or past the kernel's limit)
+    fail closed with token -1 and LSAMP_ROW_OVERFLOW instead of running a
+    different sampler silently.  The other rows are exact, and the next
+    step, with matching parameters, is exact too (the rows' hand-off state
+    is not left behind)."""
+    import torch
+    from lsamp.api import to_device_bytes
+    cfg = W.config2(rows=16)
+    host = np.array(cfg["params"]).copy()
+    dev = host.copy()
+    dev[3]["top_k"] = 0        # histogram-path row: not the top-k kernel's
+    dev[9]["top_k"] = 100      # past kTopkMaxK
+    lt = to_torch_logits(cfg)
+    prep = ctx.prepare_sample(lt, host, semantics=cfg["semantics"], row_ptr=cfg["row_ptr"],
+                              entries=cfg["entries"], uniforms=cfg["uniforms"])
+    prep.params.copy_(to_device_bytes(dev, lt.device))
+    prep.launch()
+    torch.cuda.synchronize()
+    assert ctx.last_launch()["fused"] == 2
+    tok = prep.tokens.cpu().numpy()
+    flags = prep.row_flags.cpu().numpy().astype(np.uint32)
+    ref = run_oracle(cfg)
+    for r in range(16):
+        if r in (3, 9):
+            assert tok[r] == -1 and flags[r] & _ffi.ROW_OVERFLOW, (r, tok[r], flags[r])
+        else:
+            assert tok[r] == ref["tokens"][r] and flags[r] == ref["row_flags"][r], r
+    out = run_gpu(ctx, cfg)   # the next step, parameters consistent again
+    assert ctx.last_launch()["fused"] == 2
+    compare(cfg, out, ref, label="step after the mismatch")

@@ -88,3 +88,39 @@ def test_no_alloc_rejects_sizes_past_its_limits(ctx):
     args.rows, args.vocab = 2, 262145
     assert lib.lsamp_sample_noalloc(ctypes.byref(args), None) == _ffi.LSAMP_ERR_CAPACITY
     torch.cuda.synchronize()
+
+
+def test_no_alloc_under_graph_capture(ctx):
+    """A call captured in a HIP graph (after one eager call, which sets up the
+    device's scratch address outside the capture) replays exactly: three
+    replays with other work and synchronizations between them, each equal to
+    the context path bit for bit.  The counters the call clears are cleared
+    by a fill kernel, so the graph holds no memset node."""
+    import torch
+    from lsamp.api import current_stream_handle
+    lib = _ffi.load_library()
+    cfg = W.config2(rows=16)
+    ref_prep = _prepare(ctx, cfg)
+    ref_prep.launch()
+    ref = _outputs(ref_prep)
+    prep = _prepare(ctx, cfg)
+    st = lib.lsamp_sample_noalloc(ctypes.byref(prep.args),
+                                  ctypes.c_void_p(current_stream_handle(torch.device("cuda", 0))))
+    assert st == 0, _ffi.last_error()
+    _same(ref, _outputs(prep), "eager call before the capture")
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=s):
+        st = lib.lsamp_sample_noalloc(ctypes.byref(prep.args), ctypes.c_void_p(s.cuda_stream))
+    assert st == 0, _ffi.last_error()
+    other = W.config4(rows=8, vocab=40000)
+    for i in range(3):
+        # other work on the same scratch array between replays, and fresh
+        # garbage in the outputs the replay must overwrite
+        a, b = _run_both(ctx, other)
+        _same(a, b, f"other work before replay {i}")
+        prep.tokens.fill_(-7)
+        prep.processed.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        _same(ref, _outputs(prep), f"replay {i}")
