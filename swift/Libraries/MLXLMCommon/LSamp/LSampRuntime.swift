@@ -40,14 +40,21 @@ public protocol LSampRuntime: AnyObject {
     func deviceView(_ array: MLXArray) -> LSampDeviceView
     /// Device memory for the adapter's own buffers (allocated once, reused).
     func allocate(bytes: Int) -> UnsafeMutableRawPointer
+    /// Release memory from `allocate`, ordered on `stream` (as hipFreeAsync
+    /// is): work already enqueued there may still read or write it.
     func free(_ pointer: UnsafeMutableRawPointer)
     /// Copy host bytes to device memory, ordered on `stream`.
     func upload(_ source: UnsafeRawPointer, to destination: UnsafeMutableRawPointer, bytes: Int)
+    /// Copy device bytes to device memory, ordered on `stream`.
+    func copyDevice(_ source: UnsafeRawPointer, to destination: UnsafeMutableRawPointer, bytes: Int)
     /// Arrays of the runtime over device buffers (no copy; the buffer must
     /// stay valid until the array has been consumed).
     func int32Array(_ pointer: UnsafeMutableRawPointer, shape: [Int]) -> MLXArray
     func float32Array(_ pointer: UnsafeMutableRawPointer, shape: [Int]) -> MLXArray
     func boolArray(_ pointer: UnsafeMutableRawPointer, shape: [Int]) -> MLXArray
+    /// A logits array of `dtype` (bfloat16, float16 or float32) over a
+    /// device buffer (no copy).
+    func logitsArray(_ pointer: UnsafeMutableRawPointer, dtype: lsamp_dtype, shape: [Int]) -> MLXArray
 }
 
 /// A status check with the library's last error message (the xgrammar C ABI
@@ -96,6 +103,43 @@ final class LSampDeviceBuffer<T> {
     }
 
     deinit { runtime.free(raw) }
+}
+
+/// A device buffer that grows on demand: a larger request replaces it (the
+/// old memory is released through the runtime's stream-ordered free).
+final class LSampGrowingBuffer<T> {
+    let runtime: LSampRuntime
+    private(set) var buffer: LSampDeviceBuffer<T>
+
+    init(_ runtime: LSampRuntime, count: Int) {
+        self.runtime = runtime
+        buffer = LSampDeviceBuffer(runtime, count: count)
+    }
+
+    /// The buffer, at least `count` values long.
+    func reserve(_ count: Int) -> LSampDeviceBuffer<T> {
+        if count > buffer.count { buffer = LSampDeviceBuffer(runtime, count: max(count, 2 * buffer.count)) }
+        return buffer
+    }
+}
+
+/// Output buffers used in turn, so that a step's outputs stay valid while
+/// the next step runs (chained decode reads step N's tokens after step N+1
+/// has been enqueued).
+final class LSampOutputRing<T> {
+    private let slots: [LSampGrowingBuffer<T>]
+    private var next = 0
+
+    init(_ runtime: LSampRuntime, count: Int, depth: Int = 2) {
+        slots = (0 ..< depth).map { _ in LSampGrowingBuffer<T>(runtime, count: count) }
+    }
+
+    /// The next buffer in turn, at least `count` values long (a larger
+    /// request grows that slot).
+    func take(_ count: Int = 0) -> LSampDeviceBuffer<T> {
+        defer { next = (next + 1) % slots.count }
+        return slots[next].reserve(count)
+    }
 }
 
 /// Sparse penalty entries of one row: its distinct tokens with their counts
