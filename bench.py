@@ -485,19 +485,43 @@ def bench_masks(args):
     return 0
 
 
-def cpu_baseline(cfg, seconds):
-    """The oracle on whole steps of the headline workload (cpu_baseline_of)."""
+def tokens_check(baseline, gpu_tokens, seen):
+    """Compare the GPU's tokens for the workload's own input copy with the
+    oracle's from the baseline's whole-step runs; the result goes into the
+    baseline object and the caller's exit status."""
+    import numpy as np
+
+    want = seen.get("tokens")
+    if want is None:
+        baseline["tokens_match"] = None
+        return True
+    got = np.asarray(gpu_tokens)
+    bad = np.flatnonzero(got != want)
+    baseline["tokens_match"] = bool(bad.size == 0)
+    if bad.size:
+        baseline["tokens_mismatch_rows"] = bad[:8].tolist()
+    return bad.size == 0
+
+
+def cpu_baseline(cfg, seconds, gpu_tokens):
+    """The oracle on whole steps of the headline workload (cpu_baseline_of),
+    and its tokens checked against the GPU's (tokens_check)."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
 
+    seen = {}
+
     def step(threads, nrows):
         rp = cfg["row_ptr"]
-        O.sample(semantics=cfg["semantics"], logits=cfg["logits"][:nrows], dtype=cfg["dtype"],
-                 params=cfg["params"][:nrows], row_ptr=rp[:nrows + 1] - rp[0],
-                 entries=cfg["entries"][rp[0]:rp[nrows]], uniforms=cfg["uniforms"][:nrows],
-                 threads=threads)
+        res = O.sample(semantics=cfg["semantics"], logits=cfg["logits"][:nrows],
+                       dtype=cfg["dtype"], params=cfg["params"][:nrows],
+                       row_ptr=rp[:nrows + 1] - rp[0], entries=cfg["entries"][rp[0]:rp[nrows]],
+                       uniforms=cfg["uniforms"][:nrows], threads=threads)
+        if nrows == cfg["rows"]:
+            seen["tokens"] = res["tokens"]
 
-    return cpu_baseline_of(step, cfg["rows"], seconds)
+    base = cpu_baseline_of(step, cfg["rows"], seconds)
+    return base, tokens_check(base, gpu_tokens, seen)
 
 
 def bench_config(args, n):
@@ -575,6 +599,8 @@ def bench_config(args, n):
         sys.path.insert(0, os.path.join(REPO, "oracle"))
         import oracle as O
 
+        seen = {}
+
         def step(threads, nrows):
             r = slice(0, nrows)
             rp = cfg.get("row_ptr")
@@ -585,13 +611,18 @@ def bench_config(args, n):
             if cfg.get("bitmask") is not None:
                 kw2.update(bitmask=cfg["bitmask"][r], mask_bits=cfg["mask_bits"],
                            mask_tail=cfg.get("mask_tail", 0))
-            O.sample(semantics=cfg["semantics"], logits=cfg["logits"][r], dtype=cfg["dtype"],
-                     params=cfg["params"][r], uniforms=cfg["uniforms"][r], threads=threads, **kw2)
+            res = O.sample(semantics=cfg["semantics"], logits=cfg["logits"][r],
+                           dtype=cfg["dtype"], params=cfg["params"][r],
+                           uniforms=cfg["uniforms"][r], threads=threads, **kw2)
+            if nrows == B:
+                seen["tokens"] = res["tokens"]
 
         out["cpu_baseline"] = cpu_baseline_of(step, B, args.cpu_seconds)
+        ok = tokens_check(out["cpu_baseline"], preps[0].tokens.cpu().numpy(), seen)
+        out["tokens_match"] = out["cpu_baseline"]["tokens_match"]
     ctx.close()
     print(json.dumps(out))
-    return 0
+    return 0 if args.no_cpu or ok else 1
 
 
 def bench_c5(args):
@@ -652,17 +683,22 @@ def bench_c5(args):
         sys.path.insert(0, os.path.join(REPO, "oracle"))
         import oracle as O
         dnp = drafts.cpu().numpy()
+        seen = {}
 
         def step(threads, nseq):
-            O.verify(mode=_ffi.VERIFY_RESIDUAL, target=cfg["target"][:nseq],
-                     draft=cfg["draft"][:nseq], draft_tokens=dnp[:nseq], dtype=_ffi.DTYPE_BF16,
-                     params=cfg["params"][:nseq], uniforms=cfg["uniforms"][:nseq],
-                     threads=threads)
+            res = O.verify(mode=_ffi.VERIFY_RESIDUAL, target=cfg["target"][:nseq],
+                           draft=cfg["draft"][:nseq], draft_tokens=dnp[:nseq],
+                           dtype=_ffi.DTYPE_BF16, params=cfg["params"][:nseq],
+                           uniforms=cfg["uniforms"][:nseq], threads=threads)
+            if nseq == S:
+                seen["tokens"] = res["tokens"].reshape(-1)
 
         out["cpu_baseline"] = cpu_baseline_of(step, S, args.cpu_seconds, unit="verifies/s")
+        ok = tokens_check(out["cpu_baseline"], preps[0].tokens.cpu().numpy().reshape(-1), seen)
+        out["tokens_match"] = out["cpu_baseline"]["tokens_match"]
     ctx.close()
     print(json.dumps(out))
-    return 0
+    return 0 if args.no_cpu or ok else 1
 
 
 def bench_verify(args):
@@ -810,15 +846,19 @@ def main():
     launch = ctx.last_launch()
     k1_us = 1e3 * k1_ms / n_timed
     k2_us = 1e3 * k2_ms / n_timed
+    # eager launches, each bracketed by the library's timing-hook events: a
+    # per-launch figure that includes the hook's own event overhead, outside
+    # the timed region (the roofline uses the timed region's events)
     if launch["fused"]:
         dom_name = sample_kernel_name(launch)
-        kernel_us = {dom_name: k1_us, "timed_calls": n_timed}
+        eager_hook_us = {dom_name: k1_us, "timed_calls": n_timed}
         dom_us = k1_us
     else:
-        kernel_us = {"k_stats": k1_us, "k_select": k2_us, "timed_calls": n_timed}
+        eager_hook_us = {"k_stats": k1_us, "k_select": k2_us, "timed_calls": n_timed}
         dom_name, dom_us = "k_stats+k_select", k1_us + k2_us
 
-    # correctness guard for the copy that is the workload itself
+    # the tokens of the copy that is the workload itself (checked against
+    # the oracle in the CPU-baseline leg)
     tok0 = preps[0].tokens.cpu().numpy()
 
     alg_bytes = W.algorithmic_bytes(cfg)
@@ -850,7 +890,7 @@ def main():
         "data": "synthetic",
         "config": {"workload": cfg["workload"], "rows": B, "vocab": V, "logits_dtype": "bf16",
                    "semantics": "CBv2", "input_copies": R, "graph_steps_per_replay": R},
-        "kernel_us": kernel_us,
+        "eager_hook_us": eager_hook_us,
         "launch": launch,
         "step_effective_GBps": alg_bytes / (us_step * 1e-6) / 1e9,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -858,13 +898,15 @@ def main():
                      "algorithmic_bytes": alg_bytes, "kernel": dom_name, "launch_us": launch_us},
         "tokens_copy0_head": tok0[:4].tolist(),
     }
+    ok = True
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+        out["cpu_baseline"], ok = cpu_baseline(cfg, args.cpu_seconds, tok0)
+        out["tokens_match"] = out["cpu_baseline"]["tokens_match"]
     else:
         out["cpu_baseline"] = None
     ctx.close()
     print(json.dumps(out))
-    return 0
+    return 0 if ok else 1
 
 
 if __name__ == "__main__":
