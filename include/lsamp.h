@@ -108,9 +108,14 @@ typedef enum lsamp_mask_tail {
                                   context's candidate capacity; token = -1   */
 #define LSAMP_ROW_TOKEN_RANGE 8u /* lsamp_logprobs: the row's token lies outside
                                     [0, vocab); its log-probability is NaN  */
-#define LSAMP_ROW_TIMEOUT 16u    /* a fused step's bounded wait for the row's other
-                                    slices gave up (another workload held the
-                                    CUs); token = -1 (fail closed)           */
+#define LSAMP_ROW_TIMEOUT 16u    /* a one-pass top-k step's finalizer gave up
+                                    waiting for a slice that had started
+                                    (another workload held the CUs); token = -1
+                                    (fail closed).  The sampling kernels' other
+                                    arrangements never wait for a slice that
+                                    has not started, and hand the work of a
+                                    slice that gives up to the row's last
+                                    arriver: their rows are never timed out */
 
 /* ---- per-row inputs ------------------------------------------------------- */
 
@@ -335,9 +340,11 @@ lsamp_status lsamp_context_read_timing(lsamp_context* ctx, double* stats_ms, dou
 lsamp_status lsamp_context_set_mode(lsamp_context* ctx, int32_t mode);
 
 /* Sticky device-side status bits raised since the last read (waits for the
- * device); clears them.  LSAMP_STATUS_SPIN_TIMEOUT: a fused or top-k step
- * could not gather all slices of a row (another workload held the CUs); the affected
- * rows carry LSAMP_ROW_TIMEOUT and token -1 in the same step's outputs. */
+ * device); clears them.  LSAMP_STATUS_SPIN_TIMEOUT: a bounded wait for a
+ * row's other slices gave up (another workload held the CUs).  In a top-k
+ * step the affected rows carry LSAMP_ROW_TIMEOUT and token -1 in the same
+ * step's outputs; in a fused step the slice that gave up left its work to
+ * the row's last arriver, and every row is exact. */
 #define LSAMP_STATUS_SPIN_TIMEOUT 1u
 /* a penalty-aware verify position had more entries than penalty_scratch_cap
  * (its outputs are unreliable) */

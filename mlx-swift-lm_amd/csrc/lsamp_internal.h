@@ -112,7 +112,6 @@ struct SelectPartial {
   int32_t n_cand;    // candidates this slice produced
   int32_t n_list;    // kept tokens listed (> kKeptCap: list incomplete)
   int32_t overflow;  // entry-table overflow in this slice
-  int32_t timeout;   // this slice's bounded wait for the row's other slices gave up
 };
 
 struct Candidate {
@@ -159,6 +158,7 @@ struct VerifySpan {
   uint64_t tgt;  // the target's kept weight
 };
 
+constexpr int kRowSyncWords = 4;  // per-row synchronisation words of the sampling kernels
 struct Workspace {
   int32_t max_rows;
   int32_t max_vocab;
@@ -171,7 +171,8 @@ struct Workspace {
   KeptItem* klist;          // [max_rows][kMaxSlices][kKeptCap]
   SelectPartial* partials;  // [max_rows][kMaxSlices]
   uint32_t* cand_count;     // [max_rows]
-  uint32_t* arrive_stats;   // [max_rows]
+  uint32_t* arrive_stats;   // [max_rows][kRowSyncWords]: split mode's stats arrivals (word 0);
+                            // the fused arrangement's arrivals, start tickets, claims, departures
   uint32_t* arrive_select;  // [max_rows]
   uint32_t* status;         // [1] sticky error bits (kStatus*)
   uint32_t* tasks;          // [1] fused kernel over several rounds: tasks taken
@@ -233,7 +234,7 @@ constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
   L.status = off; off = align256(off + sizeof(uint32_t));
   L.tasks = off;  off = align256(off + sizeof(uint32_t));
   L.cc = off;     off = align256(off + R * sizeof(uint32_t));
-  L.as = off;     off = align256(off + R * sizeof(uint32_t));
+  L.as = off;     off = align256(off + R * kRowSyncWords * sizeof(uint32_t));
   L.asel = off;   off = align256(off + R * sizeof(uint32_t));
   L.tticket = off; off = align256(off + R * sizeof(uint32_t));
   L.vtick = off;  off = align256(off + R * sizeof(uint32_t));

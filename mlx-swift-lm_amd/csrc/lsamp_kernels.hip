@@ -18,14 +18,20 @@
 //                the row's semantics and draws the token by inverse CDF in
 //                token-id order.
 //
-// Fused mode runs both phases in one kernel whose grid fits on the device at
-// once: each slice of a row waits (bounded spin) until all slices have
-// published their histograms, then merges them itself, so no second hand-off
-// is needed; a wait that runs out sets a status bit and the work-group carries
-// on, so the grid always drains.  Split mode runs the phases as two kernels
-// (the last stats work-group of a row merges; the second kernel re-reads its
-// slice from L2) and needs no co-residency.  Neither mode uses MFMA: the stage
-// is a bandwidth- and reduction-bound pass, not a contraction.
+// Fused mode runs both phases in one kernel and assumes nothing about which
+// work-groups are resident.  Each slice takes a start ticket on its row.  At
+// the exchange a slice waits for the others' histograms only when every slice
+// of the row has started (those finish their stats without waiting for
+// anyone); otherwise, or when its bounded wait runs out, it leaves.  The
+// slice that arrives last merges at once, does its own select, and then
+// claims the select of every slice that left and does it from a re-read of
+// that slice; a slice claims its own select before doing it, so each select
+// runs exactly once.  The short-list rows' first exchange works the same way
+// (the fallback's histograms of slices that left are claimed by the first
+// exchange's last arriver).  Split mode runs the phases as two kernels (the
+// last stats work-group of a row merges; the second kernel re-reads its slice
+// from L2).  Neither mode uses MFMA: the stage is a bandwidth- and
+// reduction-bound pass, not a contraction.
 #include <hip/hip_runtime.h>
 
 #include "lsamp_device.h"
@@ -43,22 +49,82 @@ constexpr int kSpinLimit = 1 << 20;                   // ~0.2 s of polling
 // its limit this many polls (the waits' fail-closed path, under test)
 __device__ int32_t g_spin_test = 0;
 
-// A bounded wait of the fused kernel (thread 0): until `*counter` reaches
-// `target`; false when it gave up (the sticky status bit is raised).
-__device__ __forceinline__ bool spin_until(const Workspace& ws, const uint32_t* counter,
-                                           uint32_t target) {
+// The fused arrangement's per-row synchronisation words (in the arrive_stats
+// array): arrivals at the exchange in the low half of word 0 and start
+// tickets in its high half (an arrival's atomic returns both counts), claims
+// (bit s: slice s's select; bit kClaimStats + s: its fallback histogram) and
+// departures.  The last slice to leave returns them to zero.  (Split mode
+// counts its arrivals in word 0 alone.)
+constexpr int kSyncArrive = 0, kSyncClaims = 2, kSyncOut = 3;
+constexpr uint32_t kStartOne = 1u << 16, kArriveMask = 0xffffu;
+constexpr uint32_t kClaimStats = 8;
+static_assert(kMaxSlices <= (int)kClaimStats, "claim bits of both kinds fit one word");
+__device__ __forceinline__ uint32_t* row_sync(const Workspace& ws, int row) {
+  return ws.arrive_stats + (size_t)kRowSyncWords * (size_t)row;
+}
+
+// Thread 0: set bit `bit` of the row's claims; true for the one caller that
+// set it.
+__device__ __forceinline__ bool claim_bit(uint32_t* sync, uint32_t bit) {
+  const uint32_t old = __hip_atomic_fetch_or(sync + kSyncClaims, 1u << bit, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+  return ((old >> bit) & 1u) == 0u;
+}
+
+// Thread 0: the first slice from `from` on, other than `own`, whose claim
+// bit `base + s` this work-group sets (and `from` moves past it); -1 when
+// none is left.
+__device__ __forceinline__ int claim_next(uint32_t* sync, int G, int own, uint32_t base,
+                                          int& from) {
+  for (; from < G; ++from) {
+    if (from == own) continue;
+    if (claim_bit(sync, base + (uint32_t)from)) return from++;
+  }
+  return -1;
+}
+
+// A bounded wait of the fused kernel (thread 0) for the row's exchange: 1
+// when the arrivals reach `target`; -1 when another work-group set claim bit
+// `bit` (it does that work itself, so this slice can leave); 0 when the wait
+// gave up (the sticky status bit is raised, and the slice leaves).  Callers
+// wait only when every slice of the row has started, so the arrivals come
+// from work-groups that are running.
+__device__ __forceinline__ int wait_exchange(const Workspace& ws, const uint32_t* sync,
+                                             uint32_t target, uint32_t bit) {
   const int32_t test = __hip_atomic_load(&g_spin_test, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const uint32_t tgt = test > 0 ? 0xffffffffu : target;
   const int lim = test > 0 ? test : kSpinLimit;
-  int it = 0;
-  while (ld_coherent(counter) < tgt) {
+  for (int it = 0;;) {
+    if ((ld_coherent(sync + kSyncArrive) & kArriveMask) >= tgt) return 1;
+    // (claims are rare: every 16th poll looks)
+    if ((it & 15) == 15 && ((ld_coherent(sync + kSyncClaims) >> bit) & 1u)) return -1;
     if (++it >= lim) {
       atomicOr(ws.status, kStatusSpinTimeout);
-      return false;
+      return 0;
     }
     __builtin_amdgcn_s_sleep(2);
   }
-  return true;
+}
+
+// A slice's last act on its row (fused arrangement, thread 0): count it out.
+// Thread 0 has the results of all its other operations on the row's words
+// by now (the start ticket's included), so none of them can land after a
+// clear.  The old count is checked later (clear_if_last), so the round trip
+// overlaps the next task's take.
+__device__ __forceinline__ uint32_t leave_row(const Workspace& ws, int row) {
+  return __hip_atomic_fetch_add(row_sync(ws, row) + kSyncOut, 1u, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Thread 0: the last of the row's G slices to leave clears its
+// synchronisation words for the next step (every slice is done with them).
+__device__ __forceinline__ void clear_if_last(const Workspace& ws, int row, int G, uint32_t out) {
+  if (out + 1u == (uint32_t)G) {
+    uint32_t* sync = row_sync(ws, row);
+    st_coherent(sync + kSyncArrive, 0u);
+    st_coherent(sync + kSyncClaims, 0u);
+    st_coherent(sync + kSyncOut, 0u);
+  }
 }
 // Buckets of the short-list finalize's counting sort (by a key's high word);
 // their counts and starts live in the thread-maximum histogram.
@@ -186,7 +252,14 @@ struct TaskLds {
   int32_t nlist;
   int32_t nitems;
   int32_t last;
-  int32_t tmo;  // this task's bounded wait gave up
+  // the fused arrangement's hand-off (thread 0 writes, the work-group reads)
+  int32_t wait;         // the first exchange's wait: 1 reached, 0 gave up / not started, -1 claimed
+  int32_t won;          // a claim of this work-group's own work succeeded
+  int32_t x1;           // first exchange's last arriver of a row that fell back
+  int32_t xlast;        // this work-group made the exchange's last arrival
+  int32_t job;          // the slice of the claimed job, or -1
+  int32_t from_stats;   // claim scans: the next slice to try
+  int32_t from_select;
   uint32_t flags;
   uint32_t task;  // fused kernel over several rounds: the task taken
 };
@@ -442,7 +515,6 @@ __device__ __forceinline__ int draw_slot(int o) { return o + (o >> 4); }
 struct TailIn {
   int nc;           // candidates in F.keys, sorted by cand_key descending
   bool overflow;    // the row's keep set could not be resolved
-  bool timeout;     // a slice's wait for the others gave up (fail closed)
   double ent_all;   // kept tokens outside the candidates: entropy numerator,
   float min_all;    //   smallest kept value,
   int32_t kept_all; //   count
@@ -452,7 +524,6 @@ struct TailIn {
   float probe_x;
   int32_t n_list;   // lane s < G: kept tokens slice s listed (> kKeptCap: incomplete)
   bool reset;       // clear the row's select counters (histogram path)
-  bool fused;
   int32_t done;     // RowInfo.done of the written row decision
 };
 
@@ -747,10 +818,7 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
 
   if (l == 0) {
     uint32_t flags = info.flags;
-    if (t.timeout)
-      flags |= LSAMP_ROW_TIMEOUT;
-    else if (overflow)
-      flags |= LSAMP_ROW_OVERFLOW;
+    if (overflow) flags |= LSAMP_ROW_OVERFLOW;
     if (!overflow && ((draw && token < 0) || W == 0ull)) flags |= LSAMP_ROW_EMPTY;
     const int tok = overflow ? -1 : token;
     P.tokens[row] = tok;
@@ -776,9 +844,11 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
     out.done = t.done;
     ws.rows[row] = out;
     if (t.reset) {
+      // (every select of the row has arrived: nothing counts on these any
+      // more this step; the exchange's words are cleared by the last slice
+      // to leave the row, or, in split mode, by the stats kernel)
       ws.cand_count[row] = 0u;
       ws.arrive_select[row] = 0u;
-      if (t.fused) ws.arrive_stats[row] = 0u;
     }
   }
 }
@@ -787,7 +857,7 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
                              const lsamp_row_params& prm, const RowInfo& info, TaskLds& L,
-                             const char* rowp, const uint32_t* mrow, bool fused) {
+                             const char* rowp, const uint32_t* mrow) {
   const int tid = fresh_tid();
   const int l = tid & 63;
   const bool wave0 = tid < 64;
@@ -819,7 +889,6 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
       part.n_cand = ld_coherent(&sp->n_cand);
       part.n_list = ld_coherent(&sp->n_list);
       part.overflow = ld_coherent(&sp->overflow);
-      part.timeout = ld_coherent(&sp->timeout);
     }
 #pragma unroll
     for (int i = 0; i < kChunksPerLane; ++i) {
@@ -848,7 +917,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   double ent_all = 0.0;
   float min_all = kPosInf;
   int32_t kept_all = 0;
-  bool overflow = false, timeout = false;
+  bool overflow = false;
   int nc = 0;
   if (wave0) {
     const bool in = l < G;
@@ -856,9 +925,8 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
     min_all = wave_min(in ? part.min_kept : kPosInf);
     kept_all = wave_sum(in ? part.n_kept : 0);
     const int32_t ov = wave_max(in && (part.n_cand > kWgCandCap || part.overflow) ? 1 : 0);
-    timeout = __ballot(in && part.timeout != 0) != 0ull;
     overflow = (info.flags & LSAMP_ROW_OVERFLOW) != 0 || ov != 0 || total_cand > kCandCap;
-    nc = (overflow || timeout || !active) ? 0 : total_cand;
+    nc = (overflow || !active) ? 0 : total_cand;
     if (l == 0) L.misc[1] = nc;
   }
   __syncthreads();
@@ -919,8 +987,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
 
   TailIn t;
   t.nc = nc;
-  t.overflow = overflow || timeout;
-  t.timeout = timeout;
+  t.overflow = overflow;
   t.ent_all = ent_all;
   t.min_all = min_all;
   t.kept_all = kept_all;
@@ -930,20 +997,8 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   t.probe_x = probe_x;
   t.n_list = part.n_list;
   t.reset = true;
-  t.fused = fused;
   t.done = 0;
   finalize_tail<DT>(ws, P, row, c, prm, info, L, rowp, mrow, t, rch);
-}
-
-// A short-list row's slice leaves through a second counter; the last one out
-// clears both counters for the next step (fused mode).
-__device__ __forceinline__ void short_depart(const Workspace& ws, int row, int G) {
-  const uint32_t out = __hip_atomic_fetch_add(&ws.arrive_select[row], 1u, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-  if (out + 1u == (uint32_t)G) {
-    st_coherent(&ws.arrive_stats[row], 0u);
-    st_coherent(&ws.arrive_select[row], 0u);
-  }
 }
 
 // Single-wave tail of a short-list row with at most 64 candidates (lane r
@@ -1188,12 +1243,6 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   const int64_t V = P.vocab;
   FinalLds& F = L.u.f;
   const uint64_t* pub = reinterpret_cast<const uint64_t*>(ws.cands + (size_t)row * kCandCap);
-  // the departure ticket is taken now and checked at the end, so its round
-  // trip overlaps the rest (the barriers below order LDS only, not memory)
-  uint32_t ticket = 0u;
-  if (P.fused && tid == 64)
-    ticket = __hip_atomic_fetch_add(&ws.arrive_select[row], 1u, __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
   const int n_tot = L.soff[G];
   const int npmax = L.misc[7];
   if (npmax > 64) {
@@ -1327,13 +1376,7 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
       if ((uint32_t)(F.keys[i] >> 32) < kv && (uint32_t)(F.keys[i - 1] >> 32) >= kv) L.misc[6] = i;
   }
   lds_barrier();
-  if (!wave0) {
-    if (P.fused && tid == 64 && ticket + 1u == (uint32_t)G) {
-      st_coherent(&ws.arrive_stats[row], 0u);
-      st_coherent(&ws.arrive_select[row], 0u);
-    }
-    return;
-  }
+  if (!wave0) return;
   int nc = L.misc[6];
   const RowInfo info = L.info;
   if (info.mode != kModeNormal) nc = 0;
@@ -1346,7 +1389,6 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   TailIn t;
   t.nc = nc;
   t.overflow = false;
-  t.timeout = false;
   t.ent_all = 0.0;
   t.min_all = kPosInf;
   t.kept_all = 0;
@@ -1356,7 +1398,6 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   t.probe_x = 0.0f;
   t.n_list = 0;
   t.reset = false;
-  t.fused = P.fused != 0;
   t.done = 1;
   uint64_t rch[kChunksPerLane];
 #pragma unroll
@@ -1378,11 +1419,25 @@ __device__ __forceinline__ bool short_fallback(const Workspace& ws, int row, int
   return L.misc[5] != 0;
 }
 
-template <int DT, int MODE>
-__device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& P, int row, int slice,
-                                         TaskLds& L) {
+// What a fused work-group does next on its row (slice_job's result): leave
+// it, or a job for another slice: its fallback histogram (kBehalfStats) or
+// its select (kSelectOnly), from a re-read of that slice.
+constexpr int kJobLeave = -1;
+constexpr int kBehalfStats = 3;
+__device__ __forceinline__ int next_job(int kind, int slice) { return (kind << 8) | slice; }
+
+// One pass of a work-group over one slice of a row.  Split mode: MODE is the
+// kernel's phase (and JM == MODE).  Fused arrangement (MODE == kFused): JM is
+// the job: the work-group's own slice (kFused), or work it claimed for slice
+// `slice` of a slice that left (kBehalfStats, kSelectOnly); `own` is its own
+// slice.  (Each job is its own instantiation, so the own pass compiles as
+// if the others did not exist.)
+template <int DT, int MODE, int JM>
+__device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& P, int row, int slice,
+                                         TaskLds& L, int own) {
+  constexpr int jm = JM;
   // split mode: rows the stats kernel already drew (short lists) are done
-  if (MODE == kSelectOnly && ws.rows[row].done) return;
+  if (MODE == kSelectOnly && ws.rows[row].done) return kJobLeave;
   constexpr int N = Vec<DT>::N;
   constexpr int Q = Slab<DT>::Q;
   static_assert(Q <= 32, "staged quad numbers take 5 bits");
@@ -1439,14 +1494,20 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       quad_set(S.bank[g / kQuadsPerBank], g % kQuadsPerBank, make_uint4(w[0], w[1], w[2], w[3]));
     }
   }
-  if (MODE != kSelectOnly) {
+  // (fused, own slice) the row's start ticket, issued after the slice's
+  // loads so that their waits do not include it; its result is consumed at
+  // the first exchange, before the arrival
+  uint32_t tick = 0u;
+  if (MODE == kFused && jm == kFused && tid == 0)
+    tick = __hip_atomic_fetch_add(row_sync(ws, row) + kSyncArrive, kStartOne, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+  if (jm != kSelectOnly) {
     for (int i = tid; i < kHist; i += kThreads) L.u.hist[i] = 0ull;
     for (int i = tid; i < kTauBins; i += kThreads) L.sh.tcnt[i] = 0u;
   }
   if (tid == 0) {
     L.flags = 0u;
     L.ncand = 0;
-    L.tmo = 0;
   }
   SliceEntries se{L.pen, L.etok, L.ex, &L.ecount};
   EntryMarks<> em;
@@ -1480,7 +1541,10 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   // integer anchored at a quad maximum (re-anchored by an exact power of two
   // only if the running maximum climbs 64 binary orders above it), so the
   // largest terms are computed at full precision.
-  const int K = MODE != kSelectOnly ? short_k(c, prm, V) : 0;
+  // (a claimed fallback histogram skips the short list: K = 0; Krow is the
+  // row's own, which sets the exchange's arrival count)
+  const int Krow = jm != kSelectOnly ? short_k(c, prm, V) : 0;
+  const int K = jm == kBehalfStats ? 0 : Krow;
   const bool zon = K > 0 && c.kind != LSAMP_KIND_ARGMAX;
   const float lgz = (float)(1.4426950408889634 / c.tf);  // log2(e) / T_f
   // penalty-bitmap word of quad g (the bitmap is zeroed over the largest
@@ -1522,7 +1586,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       }
     }
     exclude_elems<DT>(v, ex);
-    if (MODE != kSelectOnly) {
+    if (jm != kSelectOnly) {
       const float qm = vec_max_nn<DT>(v);  // NaNs are excluded by now
       if constexpr (kKeepQm) qmc[g * kThreads + tid] = qm;
       xmax = __builtin_elementwise_maximum(xmax, qm);
@@ -1551,7 +1615,7 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
   const bool nonfinite = nonfinite_seen<DT>(nf_acc);
 
   RowInfo info;
-  if (MODE != kSelectOnly) {
+  if (jm != kSelectOnly) {
     // ------------------------------------------------ B: max
     if (nonfinite) atomicOr(&L.flags, LSAMP_ROW_NONFINITE);
     const float tmax = xmax;  // this thread's largest (transformed) logit
@@ -1798,30 +1862,47 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
         st_coherent_f32(&Ssum->ylo, ylo);
       }
       if (MODE == kFused) {
-        // first exchange of a short-list row: the last slice to publish
-        // draws the token; the others wait for it only to learn whether a
-        // slice needs the histogram path instead
+        // First exchange of a short-list row: the last slice to publish
+        // draws the token.  The others wait, only when every slice of the
+        // row has started, to learn whether a slice needs the histogram path
+        // instead; a slice that cannot wait or gives up leaves, and if the
+        // row does fall back, the last arriver builds its histogram.
         drain_memory();
         __syncthreads();
         if (tid == 0) {
-          const uint32_t prev = __hip_atomic_fetch_add(&ws.arrive_stats[row], 1u, __ATOMIC_RELAXED,
+          asm volatile("" ::"v"(tick));
+          uint32_t* sync = row_sync(ws, row);
+          // (the arrival's atomic returns the start count too; a slice that
+          // has started since only makes this one leave)
+          const uint32_t word = __hip_atomic_fetch_add(sync + kSyncArrive, 1u, __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT);
+          const uint32_t prev = word & kArriveMask, started = word >> 16;
           const bool last = prev + 1u == (uint32_t)G;
-          L.tmo = (!last && !spin_until(ws, &ws.arrive_stats[row], (uint32_t)G)) ? 1 : 0;
+          int w = 1;
+          if (!last)
+            w = started >= (uint32_t)G
+                    ? wait_exchange(ws, sync, (uint32_t)G, kClaimStats + (uint32_t)slice)
+                    : 0;
+          L.wait = w;
           L.last = last ? 1 : 0;
         }
         __syncthreads();
         if (L.last) {
           if (short_gather<DT>(ws, P, row, c, prm, L)) {
             short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K);
-            return;
+            return kJobLeave;
           }
-        } else if (L.tmo || !short_fallback(ws, row, G, L)) {
-          // (a slice that gave up waiting cannot trust the fallback flags; it
-          // leaves, and a row that did fall back then fails closed in its
-          // histogram wait)
-          if (tid == 0) short_depart(ws, row, G);
-          return;
+          // the row falls back: this slice's histogram, then those of the
+          // slices that left
+          if (tid == 0) L.x1 = 1;
+        } else if (L.wait != 1 || !short_fallback(ws, row, G, L)) {
+          return kJobLeave;
+        } else {
+          // the row falls back: this slice's histogram, unless the first
+          // exchange's last arriver has claimed it
+          if (tid == 0) L.won = claim_bit(row_sync(ws, row), kClaimStats + (uint32_t)slice) ? 1 : 0;
+          __syncthreads();
+          if (!L.won) return kJobLeave;
         }
       }
     }
@@ -1901,36 +1982,86 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
       st_coherent_f64(&Ssum->z, zs);
     }
     if (MODE == kFused) {
-      // all-gather: wait until every slice of the row has published, then
-      // merge here (the merge is deterministic, so all slices agree); a
-      // short-list row that fell back counts its second arrival
-      const uint32_t target = (uint32_t)(K > 0 ? 2 * G : G);
+      // The exchange (a short-list row that fell back counts its second
+      // arrival).  The last arrival merges at once.  Another slice waits for
+      // the rest only when every slice of the row has started, then claims
+      // its own select; a slice that cannot wait, gives up, or finds its
+      // select claimed leaves it to the last arriver.  Every slice that
+      // merges computes the same cut (the merge is deterministic).
+      const uint32_t target = (uint32_t)(Krow > 0 ? 2 * G : G);
       drain_memory();
       __syncthreads();
+      // Thread 0 arrives (the atomic returns the start count too); unless
+      // this is the last arrival (or the hand-off of a row that fell back,
+      // below), it waits and sends the claim of its own select, whose
+      // result is checked after the merge (the round trip overlaps the
+      // merge's loads).  Same barriers as a plain wait.
+      uint32_t claimed = 0u;
       if (tid == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(&ws.arrive_stats[row], 1u, __ATOMIC_RELAXED,
+        asm volatile("" ::"v"(tick));
+        uint32_t* sync = row_sync(ws, row);
+        const uint32_t word = __hip_atomic_fetch_add(sync + kSyncArrive, 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
-        // bounded: a wait that runs out sets a status bit and this slice's
-        // timeout mark, so the grid drains and the row fails closed
-        if (prev + 1u < target && !spin_until(ws, &ws.arrive_stats[row], target)) L.tmo = 1;
+        const uint32_t prev = word & kArriveMask, started = word >> 16;
+        const bool last = prev + 1u == target;
+        if (last) L.xlast = 1;
+        int w = 1;
+        if (!last && !L.x1) {
+          w = started >= (uint32_t)G ? wait_exchange(ws, sync, target, (uint32_t)own) : 0;
+          if (w == 1)
+            claimed = __hip_atomic_fetch_or(sync + kSyncClaims, 1u << own, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+        }
+        L.wait = w;
       }
       __syncthreads();
-      merge_row(ws, P, row, c, prm, L);
+      if (L.x1) {
+        // the first exchange's last arriver of a row that fell back builds
+        // the histograms of the slices that left that exchange, then waits
+        // (unless its arrival was the last) as any slice does
+        if (tid == 0) L.job = claim_next(row_sync(ws, row), G, own, kClaimStats, L.from_stats);
+        __syncthreads();
+        if (L.job >= 0) return next_job(kBehalfStats, L.job);
+        if (tid == 0 && !L.xlast) {
+          uint32_t* sync = row_sync(ws, row);
+          // (claimed histograms took a while: the start count is read again)
+          const int w = (ld_coherent(sync + kSyncArrive) >> 16) >= (uint32_t)G
+                            ? wait_exchange(ws, sync, target, (uint32_t)own)
+                            : 0;
+          if (w == 1)
+            claimed = __hip_atomic_fetch_or(sync + kSyncClaims, 1u << own, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+          L.wait = w;
+        }
+        __syncthreads();
+      }
+      if (!L.xlast && L.wait != 1) return kJobLeave;
+      if (tid < 64) merge_wave(ws, P, row, c, prm, L);
+      if (tid == 0) L.won = (L.xlast || ((claimed >> own) & 1u) == 0u) ? 1 : 0;
+      __syncthreads();
+      if (!L.won) return kJobLeave;  // (the last arriver does this select)
+      // (after a claimed histogram the registers hold another slice: the
+      // own select re-reads the own slice)
+      if (jm == kBehalfStats) return next_job(kSelectOnly, own);
       info = L.info;
     } else {
-      if (!arrive_last(&ws.arrive_stats[row], (uint32_t)G, &L.last)) return;
+      uint32_t* const arrive = row_sync(ws, row) + kSyncArrive;
+      if (!arrive_last(arrive, (uint32_t)G, &L.last)) return kJobLeave;
       if (K > 0 && short_gather<DT>(ws, P, row, c, prm, L)) {
         short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K);
-        if (tid == 0) ws.arrive_stats[row] = 0u;
-        return;
+        if (tid == 0) *arrive = 0u;
+        return kJobLeave;
       }
       merge_row(ws, P, row, c, prm, L);
       if (tid == 0) {
         ws.rows[row] = L.info;
-        ws.arrive_stats[row] = 0u;
+        *arrive = 0u;
       }
-      return;
+      return kJobLeave;
     }
+  } else if (MODE == kFused) {
+    // a claimed select: the cut this work-group merged
+    info = L.info;
   } else {
     if (tid == 0) L.info = ws.rows[row];
     __syncthreads();
@@ -2145,10 +2276,52 @@ __device__ __forceinline__ void run_task(const Workspace& ws, const SamplePlan& 
     st_coherent(&sp->n_cand, ncand);
     st_coherent(&sp->n_list, nlist);
     st_coherent(&sp->overflow, ent_overflow ? 1 : 0);
-    st_coherent(&sp->timeout, L.tmo);
   }
-  if (!arrive_last(&ws.arrive_select[row], (uint32_t)G, &L.last)) return;
-  finalize_row<DT>(ws, P, row, c, prm, info, L, rowp, mrow, MODE == kFused);
+  if (arrive_last(&ws.arrive_select[row], (uint32_t)G, &L.last))
+    finalize_row<DT>(ws, P, row, c, prm, info, L, rowp, mrow);
+  if (MODE != kFused) return kJobLeave;
+  // the exchange's last arriver does the selects of the slices that left
+  if (L.xlast) {
+    if (tid == 0) L.job = claim_next(row_sync(ws, row), G, own, 0u, L.from_select);
+    __syncthreads();
+    if (L.job >= 0) return next_job(kSelectOnly, L.job);
+  }
+  return kJobLeave;
+}
+
+// A task (row, slice).  Split mode: one pass.  Fused arrangement: the
+// work-group's own slice (with its start ticket), then whatever it claimed
+// for slices that left, and the departure; returns (thread 0) the row's
+// departure count before this one, for clear_if_last.
+template <int DT, int MODE>
+__device__ __forceinline__ uint32_t run_task(const Workspace& ws, const SamplePlan& P, int row,
+                                             int slice, TaskLds& L) {
+  if constexpr (MODE != kFused) {
+    (void)slice_job<DT, MODE, MODE>(ws, P, row, slice, L, slice);
+    return 0u;
+  } else {
+    if (threadIdx.x == 0) {
+      L.x1 = 0;
+      L.xlast = 0;
+      L.from_stats = 0;
+      L.from_select = 0;
+    }
+    // (no barrier: the job's first barriers come after its loads are issued,
+    // before anything reads these)
+    int next = slice_job<DT, kFused, kFused>(ws, P, row, slice, L, slice);
+    // (after the own pass: at most G - 1 claimed histograms and G claimed
+    // selects; every thread returns the same job, read from LDS)
+    for (int n = 0; n < 2 * kMaxSlices && next >= 0; ++n) {
+      next = __builtin_amdgcn_readfirstlane(next);
+      const int s = next & 0xff;
+      __syncthreads();
+      next = (next >> 8) == kBehalfStats
+                 ? slice_job<DT, kFused, kBehalfStats>(ws, P, row, s, L, slice)
+                 : slice_job<DT, kFused, kSelectOnly>(ws, P, row, s, L, slice);
+    }
+    // (thread 0 has consumed its start ticket's result at the exchange)
+    return threadIdx.x == 0 ? leave_row(ws, row) : 0u;
+  }
 }
 
 // ================================================================ kernels
@@ -2166,7 +2339,10 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
   const int rowslot = (int)blockIdx.x / G;
   const int slice = (int)blockIdx.x % G;
   if (ONE) {
-    if (rowslot < P.rows) run_task<DT, kFused>(ws, P, rowslot, slice, L);
+    if (rowslot < P.rows) {
+      const uint32_t out = run_task<DT, kFused>(ws, P, rowslot, slice, L);
+      if (threadIdx.x == 0) clear_if_last(ws, rowslot, G, out);
+    }
     return;
   }
   // More tasks than work-groups: each work-group takes the next task (row-
@@ -2208,11 +2384,17 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
   // would return 0 .. grid - 1 in some order, all at once on one counter);
   // later takes count from the grid's size.
   uint32_t t = blockIdx.x;
+  // (thread 0) the last task's row and its departure count, checked once the
+  // next take has come back: the two round trips overlap
+  int pend_row = -1;
+  uint32_t pend_out = 0u;
   for (bool first = true;; first = false) {
     if (!first) {
-      if (threadIdx.x == 0)
+      if (threadIdx.x == 0) {
         L.task = gridDim.x + __hip_atomic_fetch_add(ws.tasks, 1u, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
+        if (pend_row >= 0) clear_if_last(ws, pend_row, G, pend_out);
+      }
       __syncthreads();
       t = L.task;
       __syncthreads();
@@ -2223,7 +2405,13 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
     const Workspace wsr = in_sgprs(ws);
     const SamplePlan Pr = in_sgprs(P);
     const int q = (int)(t / (uint32_t)G);
-    run_task<DT, kFused>(wsr, Pr, ordered ? (int)order[q] : q, (int)(t % (uint32_t)G), L);
+    // (row and slice through readfirstlane: the divergence analysis cannot
+    // see that a value read from LDS at a uniform address is uniform once
+    // the task holds a loop of its own)
+    const int row = __builtin_amdgcn_readfirstlane(ordered ? (int)order[q] : q);
+    const int slice_t = __builtin_amdgcn_readfirstlane((int)(t % (uint32_t)G));
+    pend_out = run_task<DT, kFused>(wsr, Pr, row, slice_t, L);
+    pend_row = row;
     __syncthreads();
   }
   // every work-group ends with one failed take (the counter then holds
