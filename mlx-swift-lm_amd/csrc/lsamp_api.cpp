@@ -233,7 +233,10 @@ lsamp_status lsamp::sample_step(const WorkspaceViews& v, const DeviceShape& d, i
   // (the top-k kernel: one work-group per CU is enough, and fewer slices per
   // row mean a shorter merge)
   plan_slices(a->rows, a->vocab, topk ? d.cus : slots, &P.slices, &P.slice_len, &P.nchunks);
-  P.fused = !topk && mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;
+  // (fp32 steps run fused in one round only: the fused kernel's several-rounds
+  // form is not built for the fp32 slab)
+  P.fused = !topk && mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices &&
+            (a->dtype != LSAMP_DTYPE_F32 || (int64_t)a->rows * P.slices <= slots);
   P.rows_per_round = P.fused ? slots / P.slices : a->rows;
   const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
   P.aligned = aligned16(a->logits) && ((size_t)a->row_stride * es) % 16 == 0;
@@ -940,7 +943,8 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   const int32_t bpc = ctx->shape.fused_bpc[a->dtype];
   const int32_t slots = ctx->cus * (bpc > 0 ? bpc : 1);
   plan_slices(P.rows, P.vocab, slots, &P.slices, &P.slice_len, &P.nchunks);
-  P.fused = ctx->mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices;
+  P.fused = ctx->mode != LSAMP_MODE_SPLIT && bpc > 0 && slots >= P.slices &&
+            (a->dtype != LSAMP_DTYPE_F32 || (int64_t)P.rows * P.slices <= slots);
   P.rows_per_round = P.fused ? slots / P.slices : P.rows;
   const size_t es = a->dtype == LSAMP_DTYPE_F32 ? 4 : 2;
   P.aligned = aligned16(a->target_logits) && (!residual || aligned16(a->draft_logits)) &&

@@ -2440,9 +2440,18 @@ int launch_dt(const Workspace& ws, const SamplePlan& P, hipStream_t st, void* co
   mark(0);
   if (P.fused) {
     const int rounds_rows = P.rows < P.rows_per_round ? P.rows : P.rows_per_round;
-    auto kf = P.rows <= P.rows_per_round ? k_fused<DT, true> : k_fused<DT, false>;
-    hipLaunchKernelGGL(kf, dim3((unsigned)(rounds_rows * P.slices)), dim3(kThreads), 0, st,
-                       ws, P);
+    // (fp32 steps run fused only when every row fits one round: the
+    // several-rounds instantiation with the fp32 slab does not fit the
+    // registers, so it is not built, and the planner gives such steps the
+    // split kernels)
+    if constexpr (DT == LSAMP_DTYPE_F32) {
+      hipLaunchKernelGGL((k_fused<DT, true>), dim3((unsigned)(rounds_rows * P.slices)),
+                         dim3(kThreads), 0, st, ws, P);
+    } else {
+      auto kf = P.rows <= P.rows_per_round ? k_fused<DT, true> : k_fused<DT, false>;
+      hipLaunchKernelGGL(kf, dim3((unsigned)(rounds_rows * P.slices)), dim3(kThreads), 0, st,
+                         ws, P);
+    }
     mark(1);
   } else {
     const dim3 grid((unsigned)P.slices, (unsigned)P.rows);
@@ -2906,10 +2915,16 @@ int set_spin_test(int32_t polls) {
 template <int DT>
 int fused_blocks_dt() {
   int a = 0, b = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_fused<DT, true>, kThreads, 0) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_fused<DT, false>, kThreads, 0) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_fused<DT, true>, kThreads, 0) != hipSuccess)
     return 0;
-  return a < b ? a : b;
+  if constexpr (DT == LSAMP_DTYPE_F32) {
+    return a;  // (one round only)
+  } else {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_fused<DT, false>, kThreads, 0) !=
+        hipSuccess)
+      return 0;
+    return a < b ? a : b;
+  }
 }
 
 int fused_blocks_per_cu(int dtype) {

@@ -1,7 +1,7 @@
 """The two execution modes of lsamp_sample agree bit for bit.
 
-Fused mode runs the whole step as one co-resident kernel whose work-groups
-wait for their row's histogram merge; split mode runs it as two kernels.  Both
+Fused mode runs the whole step as one kernel whose work-groups hand their
+row's histogram merge to each other; split mode runs it as two kernels.  Both
 must give identical tokens, flags, processed logits, keep sets and statistics
 (integer histogram and weight sums make the result independent of the order in
 which work-groups finish), and a fused step must never leave the device's
@@ -57,7 +57,7 @@ def test_fused_equals_split_full_configs(ctx, n):
     _assert_same(f, s, f"config{n}")
 
 
-def test_fused_equals_split_many_rounds(ctx):
+def _many_rounds_cfg(dtype):
     # 512 rows of a 40,001-token vocabulary: several rounds of the fused grid
     rng = np.random.default_rng(21)
     V, B = 40001, 512
@@ -66,10 +66,38 @@ def test_fused_equals_split_many_rounds(ctx):
                              top_k=[0, 40, 5, 400][(r // 4) % 4],
                              top_p=[1.0, 0.9, 0.5][r % 3], min_p=[0.0, 0.05][r % 2], vocab=V)
               for r in range(B)]
-    cfg = dict(semantics=_ffi.SEM_CBV2, dtype=_ffi.DTYPE_F32, rows=B, vocab=V, logits=x,
-               params=W._params(params), uniforms=rng.random(B, dtype=np.float32))
+    logits = x if dtype == _ffi.DTYPE_F32 else W.f32_to_bf16_bits(x)
+    return dict(semantics=_ffi.SEM_CBV2, dtype=dtype, rows=B, vocab=V, logits=logits,
+                params=W._params(params), uniforms=rng.random(B, dtype=np.float32))
+
+
+def test_fused_equals_split_many_rounds(ctx):
+    cfg = _many_rounds_cfg(_ffi.DTYPE_BF16)
     f, s = _both_modes(ctx, cfg)
     _assert_same(f, s, "many rounds")
+    ctx.set_mode(_ffi.MODE_FUSED)
+    try:
+        run_gpu(ctx, cfg)
+        launch = ctx.last_launch()
+    finally:
+        ctx.set_mode(_ffi.MODE_AUTO)
+    assert launch["fused"] == 1 and launch["rows_per_round"] < cfg["rows"], launch
+
+
+def test_fp32_steps_of_several_rounds_run_split(ctx):
+    """The fused kernel's several-rounds form is not built for the fp32 slab
+    (it would not fit the registers): such steps take the split kernels, in
+    every mode, with the same results."""
+    cfg = _many_rounds_cfg(_ffi.DTYPE_F32)
+    f, s = _both_modes(ctx, cfg)
+    _assert_same(f, s, "fp32 many rounds")
+    for mode in (_ffi.MODE_AUTO, _ffi.MODE_FUSED):
+        ctx.set_mode(mode)
+        try:
+            run_gpu(ctx, cfg)
+            assert ctx.last_launch()["fused"] == 0
+        finally:
+            ctx.set_mode(_ffi.MODE_AUTO)
 
 
 def test_status_clear_after_default_mode(ctx):
