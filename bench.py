@@ -91,13 +91,18 @@ def parse():
                     help="--path verify: penalty-aware windows")
     ap.add_argument("--top-k", type=int, default=20,
                     help="--path logprobs / step: top_k of the log-probabilities")
+    ap.add_argument("--step-config", default="c2", choices=["c2", "c3", "c4"],
+                    help="--path step: the headline batch (with a commit), or the mixed (c3) "
+                         "or grammar-constrained fp32 (c4) batch (draw only), which take the "
+                         "fused sampling kernel")
     return ap.parse_args()
 
 
 def sample_kernel_name(launch):
     """The kernel(s) one sampling step launched (lsamp_launch_info.fused:
     2 the one-pass top-k kernel, 1 the fused kernel, 0 the two-kernel split)."""
-    return {3: "k_topk", 2: "k_topk", 1: "k_fused"}.get(launch["fused"], "k_stats+k_select")
+    return {4: "k_fused", 3: "k_topk", 2: "k_topk", 1: "k_fused"}.get(launch["fused"],
+                                                                       "k_stats+k_select")
 
 
 def graph_runner(launches, stream):
@@ -335,6 +340,8 @@ def bench_step(args):
     from lsamp.api import Context, PenaltyTable
     from lsamp.history import Cbv2RowState
 
+    if args.step_config != "c2":
+        return bench_step_fused(args)
     cfg = W.config2()
     B, V, R = cfg["rows"], cfg["vocab"], args.copies
     steps, warm = args.steps, args.warmup
@@ -394,6 +401,90 @@ def bench_step(args):
                    "input_copies": R,
                    "kernels": kinds.get(launch["fused"], sample_kernel_name(launch)) ,
                    "kernels_without_logprobs": sample_kernel_name(launch0) + " + k_commit"},
+        "roofline": None, "cpu_baseline": None,
+    }
+    ctx.close()
+    print(json.dumps(out))
+    return 0
+
+
+def bench_step_fused(args):
+    """lsamp_step (draw + raw log-probabilities, no commit) on the mixed
+    (c3) or grammar-constrained fp32 (c4) batch, whose rows take the fused
+    sampling kernel: with the log-probabilities it ranks the raw logits in
+    its own pass (launch kind 4), so the line's ratio is what they cost in
+    that pass; `lsamp_logprobs` alone on the same batch is timed beside it
+    (the second pass the step no longer makes)."""
+    import numpy as np
+    import torch
+
+    from lsamp import _ffi, workloads as W
+    from lsamp.api import Context
+
+    n = int(args.step_config[1])
+    cfg = W.CONFIGS[n]()
+    B, V = cfg["rows"], cfg["vocab"]
+    R = args.copies if n != 3 else min(args.copies, 4)
+    steps, warm = args.steps, args.warmup
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(30 + n)
+    if cfg["dtype"] == _ffi.DTYPE_F32:
+        base = torch.from_numpy(np.ascontiguousarray(cfg["logits"], np.float32))
+        tdt = torch.float32
+    else:
+        base = torch.from_numpy(cfg["logits"].view(np.int16)).view(torch.bfloat16)
+        tdt = torch.bfloat16
+    copies = torch.empty((R, B, V), dtype=tdt, device=dev)
+    for i in range(R):
+        copies[i].copy_(base)
+        if i:
+            idx = torch.from_numpy(rng.integers(0, V, B)).to(dev)
+            copies[i, torch.arange(B, device=dev), idx] = 0.0
+    ctx = Context(0, max_rows=B, max_vocab=V)
+    assert cfg["semantics"] == _ffi.SEM_CBV2  # (lsamp_step is the CBv2 step)
+    kw = dict(row_ptr=cfg.get("row_ptr"), entries=cfg.get("entries"), uniforms=cfg["uniforms"])
+    if cfg.get("bitmask") is not None:
+        kw.update(bitmask=cfg["bitmask"], mask_bits=cfg["mask_bits"],
+                  mask_tail=cfg.get("mask_tail", 0))
+    stream = torch.cuda.Stream(device=dev)
+    res = {}
+    for k in (args.top_k, -1):
+        preps = [ctx.prepare_step(copies[i], cfg["params"], logprobs_top_k=k, **kw)
+                 for i in range(R)]
+        with torch.cuda.stream(stream):
+            for p in preps:
+                p.launch(stream.cuda_stream)
+        torch.cuda.synchronize()
+        launch = ctx.last_launch()
+        run = graph_runner([(lambda p=p: p.launch(stream.cuda_stream)) for p in preps], stream)
+        wall_s, ev_ms = time_steps(run, stream, steps, warm)
+        res[k] = (wall_s, 1e3 * ev_ms / steps, launch)
+        del preps, run
+        torch.cuda.synchronize()
+    # the second pass alone (lsamp_logprobs), which the step no longer makes
+    tok = torch.zeros(B, dtype=torch.int32, device=dev)
+    lps = [ctx.prepare_logprobs(copies[i], tokens=tok, top_k=args.top_k) for i in range(R)]
+    with torch.cuda.stream(stream):
+        for p in lps:
+            p.launch(stream.cuda_stream)
+    torch.cuda.synchronize()
+    run = graph_runner([(lambda p=p: p.launch(stream.cuda_stream)) for p in lps], stream)
+    _, ev_lp = time_steps(run, stream, steps, warm)
+    wall_s, us, launch = res[args.top_k]
+    wall0, us0, launch0 = res[-1]
+    out = {
+        "metric": f"sampling steps/s with raw log-probabilities (top {args.top_k}) at B={B} V={V} "
+                  "(lsamp_step, fused sampling kernel)",
+        "value": steps / wall_s, "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": 1e3 * wall_s / steps, "us_per_step_events": us,
+        "us_per_step_without_logprobs": us0, "logprob_cost_ratio": us / us0,
+        "us_second_pass_lsamp_logprobs": 1e3 * ev_lp / steps,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": cfg["workload"] + f" + log-probs top {args.top_k} (no commit)",
+                   "input_copies": R, "launch": launch, "launch_without_logprobs": launch0,
+                   "kernels": sample_kernel_name(launch) +
+                   (" with raw log-probabilities" if launch["fused"] == 4 else " + k_rank")},
         "roofline": None, "cpu_baseline": None,
     }
     ctx.close()

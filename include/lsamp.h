@@ -354,9 +354,10 @@ lsamp_status lsamp_context_read_status(lsamp_context* ctx, uint32_t* bits);
 /* (The test hook of the bounded waits is declared apart, in lsamp_testing.h.) */
 
 /* Launch shape of the context's last lsamp_sample call (diagnostics; no
- * device work): top-k with raw log-probabilities (3, lsamp_step), top-k (2),
- * fused (1) or split (0), slices per row, tokens per slice, rows per round of
- * the fused grid, work-groups per kernel launch. */
+ * device work): fused with raw log-probabilities (4, lsamp_step), top-k with
+ * raw log-probabilities (3, lsamp_step), top-k (2), fused (1) or split (0),
+ * slices per row, tokens per slice, rows per round of the fused grid,
+ * work-groups per kernel launch. */
 typedef struct lsamp_launch_info {
   int32_t fused;
   int32_t slices;

@@ -282,12 +282,23 @@ lsamp_status lsamp::sample_step(const WorkspaceViews& v, const DeviceShape& d, i
     P.mask_bits = a->vocab;
     P.mask_tail = LSAMP_MASK_TAIL_KEEP;
   }
-  // raw log-probabilities in the same launch: the top-k kernel, 16-bit logits
+  // raw log-probabilities in the same launch: the top-k kernel (16-bit
+  // logits), or the fused sampling kernel (any dtype)
   const bool lp_fused = topk && lp && lp->k >= 0 && a->dtype != LSAMP_DTYPE_F32;
+  const bool lp_sample = !topk && P.fused && lp && lp->k >= 0;
   TopkLp lpk{};
   lpk.k = -1;
   if (lp_fused) lpk = *lp;
-  last->fused = topk ? (lp_fused ? 3 : 2) : P.fused;
+  FusedLp flp{};
+  flp.k = -1;
+  if (lp_sample) {
+    flp.k = lp->k;
+    flp.chosen = lp->chosen;
+    flp.values = lp->values;
+    flp.ids = lp->ids;
+    flp.rec = v.rawrec;
+  }
+  last->fused = topk ? (lp_fused ? 3 : 2) : (lp_sample ? 4 : P.fused);
   last->slices = P.slices;
   last->slice_len = P.slice_len;
   last->rows_per_round = P.rows_per_round;
@@ -295,10 +306,11 @@ lsamp_status lsamp::sample_step(const WorkspaceViews& v, const DeviceShape& d, i
                     : P.fused ? (P.rows < P.rows_per_round ? P.rows : P.rows_per_round) * P.slices
                               : P.rows * P.slices;
   const int err =
-      topk ? launch_topk(P, v.topk, lpk, stream, ev) : launch_sample(v.ws, P, stream, ev);
+      topk ? launch_topk(P, v.topk, lpk, stream, ev)
+           : launch_sample(v.ws, P, lp_sample ? &flp : nullptr, stream, ev);
   if (err != 0) return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s",
                             hipGetErrorString((hipError_t)err));
-  if (lp_done) *lp_done = lp_fused;
+  if (lp_done) *lp_done = lp_fused || lp_sample;
   return ok();
 }
 
@@ -987,7 +999,7 @@ lsamp_status lsamp_verify(lsamp_context* ctx, const lsamp_verify_args* a, void* 
   Q.parts = a->mode == LSAMP_VERIFY_RESIDUAL ? (int32_t)verify_parts((size_t)a->vocab) : 1;
   DeviceGuard guard(ctx->device);
   int err = penalized ? launch_window_entries(E, stream) : 0;
-  if (err == 0) err = launch_sample(ctx->ws, P, stream, nullptr);
+  if (err == 0) err = launch_sample(ctx->ws, P, nullptr, stream, nullptr);
   if (err == 0) err = launch_verify_finish(ctx->ws, Q, stream);
   if (err != 0)
     return fail(LSAMP_ERR_DEVICE, "kernel launch failed: %s", hipGetErrorString((hipError_t)err));

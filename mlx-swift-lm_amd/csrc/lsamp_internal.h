@@ -200,6 +200,19 @@ constexpr int kTopkWordsBase = kTopkHead + 2 * kTopkMaxK;  // + (value, id) per 
 // log-probabilities (the payload stride is the larger size either way)
 constexpr int kTopkRawWords = 2 * kTopkMaxLp;
 constexpr int kTopkWords = kTopkWordsBase + kTopkRawWords;
+// A slice's record of the fused sampling kernel's in-pass raw
+// log-probabilities (FusedLp, below): its largest non-NaN raw logit, NaN /
+// +inf flags, the sum of exp(x - max) over its raw logits, and its best
+// raw keys in order.
+struct RawRecord {
+  float max;
+  uint32_t flags;
+  int32_t n;  // keys
+  int32_t pad;
+  double z;
+  uint64_t keys[kTopkMaxLp];
+};
+
 struct TopkWs {
   uint64_t* pub;     // [max_rows][kMaxSlices][kTopkWords]
   uint32_t* ticket;  // [max_rows]
@@ -214,7 +227,7 @@ struct TopkWs {
 // the end of every step.
 struct WorkspaceLayout {
   size_t sum, rows, chunk, cand, klist, part, status, tasks, cc, as, asel, tticket, vtick;
-  size_t vstats, vtok, vfl, vspan, rpart, arank, vrp, vrl, smask, tpub, tepoch;
+  size_t vstats, vtok, vfl, vspan, rpart, arank, vrp, vrl, smask, tpub, tepoch, rawrec;
   size_t zero_begin, zero_end, total;
 };
 constexpr size_t align256(size_t v) { return (v + 255) / 256 * 256; }
@@ -252,6 +265,7 @@ constexpr WorkspaceLayout workspace_layout(size_t R, size_t max_vocab) {
   // earlier step must never carry the current step's tag)
   L.tpub = off;   off = align256(off + R * kMaxSlices * kTopkWords * sizeof(uint64_t));
   L.tepoch = off; off = align256(off + R * sizeof(uint32_t));
+  L.rawrec = off; off = align256(off + R * kMaxSlices * sizeof(RawRecord));
   L.total = off;
   return L;
 }
@@ -368,13 +382,28 @@ struct TopkLp {
 };
 int launch_topk(const SamplePlan& plan, const TopkWs& tw, const TopkLp& lp, void* stream,
                 void* const* events);
+
+// Raw log-probabilities in the fused sampling kernel's own pass over the
+// logits (lsamp_step): each slice publishes a record before its first
+// exchange (its largest non-NaN raw logit, the sum of exp(x - max) over its
+// raw logits, NaN / +inf flags, and its k best raw keys in order), and the
+// row's finalizer merges the records once the token is drawn.
+struct FusedLp {
+  int32_t k;        // -1: none; else 0 .. kTopkMaxLp
+  float* chosen;    // [rows]
+  float* values;    // [rows, k]
+  int32_t* ids;     // [rows, k]
+  RawRecord* rec;   // [max_rows][kMaxSlices] (in the workspace)
+};
 // Work-groups of the top-k kernel that fit on one CU.
 int topk_blocks_per_cu(int dtype);
 
 // Kernel launchers (lsamp_kernels.hip).  Return a hipError_t as int.
 // `events` (3 hipEvent_t or NULL) bracket the step: before, between the two
 // kernels (split mode; same as before in fused mode), after.
-int launch_sample(const Workspace& ws, const SamplePlan& plan, void* stream, void* const* events);
+// `lp` (or NULL): raw log-probabilities in the same pass (fused steps only).
+int launch_sample(const Workspace& ws, const SamplePlan& plan, const FusedLp* lp, void* stream,
+                  void* const* events);
 // Work-groups of the fused kernel that fit on one CU (occupancy query).
 int fused_blocks_per_cu(int dtype);
 // Acceptance, residual / bonus draws and outputs of an MTP verification whose
@@ -473,6 +502,7 @@ struct WorkspaceViews {
   uint32_t* smask;        // [max_rows][smask_words]: bitmask with suppressed ids
   int32_t smask_words;
   TopkWs topk;            // the one-pass top-k kernel's exchange
+  RawRecord* rawrec;      // [max_rows][kMaxSlices]: in-pass raw log-probability records
   char* zero_begin;       // the words that must start at zero
   size_t zero_bytes;
 };
@@ -509,6 +539,7 @@ inline WorkspaceViews bind_workspace(char* b, int32_t max_rows, int32_t max_voca
   v.topk.pub = reinterpret_cast<uint64_t*>(b + L.tpub);
   v.topk.ticket = reinterpret_cast<uint32_t*>(b + L.tticket);
   v.topk.epoch = reinterpret_cast<uint32_t*>(b + L.tepoch);
+  v.rawrec = reinterpret_cast<RawRecord*>(b + L.rawrec);
   v.topk.status = ws.status;
   v.zero_begin = b + L.zero_begin;
   v.zero_bytes = L.zero_end - L.zero_begin;

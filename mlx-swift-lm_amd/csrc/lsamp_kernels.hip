@@ -258,6 +258,7 @@ struct TaskLds {
   int32_t x1;           // first exchange's last arriver of a row that fell back
   int32_t xlast;        // this work-group made the exchange's last arrival
   int32_t job;          // the slice of the claimed job, or -1
+  int32_t nraw;         // raw log-probability candidates listed
   int32_t from_stats;   // claim scans: the next slice to try
   int32_t from_select;
   uint32_t flags;
@@ -511,6 +512,15 @@ constexpr int kSlotsPerLane = kChunk / 64;           // draw slots per lane
 // of kSlotsPerLane with one pad word per run (no bank conflicts).
 __device__ __forceinline__ int draw_slot(int o) { return o + (o >> 4); }
 
+// The row's raw log-probabilities, once its token is drawn (defined with
+// the rest of the in-pass log-probabilities below).
+template <int DT>
+__device__ __forceinline__ void raw_chosen(const SamplePlan& P, const FusedLp& lp, int row,
+                                           int32_t tok, const char* rowp);
+template <int DT>
+__device__ __forceinline__ void raw_lists(const SamplePlan& P, const FusedLp& lp, int row,
+                                          uint64_t* lists);
+
 // What the finalize tail needs besides the sorted candidates in F.keys.
 struct TailIn {
   int nc;           // candidates in F.keys, sorted by cand_key descending
@@ -534,7 +544,8 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
                                               const RowCtx& c, const lsamp_row_params& prm,
                                               const RowInfo& info, TaskLds& L, const char* rowp,
                                               const uint32_t* mrow, const TailIn& t,
-                                              uint64_t (&rch)[kChunksPerLane]) {
+                                              uint64_t (&rch)[kChunksPerLane],
+                                              const FusedLp* lp) {
   const int l = fresh_tid() & 63;
   const int64_t V = P.vocab;
   const float y_max = info.mode == kModePosInf ? kPosInf : to_filter(c, info.x_max);
@@ -851,13 +862,14 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
       ws.arrive_select[row] = 0u;
     }
   }
+  if (lp) raw_chosen<DT>(P, *lp, row, overflow ? -1 : token, rowp);
 }
 
 
 template <int DT>
 __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
                              const lsamp_row_params& prm, const RowInfo& info, TaskLds& L,
-                             const char* rowp, const uint32_t* mrow) {
+                             const char* rowp, const uint32_t* mrow, const FusedLp* lp) {
   const int tid = fresh_tid();
   const int l = tid & 63;
   const bool wave0 = tid < 64;
@@ -972,7 +984,12 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
       }
     }
   }
-  if (!wave0) return;
+  if (!wave0) {
+    // (wave 1: the raw log-probability lists, beside wave 0's draw, in the
+    // staging area no finalize uses)
+    if (lp && tid < 128) raw_lists<DT>(P, *lp, row, reinterpret_cast<uint64_t*>(L.sh.squad));
+    return;
+  }
   if (nc > 0 && nc <= 64) {
     // rank sort of the wave's own keys (keys are distinct: ids are)
     const uint64_t key = l < nc ? key0 : 0ull;
@@ -998,7 +1015,7 @@ __device__ __forceinline__ void finalize_row(const Workspace& ws, const SamplePl
   t.n_list = part.n_list;
   t.reset = true;
   t.done = 0;
-  finalize_tail<DT>(ws, P, row, c, prm, info, L, rowp, mrow, t, rch);
+  finalize_tail<DT>(ws, P, row, c, prm, info, L, rowp, mrow, t, rch, lp);
 }
 
 // Single-wave tail of a short-list row with at most 64 candidates (lane r
@@ -1009,7 +1026,7 @@ template <int DT>
 __device__ __forceinline__ void short_tail(const Workspace& ws, const SamplePlan& P, int row,
                                            const RowCtx& c, const lsamp_row_params& prm,
                                            const RowInfo& info, TaskLds& L, int nc, float u_draw,
-                                           int32_t probe) {
+                                           int32_t probe, const char* rowp, const FusedLp* lp) {
   const int l = fresh_tid() & 63;
   const int64_t V = P.vocab;
   FinalLds& F = L.u.f;
@@ -1131,6 +1148,7 @@ __device__ __forceinline__ void short_tail(const Workspace& ws, const SamplePlan
     out.done = 1;
     ws.rows[row] = out;
   }
+  if (lp) raw_chosen<DT>(P, *lp, row, token, rowp);
 }
 
 // Short-list finalize (the last work-group of a short-list row to publish).
@@ -1236,7 +1254,7 @@ template <int DT>
 __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePlan& P, int row,
                                              const RowCtx& c, const lsamp_row_params& prm,
                                              TaskLds& L, const char* rowp, const uint32_t* mrow,
-                                             int K) {
+                                             int K, const FusedLp* lp) {
   const int tid = fresh_tid();
   const bool wave0 = tid < 64;
   const int G = P.slices;
@@ -1376,14 +1394,19 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
       if ((uint32_t)(F.keys[i] >> 32) < kv && (uint32_t)(F.keys[i - 1] >> 32) >= kv) L.misc[6] = i;
   }
   lds_barrier();
-  if (!wave0) return;
+  if (!wave0) {
+    // (wave 1: the raw log-probability lists, beside wave 0's draw, in the
+    // staging area no finalize uses)
+    if (lp && tid < 128) raw_lists<DT>(P, *lp, row, reinterpret_cast<uint64_t*>(L.sh.squad));
+    return;
+  }
   int nc = L.misc[6];
   const RowInfo info = L.info;
   if (info.mode != kModeNormal) nc = 0;
   const float u_draw = __uint_as_float((uint32_t)L.misc64[0]);
   const int32_t probe = L.misc[4];
   if (nc <= 64) {
-    short_tail<DT>(ws, P, row, c, prm, info, L, nc, u_draw, probe);
+    short_tail<DT>(ws, P, row, c, prm, info, L, nc, u_draw, probe, rowp, lp);
     return;
   }
   TailIn t;
@@ -1402,7 +1425,454 @@ __device__ __forceinline__ void short_finish(const Workspace& ws, const SamplePl
   uint64_t rch[kChunksPerLane];
 #pragma unroll
   for (int i = 0; i < kChunksPerLane; ++i) rch[i] = 0ull;
-  finalize_tail<DT>(ws, P, row, c, prm, info, L, rowp, mrow, t, rch);
+  finalize_tail<DT>(ws, P, row, c, prm, info, L, rowp, mrow, t, rch, lp);
+}
+
+// ==================================================== raw log-probabilities
+// In-pass raw log-probabilities of the fused arrangement (lsamp_step asking
+// for them): the reference takes raw - logSumExp(raw) before any transform
+// and gathers the chosen token and the k best by the raw order, value
+// descending, lower id on ties, +0 and -0 tied (LogitsPipelineV2.process
+// :307-314, CBv2Logprobs.gather :534-549).  Pass 1 of each slice's own pass
+// takes the raw logits' statistics before any exclusion (raw_add); the slice
+// then lists its k best raw keys (raw_slice) and publishes a record before
+// its first exchange; the row's finalizer merges the records: wave 1 the
+// lists (raw_lists) while wave 0 draws, wave 0 the chosen token's value
+// once it is drawn (raw_chosen).  A row whose log-sum-exp is not finite (a NaN or
+// +inf logit, or every logit -inf) fails closed: ids -1 and NaN values
+// (CBv2NonFiniteLogits.swift:30-38).
+constexpr uint32_t kRawNan = 1u, kRawPosInf = 2u;
+constexpr int kRawList = kThreads;       // candidates ranked by counting
+constexpr int kRawOut = kRawList;        // the sorted best k follow them
+static_assert(kRawOut + kTopkMaxLp <= kCandCap, "the raw lists fit the finalize keys");
+
+// Position of the n-th (from 0) set bit of m (n < popcount(m)).
+__device__ __forceinline__ int nth_set_bit(uint64_t m, int n) {
+  int pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const int c = (int)__popcll(m & ((1ull << w) - 1ull));
+    if (n >= c) {
+      n -= c;
+      m >>= w;
+      pos += w;
+    }
+  }
+  return pos;
+}
+
+static_assert(sizeof(ShortLds::squad) >= kMaxSlices * kTopkMaxLp * sizeof(uint64_t),
+              "the raw lists fit the staging area");
+
+struct RawAcc {
+  float m;         // largest non-NaN raw logit
+  float z;         // sum of exp2(x * log2e + nb) over the thread's raw logits
+  float nb;        // its anchor: an integer, re-set by an exact power of two
+  uint32_t flags;  // kRawNan, kRawPosInf
+};
+
+// One quad of raw logits into the thread's statistics (lanes past the slice
+// end excluded by `tail`; `probe` flags a NaN or infinity in the quad).
+template <int DT>
+__device__ __forceinline__ void raw_add(RawAcc& a, uint4 v, uint32_t tail, uint32_t probe) {
+  constexpr int N = Vec<DT>::N;
+  constexpr float kLog2e = 1.4426950408889634f;
+  exclude_elems<DT>(v, tail);
+  float q = vec_max_nn<DT>(v);
+  if (nonfinite_seen<DT>(probe)) {
+    // (rare) NaN and +inf flags; the maximum of the others
+    q = kNegInf;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      const float x = vec_elem<DT>(v, e);
+      if (x != x) a.flags |= kRawNan;
+      if (x == kPosInf) a.flags |= kRawPosInf;
+      q = __builtin_fmaxf(q, x);
+    }
+  }
+  a.m = __builtin_fmaxf(a.m, q);
+  if (__builtin_fmaf(q, kLog2e, a.nb) > 64.0f) {
+    const float nn = -__builtin_ceilf(__builtin_amdgcn_fmed3f(q * kLog2e, -0x1p20f, 0x1p20f));
+    a.z = __builtin_ldexpf(a.z, (int)__builtin_fmaxf(nn - a.nb, -512.0f));
+    a.nb = nn;
+  }
+  float t[N];
+#pragma unroll
+  for (int e = 0; e < N; ++e)
+    t[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(vec_elem<DT>(v, e), kLog2e, a.nb));
+#pragma unroll
+  for (int w = 1; w < N; w *= 2)
+#pragma unroll
+    for (int e = 0; e < N; e += 2 * w) t[e] += t[e + w];
+  a.z += t[0];
+}
+
+// The exact K-th largest raw key of the slice (a radix select over the
+// slice read again, eight bits a round), then every key at or above it
+// listed in `dst`: min(K, slice length) keys.  For slices whose threshold
+// leaves too many candidates (many equal logits, or -inf ones).  Whole
+// work-group; its counts use the thread-maximum histogram's words.
+template <int DT>
+__device__ __forceinline__ int raw_select_exact(const char* rowp, int32_t base32, int32_t end32,
+                                                int K, uint64_t* dst, TaskLds& L) {
+  const int tid = fresh_tid();
+  const int len = end32 - base32;
+  if (K > len) K = len;
+  uint32_t* const cnt = L.sh.tcnt;
+  uint64_t prefix = 0ull;
+  int need = K;
+#pragma unroll 1
+  for (int shift = 56; shift >= 0; shift -= 8) {
+    const uint64_t hmask = shift == 56 ? 0ull : ~0ull << (shift + 8);
+    for (int i = tid; i < 256; i += kThreads) cnt[i] = 0u;
+    __syncthreads();
+#pragma unroll 1
+    for (int32_t i = base32 + tid; i < end32; i += kThreads) {
+      const uint64_t key = cand_key(load_scalar<DT>(rowp, i), i);
+      if ((key & hmask) == prefix) atomicAdd(&cnt[(key >> shift) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // digits from the top: lane l holds digits 255 - 4l .. 252 - 4l
+      uint32_t cb[4];
+      uint32_t cs = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        cb[i] = cnt[255 - (4 * tid + i)];
+        cs += cb[i];
+      }
+      const uint32_t ic = wave_incl_scan(cs);
+      const uint64_t hit = __ballot(ic >= (uint32_t)need);
+      const int f = hit ? __builtin_ctzll(hit) : 63;
+      uint32_t acc = read_lane(ic - cs, f);
+      int digit = 0, above = 0;
+      if (tid == f) {
+        for (int i = 0; i < 4; ++i) {
+          if (acc + cb[i] >= (uint32_t)need) {
+            digit = 255 - (4 * tid + i);
+            above = (int)acc;
+            break;
+          }
+          acc += cb[i];
+        }
+      }
+      digit = read_lane(digit, f);
+      above = read_lane(above, f);
+      if (tid == 0) {
+        L.misc[0] = digit;
+        L.misc[1] = above;
+      }
+    }
+    __syncthreads();
+    prefix |= (uint64_t)(uint32_t)L.misc[0] << shift;
+    need -= L.misc[1];
+  }
+  if (tid == 0) L.nraw = 0;
+  __syncthreads();
+#pragma unroll 1
+  for (int32_t i0 = base32; i0 < end32; i0 += kThreads) {
+    const int32_t i = i0 + tid;
+    const float x = i < end32 ? load_scalar<DT>(rowp, i) : 0.0f;
+    const bool hit = i < end32 && cand_key(x, i) >= prefix;
+    const int slot = wave_append(hit, &L.nraw);
+    if (hit && slot < K) dst[slot] = cand_key(x, i);
+  }
+  __syncthreads();
+  return K;
+}
+
+// The slice's raw record (whole work-group, after pass 1): its maximum, its
+// sum relative to the maximum and its flags; with k > 0 and finite logits,
+// its k best raw keys.  Threshold: each wave's c-th largest thread maximum
+// (c = ceil(k / 8)), the smallest over the waves, so at least k tokens reach
+// it; the threads whose maximum reaches it read their logits again (from
+// L2) and list the keys at or above it, which are ranked by counting.  A
+// slice whose threshold leaves more than kRawList candidates takes the
+// exact select.  Leaves the short-list and histogram words zeroed.
+template <int DT>
+__device__ __forceinline__ void raw_slice(const SamplePlan& P, const FusedLp& lp, int row,
+                                          int slice, const char* rowp, int32_t base32,
+                                          int32_t end32, int nq, const RawAcc& a, TaskLds& L) {
+  constexpr int N = Vec<DT>::N;
+  constexpr float kLog2e = 1.4426950408889634f;
+  const int tid = fresh_tid(), l = tid & 63, wv = tid >> 6;
+  const int K = lp.k;
+  // 1. the slice's flags, maximum, and sum relative to the maximum
+  const uint32_t fw = (__ballot((a.flags & kRawNan) != 0u) ? kRawNan : 0u) |
+                      (__ballot((a.flags & kRawPosInf) != 0u) ? kRawPosInf : 0u);
+  const float mw = wave_max(a.m);
+  __syncthreads();
+  if (l == 0) {
+    L.redf[wv] = mw;
+    L.redi[wv] = (int32_t)fw;
+  }
+  __syncthreads();
+  float M = L.redf[0];
+  uint32_t F = (uint32_t)L.redi[0];
+#pragma unroll
+  for (int i = 1; i < kWaves; ++i) {
+    M = __builtin_fmaxf(M, L.redf[i]);
+    F |= (uint32_t)L.redi[i];
+  }
+  double zt = 0.0;
+  if (a.z > 0.0f && M > kNegInf && M < kPosInf) {
+    // the thread's terms rescaled from 2^-nb to e^M (M * log2e split into a
+    // rounded part and its exact residual)
+    const float bh = M * kLog2e;
+    const float bl = __builtin_fmaf(M, kLog2e, -bh);
+    zt = (double)(a.z * __builtin_amdgcn_exp2f((-a.nb - bh) - bl));
+  }
+  zt = wave_sum(zt);
+  __syncthreads();
+  if (l == 0) L.redd[wv] = zt;
+  __syncthreads();
+  double zsum = 0.0;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) zsum += L.redd[i];
+
+  // 2. the k best raw keys
+  int listed = 0;
+  uint64_t* const cand = L.u.f.keys;
+  if (K > 0 && F == 0u) {
+    const int c = (K + kWaves - 1) / kWaves;
+    bool taken = false;
+    float wc = kNegInf;
+    for (int i = 0; i < c; ++i) {
+      const float mx = wave_max(taken ? kNegInf : a.m);
+      const uint64_t hit = __ballot(!taken && a.m == mx);
+      if (hit != 0ull && l == __builtin_ctzll(hit)) taken = true;
+      wc = mx;
+    }
+    if (l == 0) L.redf2[wv] = wc;
+    if (tid == 0) L.nraw = 0;
+    __syncthreads();
+    float tau = L.redf2[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) tau = __builtin_fminf(tau, L.redf2[i]);
+    int n = kRawList + 1;
+    if (tau > kNegInf) {
+      // 3. candidates: the logits of the threads whose maximum reaches tau,
+      // read again by their whole wave at once: the wave's (thread, quad)
+      // pairs are dealt to its lanes, kRePer 16-byte loads a lane in flight
+      // together (through one buffer descriptor over the slice, as pass 1
+      // loads them), so up to 64 * kRePer pairs take one round trip.  The
+      // last partial quad and unaligned rows are read element by element.
+      constexpr int ES = Vec<DT>::ESIZE;
+      constexpr int kRePer = N == 4 ? 4 : 2;  // (fp32 slices: more quads a thread)
+      const bool aligned = P.aligned != 0;
+      const uint64_t mm = __ballot(a.m >= tau);
+      const int pairs = (int)__popcll(mm) * nq;  // (wave-uniform)
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(rowp) + (size_t)base32 * ES, 0, aligned ? (end32 - base32) * ES : 0,
+          kBufferWord3);
+#pragma unroll 1
+      for (int p0 = 0; p0 < pairs; p0 += 64 * kRePer) {
+        uint4 w[kRePer];
+        int32_t i0s[kRePer];
+#pragma unroll
+        for (int j = 0; j < kRePer; ++j) {
+          const int pr = p0 + j * 64 + l;
+          const bool in = pr < pairs;
+          // pair pr: quad pr % nq of the wave's (pr / nq)-th reading thread
+          const int t = wv * 64 + nth_set_bit(mm, in ? pr / nq : 0);
+          const int qd = t + (in ? pr % nq : 0) * kThreads;  // the quad's place in the slice
+          i0s[j] = in ? base32 + qd * N : end32;             // (past the end: nothing listed)
+          const auto r = __builtin_amdgcn_raw_buffer_load_b128(rs, in ? qd * 16 : 0x40000000, 0, 0);
+          w[j] = make_uint4(r[0], r[1], r[2], r[3]);
+        }
+#pragma unroll
+        for (int j = 0; j < kRePer; ++j) {
+          const int32_t i0 = i0s[j];
+          if (i0 < end32 && (!aligned || i0 + N > end32)) {
+            uint32_t b[N];
+#pragma unroll
+            for (int e = 0; e < N; ++e) b[e] = i0 + e < end32 ? load_raw_bits<DT>(rowp, i0 + e) : 0u;
+            if constexpr (N == 4) {
+              w[j] = make_uint4(b[0], b[1], b[2], b[3]);
+            } else {
+              w[j] = make_uint4(b[0] | (b[1] << 16), b[2] | (b[3] << 16), b[4] | (b[5] << 16),
+                                b[6] | (b[7] << 16));
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < N; ++e) {
+            const float x = vec_elem<DT>(w[j], e);
+            const bool hit = i0 + e < end32 && x >= tau;
+            const int slot = wave_append(hit, &L.nraw);
+            if (hit && slot < kRawList) cand[slot] = cand_key(x, i0 + e);
+          }
+        }
+      }
+      __syncthreads();
+      n = L.nraw;
+    }
+    if (n > kRawList) {
+      n = raw_select_exact<DT>(rowp, base32, end32, K, cand, L);
+      // (its counts used the words the rank counts in)
+      for (int i = tid; i < kRawList; i += kThreads) L.sh.tcnt[i] = 0u;
+      __syncthreads();
+    }
+    // 4. rank by counting, spread over the work-group: key i's count of
+    // the keys above it is summed over C chunks of the list (C = kThreads
+    // over n rounded up to a power of two), one (key, chunk) pair a thread;
+    // a wave's pairs share their chunk, so its reads are broadcasts.  The
+    // counts gather in the thread-maximum histogram's words (zero here).
+    uint32_t* const above = L.sh.tcnt;
+    static_assert(kTauBins >= kRawList, "a count per candidate");
+    if (n > 0) {
+      const int np = n <= 64 ? 64 : n <= 128 ? 128 : n <= 256 ? 256 : 512;
+      const int C = kThreads / np;
+      const int span = (n + C - 1) / C;
+      const int i = tid & (np - 1), ch = tid / np;
+      if (i < n) {
+        const uint64_t key = cand[i];
+        const int j0 = ch * span, j1 = j0 + span < n ? j0 + span : n;
+        int r = 0, jj = j0;
+        for (; jj + 4 <= j1; jj += 4) {  // (four reads in flight)
+          const uint64_t c0 = cand[jj], c1 = cand[jj + 1], c2 = cand[jj + 2], c3 = cand[jj + 3];
+          r = add_gt_u64(add_gt_u64(add_gt_u64(add_gt_u64(r, c0, key), c1, key), c2, key), c3, key);
+        }
+        for (; jj < j1; ++jj) r = add_gt_u64(r, cand[jj], key);
+        if (r != 0) atomicAdd(&above[i], (uint32_t)r);
+      }
+      __syncthreads();
+      if (tid < n) {
+        const uint32_t r = above[tid];
+        if (r < (uint32_t)K) cand[kRawOut + r] = cand[tid];
+      }
+    }
+    __syncthreads();
+    listed = n < K ? n : K;
+  }
+  // 5. the record
+  RawRecord* rec = lp.rec + (size_t)row * kMaxSlices + slice;
+  if (tid < listed) st_coherent(&rec->keys[tid], cand[kRawOut + tid]);
+  if (tid == 0) {
+    st_coherent_f32(&rec->max, M);
+    st_coherent(&rec->flags, F);
+    st_coherent(&rec->n, listed);
+    st_coherent_f64(&rec->z, zsum);
+  }
+  // the words the slice's short list and histogram count on
+  if (K > 0) {
+    for (int i = tid; i < kHist + 64; i += kThreads) L.u.hist[i] = 0ull;
+    for (int i = tid; i < kTauBins; i += kThreads) L.sh.tcnt[i] = 0u;
+  }
+  __syncthreads();
+}
+
+// The row's log-sum-exp of the raw logits from the slices' records (one
+// wave; every wave that calls it computes the same value): lane l < G
+// returns record l's key count.  A row with a NaN or +inf logit, or with
+// every logit -inf, is closed.
+struct RawHead {
+  float lse;
+  bool closed;
+  int32_t n;  // (lane l < G) record l's listed keys
+};
+__device__ __forceinline__ RawHead raw_head(const SamplePlan& P, const FusedLp& lp, int row) {
+  const int l = fresh_tid() & 63;
+  const int G = P.slices;
+  const RawRecord* rec = lp.rec + (size_t)row * kMaxSlices;
+  float ms = kNegInf;
+  double zs = 0.0;
+  uint32_t fs = 0u;
+  int32_t ns = 0;
+  if (l < G) {
+    ms = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&rec[l].max)));
+    fs = ld_coherent(&rec[l].flags);
+    ns = ld_coherent(&rec[l].n);
+    zs = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&rec[l].z)));
+  }
+  const float M = wave_max(ms);
+  RawHead h;
+  h.closed = __ballot(fs != 0u) != 0ull || !(M > kNegInf);
+  const double z = wave_sum((l < G && ms > kNegInf) ? zs * fexp((double)ms - (double)M) : 0.0);
+  h.lse = h.closed ? 0.0f : M + __builtin_logf((float)z);
+  h.n = ns;
+  return h;
+}
+
+// The chosen token's raw log-probability (wave 0 of the finalizing work-
+// group, once the token is drawn; NaN for a closed row or no token).
+template <int DT>
+__device__ __forceinline__ void raw_chosen(const SamplePlan& P, const FusedLp& lp, int row,
+                                           int32_t tok, const char* rowp) {
+  const int l = fresh_tid() & 63;
+  const bool tok_in = tok >= 0 && tok < P.vocab;
+  const float xc = (l == 0 && tok_in) ? load_scalar<DT>(rowp, tok) : 0.0f;
+  const RawHead h = raw_head(P, lp, row);
+  if (l == 0) lp.chosen[row] = (!h.closed && tok_in) ? xc - h.lse : __builtin_nanf("");
+}
+
+// The row's k best raw log-probabilities (one wave of the finalizing work-
+// group, beside wave 0's draw: they do not depend on the token; `lists`
+// holds kMaxSlices * kTopkMaxLp words of LDS the draw does not use).  Every
+// load is issued at once: the records' heads and each key slot a record can
+// list (slots past its count are dropped once the counts are in).
+template <int DT>
+__device__ __forceinline__ void raw_lists(const SamplePlan& P, const FusedLp& lp, int row,
+                                          uint64_t* lists) {
+  constexpr int kPer = kMaxSlices * kTopkMaxLp / 64;  // key slots a lane loads
+  static_assert(kPer * 64 == kMaxSlices * kTopkMaxLp, "whole lanes");
+  const int l = fresh_tid() & 63;
+  const int G = P.slices, K = lp.k;
+  if (K <= 0) return;
+  const RawRecord* rec = lp.rec + (size_t)row * kMaxSlices;
+  uint64_t kv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = l + 64 * j, s = i / kTopkMaxLp, p = i % kTopkMaxLp;
+    kv[j] = (s < G && p < K) ? ld_coherent(&rec[s].keys[p]) : 0ull;
+  }
+  const RawHead h = raw_head(P, lp, row);
+  // the keys into LDS, the slots past their record's count as zeros
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = l + 64 * j, s = i / kTopkMaxLp, p = i % kTopkMaxLp;
+    const int n_s = __shfl(h.n, s, 64);
+    lists[i] = (s < G && p < n_s) ? kv[j] : 0ull;
+  }
+  // ranks 0 .. listed - 1 each take one key (keys are distinct); the slots
+  // past them, and a closed row's, read (-1, NaN)
+  const int listed = h.closed ? 0 : wave_sum(l < G ? h.n : 0);
+  if (l < K && l >= listed) {
+    lp.ids[(size_t)row * K + l] = -1;
+    lp.values[(size_t)row * K + l] = __builtin_nanf("");
+  }
+  if (h.closed) return;
+  __builtin_amdgcn_wave_barrier();
+  // a key's rank: its place in its own list plus, in every other list,
+  // the keys above it (lists are sorted descending and padded with zeros,
+  // below every key): fixed-step searches, two lists at a time
+  static_assert(kTopkMaxLp == 32, "five halving steps and a last check");
+#pragma unroll 1
+  for (int j = 0; j < kPer; ++j) {
+    const int i = l + 64 * j, s = i / kTopkMaxLp;
+    const uint64_t key = lists[i];
+    if (s >= G || key == 0ull) continue;
+    int r = i % kTopkMaxLp;
+    constexpr int kAtOnce = 2;  // lists searched together
+#pragma unroll 1
+    for (int s0 = 0; s0 < G; s0 += kAtOnce) {
+      int lo[kAtOnce];
+#pragma unroll
+      for (int u = 0; u < kAtOnce; ++u) lo[u] = 0;
+#pragma unroll
+      for (int step = kTopkMaxLp / 2; step >= 1; step >>= 1)
+#pragma unroll
+        for (int u = 0; u < kAtOnce; ++u)
+          if (s0 + u < G && lists[(s0 + u) * kTopkMaxLp + lo[u] + step - 1] > key) lo[u] += step;
+#pragma unroll
+      for (int u = 0; u < kAtOnce; ++u)
+        if (s0 + u < G && s0 + u != s)
+          r += lo[u] + (lists[(s0 + u) * kTopkMaxLp + lo[u]] > key ? 1 : 0);
+    }
+    if (r < K) {
+      lp.ids[(size_t)row * K + r] = key_id(key);
+      lp.values[(size_t)row * K + r] = key_y(key) - h.lse;
+    }
+  }
 }
 
 // ================================================================ one task
@@ -1432,10 +1902,12 @@ __device__ __forceinline__ int next_job(int kind, int slice) { return (kind << 8
 // `slice` of a slice that left (kBehalfStats, kSelectOnly); `own` is its own
 // slice.  (Each job is its own instantiation, so the own pass compiles as
 // if the others did not exist.)
-template <int DT, int MODE, int JM>
+template <int DT, int MODE, int JM, bool LP>
 __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& P, int row, int slice,
-                                         TaskLds& L, int own) {
+                                         TaskLds& L, int own, const FusedLp& Lk) {
   constexpr int jm = JM;
+  // (LP: raw log-probabilities in this pass; the finalizer writes them)
+  const FusedLp* const lpp = LP ? &Lk : nullptr;
   // split mode: rows the stats kernel already drew (short lists) are done
   if (MODE == kSelectOnly && ws.rows[row].done) return kJobLeave;
   constexpr int N = Vec<DT>::N;
@@ -1566,6 +2038,8 @@ __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& 
   // exp-sum anchor: nbz starts above every quad, so the first finite quad
   // anchors, and the shift of that first anchor clears what came before
   float zt = 0.0f, nbz = __FLT_MAX__;
+  // (LP, own pass) the raw logits' statistics, before any exclusion
+  RawAcc ra{kNegInf, 0.0f, __FLT_MAX__, 0u};
   for_quads_static(S, nq, [&](int g, uint4& v) -> bool {
     const int32_t i0 = base32 + (tid + g * kThreads) * N;
     const uint32_t pcur = pw;
@@ -1574,6 +2048,7 @@ __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& 
     nf_acc |= probe;
     const int32_t rem = lim - g * (kThreads * N);
     const uint32_t tail = ~0u << (uint32_t)(rem < 0 ? 0 : (rem > N ? N : rem));
+    if constexpr (LP && JM == kFused) raw_add<DT>(ra, v, tail & FULL, probe);
     uint32_t ex = ((pcur >> pen_shift) | tail) & FULL;
     if (mrow) ex |= ~staged_allow_bits(mw, i0 - base32, N) & FULL;
     // (NaNs are rare, behind a branch; entry tokens are in most quads of a
@@ -1613,6 +2088,8 @@ __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& 
   const bool ent_overflow = n_all > kSliceEntryCap;
   const int n_ent = n_all < kSliceEntryCap ? n_all : kSliceEntryCap;
   const bool nonfinite = nonfinite_seen<DT>(nf_acc);
+  // (LP, own pass) the slice's raw record, out before any exchange
+  if constexpr (LP && JM == kFused) raw_slice<DT>(P, Lk, row, slice, rowp, base32, end32, nq, ra, L);
 
   RowInfo info;
   if (jm != kSelectOnly) {
@@ -1889,7 +2366,7 @@ __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& 
         __syncthreads();
         if (L.last) {
           if (short_gather<DT>(ws, P, row, c, prm, L)) {
-            short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K);
+            short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K, lpp);
             return kJobLeave;
           }
           // the row falls back: this slice's histogram, then those of the
@@ -2048,7 +2525,7 @@ __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& 
       uint32_t* const arrive = row_sync(ws, row) + kSyncArrive;
       if (!arrive_last(arrive, (uint32_t)G, &L.last)) return kJobLeave;
       if (K > 0 && short_gather<DT>(ws, P, row, c, prm, L)) {
-        short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K);
+        short_finish<DT>(ws, P, row, c, prm, L, rowp, mrow, K, lpp);
         if (tid == 0) *arrive = 0u;
         return kJobLeave;
       }
@@ -2278,7 +2755,7 @@ __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& 
     st_coherent(&sp->overflow, ent_overflow ? 1 : 0);
   }
   if (arrive_last(&ws.arrive_select[row], (uint32_t)G, &L.last))
-    finalize_row<DT>(ws, P, row, c, prm, info, L, rowp, mrow);
+    finalize_row<DT>(ws, P, row, c, prm, info, L, rowp, mrow, lpp);
   if (MODE != kFused) return kJobLeave;
   // the exchange's last arriver does the selects of the slices that left
   if (L.xlast) {
@@ -2293,11 +2770,11 @@ __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& 
 // work-group's own slice (with its start ticket), then whatever it claimed
 // for slices that left, and the departure; returns (thread 0) the row's
 // departure count before this one, for clear_if_last.
-template <int DT, int MODE>
+template <int DT, int MODE, bool LP = false>
 __device__ __forceinline__ uint32_t run_task(const Workspace& ws, const SamplePlan& P, int row,
-                                             int slice, TaskLds& L) {
+                                             int slice, TaskLds& L, const FusedLp& Lk) {
   if constexpr (MODE != kFused) {
-    (void)slice_job<DT, MODE, MODE>(ws, P, row, slice, L, slice);
+    (void)slice_job<DT, MODE, MODE, false>(ws, P, row, slice, L, slice, Lk);
     return 0u;
   } else {
     if (threadIdx.x == 0) {
@@ -2308,7 +2785,7 @@ __device__ __forceinline__ uint32_t run_task(const Workspace& ws, const SamplePl
     }
     // (no barrier: the job's first barriers come after its loads are issued,
     // before anything reads these)
-    int next = slice_job<DT, kFused, kFused>(ws, P, row, slice, L, slice);
+    int next = slice_job<DT, kFused, kFused, LP>(ws, P, row, slice, L, slice, Lk);
     // (after the own pass: at most G - 1 claimed histograms and G claimed
     // selects; every thread returns the same job, read from LDS)
     for (int n = 0; n < 2 * kMaxSlices && next >= 0; ++n) {
@@ -2316,8 +2793,8 @@ __device__ __forceinline__ uint32_t run_task(const Workspace& ws, const SamplePl
       const int s = next & 0xff;
       __syncthreads();
       next = (next >> 8) == kBehalfStats
-                 ? slice_job<DT, kFused, kBehalfStats>(ws, P, row, s, L, slice)
-                 : slice_job<DT, kFused, kSelectOnly>(ws, P, row, s, L, slice);
+                 ? slice_job<DT, kFused, kBehalfStats, LP>(ws, P, row, s, L, slice, Lk)
+                 : slice_job<DT, kFused, kSelectOnly, LP>(ws, P, row, s, L, slice, Lk);
     }
     // (thread 0 has consumed its start ticket's result at the exchange)
     return threadIdx.x == 0 ? leave_row(ws, row) : 0u;
@@ -2327,8 +2804,10 @@ __device__ __forceinline__ uint32_t run_task(const Workspace& ws, const SamplePl
 // ================================================================ kernels
 // ONE: every row fits one round of the grid (no loop over rounds, so nothing
 // is hoisted out of one and spilled before the first load).
-template <int DT, bool ONE>
-__global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk) {
+// LP: raw log-probabilities in the same pass (lsamp_step); `Lk` is read
+// where it is used (the raw record and the finalize), not held throughout.
+template <int DT, bool ONE, bool LP>
+__global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk, FusedLp Lk) {
   __shared__ TaskLds L;
   // The kernel arguments are read in one round of scalar loads and held as
   // opaque values (otherwise they are fetched lazily, over several dependent
@@ -2340,7 +2819,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
   const int slice = (int)blockIdx.x % G;
   if (ONE) {
     if (rowslot < P.rows) {
-      const uint32_t out = run_task<DT, kFused>(ws, P, rowslot, slice, L);
+      const uint32_t out = run_task<DT, kFused, LP>(ws, P, rowslot, slice, L, Lk);
       if (threadIdx.x == 0) clear_if_last(ws, rowslot, G, out);
     }
     return;
@@ -2410,7 +2889,7 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
     // the task holds a loop of its own)
     const int row = __builtin_amdgcn_readfirstlane(ordered ? (int)order[q] : q);
     const int slice_t = __builtin_amdgcn_readfirstlane((int)(t % (uint32_t)G));
-    pend_out = run_task<DT, kFused>(wsr, Pr, row, slice_t, L);
+    pend_out = run_task<DT, kFused, LP>(wsr, Pr, row, slice_t, L, Lk);
     pend_row = row;
     __syncthreads();
   }
@@ -2423,34 +2902,43 @@ __global__ __launch_bounds__(kThreads) void k_fused(Workspace wsk, SamplePlan Pk
 template <int DT>
 __global__ __launch_bounds__(kThreads) void k_stats(Workspace ws, SamplePlan P) {
   __shared__ TaskLds L;
-  run_task<DT, kStatsOnly>(ws, P, (int)blockIdx.y, (int)blockIdx.x, L);
+  const FusedLp none{-1, nullptr, nullptr, nullptr, nullptr};
+  run_task<DT, kStatsOnly>(ws, P, (int)blockIdx.y, (int)blockIdx.x, L, none);
 }
 
 template <int DT>
 __global__ __launch_bounds__(kThreads) void k_select(Workspace ws, SamplePlan P) {
   __shared__ TaskLds L;
-  run_task<DT, kSelectOnly>(ws, P, (int)blockIdx.y, (int)blockIdx.x, L);
+  const FusedLp none{-1, nullptr, nullptr, nullptr, nullptr};
+  run_task<DT, kSelectOnly>(ws, P, (int)blockIdx.y, (int)blockIdx.x, L, none);
 }
 
 template <int DT>
-int launch_dt(const Workspace& ws, const SamplePlan& P, hipStream_t st, void* const* events) {
+int launch_dt(const Workspace& ws, const SamplePlan& P, const FusedLp* lp, hipStream_t st,
+              void* const* events) {
   auto mark = [&](int i) {
     if (events) (void)hipEventRecord(reinterpret_cast<hipEvent_t>(events[i]), st);
   };
   mark(0);
   if (P.fused) {
     const int rounds_rows = P.rows < P.rows_per_round ? P.rows : P.rows_per_round;
+    const dim3 grid((unsigned)(rounds_rows * P.slices));
+    const FusedLp none{-1, nullptr, nullptr, nullptr, nullptr};
+    const FusedLp& lk = lp ? *lp : none;
     // (fp32 steps run fused only when every row fits one round: the
     // several-rounds instantiation with the fp32 slab does not fit the
     // registers, so it is not built, and the planner gives such steps the
     // split kernels)
     if constexpr (DT == LSAMP_DTYPE_F32) {
-      hipLaunchKernelGGL((k_fused<DT, true>), dim3((unsigned)(rounds_rows * P.slices)),
-                         dim3(kThreads), 0, st, ws, P);
+      if (lp)
+        hipLaunchKernelGGL((k_fused<DT, true, true>), grid, dim3(kThreads), 0, st, ws, P, lk);
+      else
+        hipLaunchKernelGGL((k_fused<DT, true, false>), grid, dim3(kThreads), 0, st, ws, P, lk);
     } else {
-      auto kf = P.rows <= P.rows_per_round ? k_fused<DT, true> : k_fused<DT, false>;
-      hipLaunchKernelGGL(kf, dim3((unsigned)(rounds_rows * P.slices)), dim3(kThreads), 0, st,
-                         ws, P);
+      const bool one = P.rows <= P.rows_per_round;
+      auto kf = lp ? (one ? k_fused<DT, true, true> : k_fused<DT, false, true>)
+                   : (one ? k_fused<DT, true, false> : k_fused<DT, false, false>);
+      hipLaunchKernelGGL(kf, grid, dim3(kThreads), 0, st, ws, P, lk);
     }
     mark(1);
   } else {
@@ -2895,12 +3383,13 @@ int launch_verify_finish(const Workspace& ws, const VerifyPlan& Q, void* stream)
   }
 }
 
-int launch_sample(const Workspace& ws, const SamplePlan& P, void* stream, void* const* events) {
+int launch_sample(const Workspace& ws, const SamplePlan& P, const FusedLp* lp, void* stream,
+                  void* const* events) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   switch (P.dtype) {
-    case LSAMP_DTYPE_F32: return launch_dt<LSAMP_DTYPE_F32>(ws, P, st, events);
-    case LSAMP_DTYPE_BF16: return launch_dt<LSAMP_DTYPE_BF16>(ws, P, st, events);
-    default: return launch_dt<LSAMP_DTYPE_F16>(ws, P, st, events);
+    case LSAMP_DTYPE_F32: return launch_dt<LSAMP_DTYPE_F32>(ws, P, lp, st, events);
+    case LSAMP_DTYPE_BF16: return launch_dt<LSAMP_DTYPE_BF16>(ws, P, lp, st, events);
+    default: return launch_dt<LSAMP_DTYPE_F16>(ws, P, lp, st, events);
   }
 }
 
@@ -2915,12 +3404,12 @@ int set_spin_test(int32_t polls) {
 template <int DT>
 int fused_blocks_dt() {
   int a = 0, b = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_fused<DT, true>, kThreads, 0) != hipSuccess)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&a, k_fused<DT, true, false>, kThreads, 0) != hipSuccess)
     return 0;
   if constexpr (DT == LSAMP_DTYPE_F32) {
     return a;  // (one round only)
   } else {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_fused<DT, false>, kThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_fused<DT, false, false>, kThreads, 0) !=
         hipSuccess)
       return 0;
     return a < b ? a : b;

@@ -19,7 +19,7 @@ import oracle as O
 from lsamp import _ffi
 from lsamp import workloads as W
 from lsamp.history import Cbv2RowState, csr
-from rank_common import BF16, F16, close_logprobs, to_bits
+from rank_common import BF16, F16, F32, close_logprobs, to_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -190,3 +190,72 @@ def test_step_logprobs_in_the_sampling_pass(ctx, dtype, vocab, k):
 def states_v(prompts, vocab):
     return [Cbv2RowState(pr, [], 8, repetition_on=True, counts_on=True, vocab=vocab)
             for pr in prompts]
+
+
+def _fused_params(rows, vocab):
+    """Rows the one-pass top-k kernel does not take (so the step runs the
+    fused sampling kernel): wide nuclei (no top-k, the histogram path), top-k
+    100 (its short list), and a greedy row."""
+    kinds = [dict(temperature=0.9, top_p=0.9), dict(temperature=0.7, top_k=100, top_p=0.95),
+             dict(temperature=1.1, top_p=0.8, min_p=0.02), dict(temperature=0.0)]
+    return W._params([W.resolve_cbv2(repetition_penalty=1.2, repetition_context_size=8,
+                                     presence_penalty=0.5, frequency_penalty=0.3, vocab=vocab,
+                                     **kinds[r % len(kinds)]) for r in range(rows)])
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("vocab,k,rows", [(151936, 0, 12), (151936, 20, 12), (151936, 32, 12),
+                                          (40003, 1, 12), (40003, 20, 12), (151936, 20, 80)])
+def test_step_logprobs_in_the_fused_pass(dtype, vocab, k, rows):
+    """The fused sampling kernel's raw log-probabilities (launch kind 4: no
+    second pass over the logits) against the oracle's raw ranking
+    (LogitsPipelineV2.process :307-314, CBv2Logprobs.gather :534-549): the
+    raw logits before penalties, the grammar mask and the temperature; NaN,
+    +inf, all -inf, tied, signed-zero rows; rows that are not 16-byte aligned
+    (odd vocabularies); 80 rows take the fused grid in several rounds (16-bit
+    logits; fp32 steps that do not fit one round run split, with the second
+    pass)."""
+    import torch
+    from lsamp.api import Context, PenaltyTable
+    ctx = Context(0, max_rows=rows, max_vocab=vocab)
+    try:
+        rng = np.random.default_rng(vocab + 7 * k + dtype + rows)
+        x = rng.normal(0.0, 3.0, (rows, vocab)).astype(np.float32)
+        special_rows(x, rng)
+        if dtype == F32:
+            bits = x
+            lt = torch.from_numpy(x).cuda()
+        else:
+            bits = to_bits(x, dtype)
+            lt = torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(
+                torch.bfloat16).cuda()
+        params = _fused_params(rows, vocab)
+        prompts = [rng.integers(0, vocab, 30).tolist() for _ in range(rows)]
+        table = PenaltyTable(states_v(prompts, vocab), capacity=256, window_capacity=8)
+        words = (vocab + 31) // 32
+        mask = np.full((rows, words), 0xFFFFFFFF, np.uint32)
+        mask[::2] = rng.integers(0, 1 << 32, (rows // 2 + rows % 2, words),
+                                 dtype=np.uint64).astype(np.uint32)
+        u = rng.random(rows, dtype=np.float32)
+        out = ctx.step(lt, params, table=table, uniforms=u, logprobs_top_k=k, bitmask=mask,
+                       mask_bits=vocab)
+        torch.cuda.synchronize()
+        launch = ctx.last_launch()
+        if dtype == F32 and rows == 80:
+            assert launch["fused"] == 0, launch  # split, with lsamp_logprobs after it
+        else:
+            assert launch["fused"] == 4, launch
+            assert rows != 80 or launch["rows_per_round"] < rows, launch
+        tok = out["tokens"].cpu().numpy()
+        ref = O.rank(np.ascontiguousarray(bits).reshape(-1), dtype=dtype, k=k, raw_values=False,
+                     rows=rows, vocab=vocab, row_stride=vocab, col_stride=1, tokens=tok)
+        if k:
+            ids = out["top_ids"].cpu().numpy()
+            bad = np.nonzero((ids != ref["ids"]).any(axis=1))[0]
+            assert bad.size == 0, f"ids differ in rows {bad}: {ids[bad[:2]]} vs {ref['ids'][bad[:2]]}"
+            assert close_logprobs(out["top_values"].cpu().numpy(), ref["values"])
+            # NaN, +inf and all-NaN rows have no finite log-sum-exp: they fail closed
+            assert (ids[[1, 2, 6]] == -1).all() and (ids[[0, 3, 4, 5, 7, 8]] >= 0).all()
+        assert close_logprobs(out["chosen"].cpu().numpy(), ref["chosen"])
+    finally:
+        ctx.close()
