@@ -1228,8 +1228,14 @@ __device__ __forceinline__ bool short_gather(const Workspace& ws, const SamplePl
     info.mass_above = 0.0;
     info.z = z;
     info.p_limit = top_p_limit(P, c, prm, z);
-    info.kept_cands = 0;
-    info.done = 1;
+    {
+      // (made here: the constant pair (0, 1) hoisted out of the fused
+      // kernel's task loop was held across it and spilled)
+      int zero = 0, one = 1;
+      asm volatile("" : "+v"(zero), "+v"(one));
+      info.kept_cands = zero;
+      info.done = one;
+    }
     if (l == 0) {
       L.info = info;
       L.misc[5] = fallback ? 1 : 0;
@@ -1446,21 +1452,6 @@ constexpr int kRawList = kThreads;       // candidates ranked by counting
 constexpr int kRawOut = kRawList;        // the sorted best k follow them
 static_assert(kRawOut + kTopkMaxLp <= kCandCap, "the raw lists fit the finalize keys");
 
-// Position of the n-th (from 0) set bit of m (n < popcount(m)).
-__device__ __forceinline__ int nth_set_bit(uint64_t m, int n) {
-  int pos = 0;
-#pragma unroll
-  for (int w = 32; w >= 1; w >>= 1) {
-    const int c = (int)__popcll(m & ((1ull << w) - 1ull));
-    if (n >= c) {
-      n -= c;
-      m >>= w;
-      pos += w;
-    }
-  }
-  return pos;
-}
-
 static_assert(sizeof(ShortLds::squad) >= kMaxSlices * kTopkMaxLp * sizeof(uint64_t),
               "the raw lists fit the staging area");
 
@@ -1652,37 +1643,57 @@ __device__ __forceinline__ void raw_slice(const SamplePlan& P, const FusedLp& lp
     int n = kRawList + 1;
     if (tau > kNegInf) {
       // 3. candidates: the logits of the threads whose maximum reaches tau,
-      // read again by their whole wave at once: the wave's (thread, quad)
-      // pairs are dealt to its lanes, kRePer 16-byte loads a lane in flight
-      // together (through one buffer descriptor over the slice, as pass 1
-      // loads them), so up to 64 * kRePer pairs take one round trip.  The
-      // last partial quad and unaligned rows are read element by element.
+      // read again by the whole work-group at once: the reading threads'
+      // (thread, quad) pairs are dealt to every thread, kRePer 16-byte loads
+      // a thread in flight together (through one buffer descriptor over the
+      // slice, as pass 1 loads them), so up to kThreads * kRePer pairs take
+      // one round trip.  The last partial quad and unaligned rows are read
+      // element by element.
       constexpr int ES = Vec<DT>::ESIZE;
       constexpr int kRePer = N == 4 ? 4 : 2;  // (fp32 slices: more quads a thread)
       const bool aligned = P.aligned != 0;
-      const uint64_t mm = __ballot(a.m >= tau);
-      const int pairs = (int)__popcll(mm) * nq;  // (wave-uniform)
+      const bool reads = a.m >= tau;
+      const uint64_t mm = __ballot(reads);
+      if (l == 0) L.redu[wv] = mm;
+      __syncthreads();
+      int before = 0, M = 0;  // reading threads in lower waves, in all
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const int cw = (int)__popcll(L.redu[w]);
+        before += w < wv ? cw : 0;
+        M += cw;
+      }
+      // the reading threads in order (in the sorted keys' area, idle until
+      // the rank)
+      uint32_t* const who = reinterpret_cast<uint32_t*>(cand + kRawOut);
+      static_assert(kRawOut + kThreads / 2 <= kCandCap, "a reader id per thread fits");
+      if (reads) who[before + (int)__popcll(mm & ((1ull << l) - 1ull))] = (uint32_t)tid;
+      __syncthreads();
+      const int pairs = M * nq;  // (uniform)
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<char*>(rowp) + (size_t)base32 * ES, 0, aligned ? (end32 - base32) * ES : 0,
           kBufferWord3);
 #pragma unroll 1
-      for (int p0 = 0; p0 < pairs; p0 += 64 * kRePer) {
+      for (int p0 = 0; p0 < pairs; p0 += kThreads * kRePer) {
+        // pair pr: quad pr % nq of the (pr / nq)-th reading thread, at
+        // quad place qd of the slice (recomputed after the loads, so only
+        // the loaded words stay live across them)
+        auto place = [&](int pr) -> int {
+          const int q = pr / nq;
+          return (int)who[q] + (pr - q * nq) * kThreads;
+        };
         uint4 w[kRePer];
-        int32_t i0s[kRePer];
 #pragma unroll
         for (int j = 0; j < kRePer; ++j) {
-          const int pr = p0 + j * 64 + l;
-          const bool in = pr < pairs;
-          // pair pr: quad pr % nq of the wave's (pr / nq)-th reading thread
-          const int t = wv * 64 + nth_set_bit(mm, in ? pr / nq : 0);
-          const int qd = t + (in ? pr % nq : 0) * kThreads;  // the quad's place in the slice
-          i0s[j] = in ? base32 + qd * N : end32;             // (past the end: nothing listed)
-          const auto r = __builtin_amdgcn_raw_buffer_load_b128(rs, in ? qd * 16 : 0x40000000, 0, 0);
+          const int pr = p0 + j * kThreads + tid;
+          const auto r = __builtin_amdgcn_raw_buffer_load_b128(
+              rs, pr < pairs ? place(pr) * 16 : 0x40000000, 0, 0);
           w[j] = make_uint4(r[0], r[1], r[2], r[3]);
         }
 #pragma unroll
         for (int j = 0; j < kRePer; ++j) {
-          const int32_t i0 = i0s[j];
+          const int pr = p0 + j * kThreads + tid;
+          const int32_t i0 = pr < pairs ? base32 + place(pr) * N : end32;  // (past the end: nothing listed)
           if (i0 < end32 && (!aligned || i0 + N > end32)) {
             uint32_t b[N];
 #pragma unroll
