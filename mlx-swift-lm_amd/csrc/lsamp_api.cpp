@@ -227,7 +227,16 @@ lsamp_status lsamp::sample_step(const WorkspaceViews& v, const DeviceShape& d, i
   P.vocab = a->vocab;
   P.dtype = a->dtype;
   P.row_stride = a->row_stride;
-  const bool topk = mode == LSAMP_MODE_AUTO && d.topk_bpc[a->dtype] > 0 && topk_eligible(a);
+  bool topk = mode == LSAMP_MODE_AUTO && d.topk_bpc[a->dtype] > 0 && topk_eligible(a);
+  if (topk && lp && lp->k >= 0 && a->dtype == LSAMP_DTYPE_F32 && d.fused_bpc[a->dtype] > 0) {
+    // raw log-probabilities of fp32 logits: the top-k kernel has no variant
+    // that ranks them and the fused sampling kernel does, in one round, so
+    // a batch that fits one round takes it (no second pass)
+    const int32_t fslots = d.cus * d.fused_bpc[a->dtype];
+    int32_t fs = 0, fl = 0, fc = 0;
+    plan_slices(a->rows, a->vocab, fslots, &fs, &fl, &fc);
+    if ((int64_t)a->rows * fs <= fslots) topk = false;
+  }
   const int32_t bpc = topk ? d.topk_bpc[a->dtype] : d.fused_bpc[a->dtype];
   const int32_t slots = d.cus * (bpc > 0 ? bpc : 1);
   // (the top-k kernel: one work-group per CU is enough, and fewer slices per

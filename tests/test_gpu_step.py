@@ -259,3 +259,43 @@ def test_step_logprobs_in_the_fused_pass(dtype, vocab, k, rows):
         assert close_logprobs(out["chosen"].cpu().numpy(), ref["chosen"])
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("k", [0, 20])
+def test_fp32_topk_batch_logprobs_take_the_fused_pass(k):
+    """fp32 rows the one-pass top-k kernel would take (top-k 50, greedy): with
+    raw log-probabilities the step runs the fused sampling kernel instead
+    (launch kind 4), which ranks them in its own pass: its token equals the
+    top-k kernel's draw and its log-probabilities match the oracle
+    (LogitsPipelineV2.process :307-314, CBv2Logprobs.gather :534-549)."""
+    import torch
+    from lsamp.api import Context, PenaltyTable
+    rows, vocab = 12, 151936
+    ctx = Context(0, max_rows=rows, max_vocab=vocab)
+    try:
+        rng = np.random.default_rng(4242 + k)
+        x = rng.normal(0.0, 3.0, (rows, vocab)).astype(np.float32)
+        lt = torch.from_numpy(x).cuda()
+        kinds = [dict(temperature=0.8, top_k=50, top_p=0.95), dict(temperature=0.0)]
+        params = W._params([W.resolve_cbv2(repetition_penalty=1.1, repetition_context_size=8,
+                                           vocab=vocab, **kinds[r % 2]) for r in range(rows)])
+        prompts = [rng.integers(0, vocab, 30).tolist() for _ in range(rows)]
+        table = PenaltyTable(states_v(prompts, vocab), capacity=256, window_capacity=8)
+        rp, en = csr([h.entries() for h in states_v(prompts, vocab)])
+        u = rng.random(rows, dtype=np.float32)
+        plain = ctx.sample(lt, params, semantics=_ffi.SEM_CBV2, row_ptr=rp, entries=en, uniforms=u)
+        torch.cuda.synchronize()
+        assert ctx.last_launch()["fused"] == 2  # (the top-k kernel, no log-probabilities)
+        out = ctx.step(lt, params, table=table, uniforms=u, logprobs_top_k=k)
+        torch.cuda.synchronize()
+        assert ctx.last_launch()["fused"] == 4, ctx.last_launch()
+        tok = out["tokens"].cpu().numpy()
+        assert np.array_equal(tok, plain["tokens"].cpu().numpy())
+        ref = O.rank(x.reshape(-1), dtype=F32, k=k, raw_values=False, rows=rows, vocab=vocab,
+                     row_stride=vocab, col_stride=1, tokens=tok)
+        if k:
+            assert np.array_equal(out["top_ids"].cpu().numpy(), ref["ids"])
+            assert close_logprobs(out["top_values"].cpu().numpy(), ref["values"])
+        assert close_logprobs(out["chosen"].cpu().numpy(), ref["chosen"])
+    finally:
+        ctx.close()
