@@ -299,3 +299,42 @@ def test_fp32_topk_batch_logprobs_take_the_fused_pass(k):
         assert close_logprobs(out["chosen"].cpu().numpy(), ref["chosen"])
     finally:
         ctx.close()
+
+
+def test_fused_logprob_step_replays_from_a_graph():
+    """lsamp_step on a batch the fused kernel takes, with log-probabilities
+    (launch kind 4), captured in a HIP graph: every replay, with eager steps
+    between them, gives the eager step's tokens, ids and values."""
+    import torch
+    from lsamp.api import Context, PenaltyTable
+    rows, vocab = 16, 151936
+    ctx = Context(0, max_rows=rows, max_vocab=vocab)
+    try:
+        rng = np.random.default_rng(77)
+        x = rng.normal(0.0, 3.0, (rows, vocab)).astype(np.float32)
+        lt = torch.from_numpy(to_bits(x, BF16).view(np.int16)).view(torch.bfloat16).cuda()
+        params = _fused_params(rows, vocab)
+        prompts = [rng.integers(0, vocab, 30).tolist() for _ in range(rows)]
+        u = torch.from_numpy(rng.random(rows, dtype=np.float32)).cuda()
+        eager_t = PenaltyTable(states_v(prompts, vocab), capacity=256, window_capacity=8)
+        graph_t = PenaltyTable(states_v(prompts, vocab), capacity=256, window_capacity=8)
+        eager = ctx.prepare_step(lt, params, table=eager_t, uniforms=u, logprobs_top_k=5)
+        graphed = ctx.prepare_step(lt, params, table=graph_t, uniforms=u, logprobs_top_k=5)
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            graphed.launch(s.cuda_stream)
+        torch.cuda.synchronize()
+        assert ctx.last_launch()["fused"] == 4, ctx.last_launch()
+        for i in range(4):
+            eager.launch(s.cuda_stream)
+            torch.cuda.synchronize()
+            with torch.cuda.stream(s):
+                g.replay()
+            torch.cuda.synchronize()
+            a, b = eager.outputs(), graphed.outputs()
+            for key in ("tokens", "top_ids", "top_values", "chosen"):
+                assert np.array_equal(a[key].cpu().numpy(), b[key].cpu().numpy(),
+                                      equal_nan=key in ("top_values", "chosen")), (i, key)
+    finally:
+        ctx.close()
