@@ -240,6 +240,7 @@ struct TaskLds {
   int32_t htop[kMaxSlices];
   uint32_t hfl[kMaxSlices];
   int32_t hn[kMaxSlices];
+  double hz[kMaxSlices];
   float redf[kWaves];
   float redf2[kWaves];
   int32_t redi[kWaves];
@@ -283,6 +284,73 @@ static_assert(kSelQueue >= kThreads / kWaves * 8, "a quad step of a wave fits th
 // of 64 and the scan stops at the block holding the cut.  Deeper cuts read
 // further bins, already aligned, 256 at a time.  Slices publish their own
 // total mass, so the scan never needs the bins below the cut.
+// The merge's first round trip, spread over the work-group: every wave reads
+// the slices' top bins and counts, wave 0 the rest of the heads (kept in LDS
+// for merge_wave), and wave s < G the top bins of slice s, which it adds,
+// aligned to the row's top bin, into the merge arrays: 512 bins a slice when
+// the row has more than 4 slices (a batch below them would cost two round
+// trips), else 256 (one).  A cut in those bins needs no further round trip.
+// Whole work-group.
+constexpr int kMergeStageBins = 512;
+__device__ __forceinline__ int merge_stage_batches(int slices) { return slices > 4 ? 2 : 1; }
+__device__ __forceinline__ void merge_stage(const Workspace& ws, const SamplePlan& P, int row,
+                                            const RowCtx& c, TaskLds& L) {
+  constexpr int kPer = kMergeStageBins / 64;
+  static_assert(kMergeStageBins <= kBins, "the staged bins fit the merge arrays");
+  static_assert(kWaves >= kMaxSlices, "a wave per slice");
+  const int tid = fresh_tid(), l = tid & 63, wv = tid >> 6;
+  const int G = P.slices;
+  const SliceSummary* summ = ws.summaries + (size_t)row * kMaxSlices;
+  const bool hist_row = c.kind != LSAMP_KIND_ARGMAX;
+  int32_t ht = 0, hn = 0;
+  if (l < G) {
+    ht = ld_coherent(&summ[l].top_bin);
+    hn = ld_coherent(&summ[l].n_finite);
+  }
+  float hx = kNegInf;
+  uint32_t hfl = 0u;
+  double hz = 0.0;
+  if (wv == 0 && l < G) {
+    hx = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&summ[l].x_max)));
+    hfl = ld_coherent(&summ[l].flags);
+    hz = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&summ[l].z)));
+  }
+  const int per = 4 * merge_stage_batches(G);  // blocks of 64 bins staged
+  uint64_t w[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    w[k] = (hist_row && wv < G && k < per) ? ld_coherent(&summ[wv].hist[64 * k + l]) : 0ull;
+  for (int i = tid; i < 64 * per; i += kThreads) {
+    L.u.m.cnt[i] = 0u;
+    L.u.m.mass[i] = 0ull;
+  }
+  __syncthreads();
+  // the row's top bin over the slices with a finite token (as merge_wave)
+  const int32_t rt = wave_max(l < G && hn > 0 ? ht : INT32_MIN);
+  const int32_t hn_w = __shfl(hn, wv < G ? wv : 0, 64);
+  if (wv < G && hn_w > 0) {
+    const int32_t off = rt - __shfl(ht, wv, 64);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int j = 64 * k + l + off;
+      if (w[k] != 0ull && j < 64 * per) {
+        atomicAdd(&L.u.m.cnt[j], (uint32_t)(w[k] >> kCountShift));
+        atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.m.mass[j]),
+                  (unsigned long long)(w[k] & kMassMask));
+      }
+    }
+  }
+  if (wv == 0 && l < G) {
+    L.hx[l] = hx;
+    L.htop[l] = ht;
+    L.hfl[l] = hfl;
+    L.hn[l] = hn;
+    L.hz[l] = hz;
+  }
+  __syncthreads();
+}
+
+template <bool STAGED>
 __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan& P, int row,
                                            const RowCtx& c, const lsamp_row_params& prm, TaskLds& L) {
   const int l = fresh_tid();  // lane, wave 0
@@ -291,23 +359,36 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
   const SliceSummary* summ = ws.summaries + (size_t)row * kMaxSlices;
   const bool hist_row = c.kind != LSAMP_KIND_ARGMAX;
   constexpr int kBlk = 4;  // blocks of 64 bins per batch
+  // (STAGED: merge_stage has the heads in LDS and the top staged_batches
+  // batches of bins aligned there)
+  const int staged_batches = STAGED ? merge_stage_batches(G) : 1;
   float hx = kNegInf;
   int32_t htop = 0, hn = 0;
   uint32_t hfl = 0u;
   double hz = 0.0;
   if (l < G) {
-    hx = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&summ[l].x_max)));
-    htop = ld_coherent(&summ[l].top_bin);
-    hfl = ld_coherent(&summ[l].flags);
-    hn = ld_coherent(&summ[l].n_finite);
-    hz = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&summ[l].z)));
+    if constexpr (STAGED) {
+      hx = L.hx[l];
+      htop = L.htop[l];
+      hfl = L.hfl[l];
+      hn = L.hn[l];
+      hz = L.hz[l];
+    } else {
+      hx = __uint_as_float(ld_coherent(reinterpret_cast<const uint32_t*>(&summ[l].x_max)));
+      htop = ld_coherent(&summ[l].top_bin);
+      hfl = ld_coherent(&summ[l].flags);
+      hn = ld_coherent(&summ[l].n_finite);
+      hz = __builtin_bit_cast(double, ld_coherent(reinterpret_cast<const uint64_t*>(&summ[l].z)));
+    }
   }
-  uint64_t w[kMaxSlices][kBlk];
+  uint64_t w[STAGED ? 1 : kMaxSlices][kBlk];
+  if constexpr (!STAGED) {
 #pragma unroll
-  for (int s = 0; s < kMaxSlices; ++s)
+    for (int s = 0; s < kMaxSlices; ++s)
 #pragma unroll
-    for (int k = 0; k < kBlk; ++k)
-      w[s][k] = (hist_row && s < G) ? ld_coherent(&summ[s].hist[64 * k + l]) : 0ull;
+      for (int k = 0; k < kBlk; ++k)
+        w[s][k] = (hist_row && s < G) ? ld_coherent(&summ[s].hist[64 * k + l]) : 0ull;
+  }
 
   float row_max = kNegInf;
   int32_t row_top = 0, n_total = 0;
@@ -374,23 +455,25 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
     }
     info.p_limit = P_lim;
 
-    // batch 0: align the top 256 bins of every slice in LDS
-#pragma unroll
-    for (int k = 0; k < kBlk; ++k) {
-      L.u.m.cnt[64 * k + l] = 0u;
-      L.u.m.mass[64 * k + l] = 0ull;
-    }
-#pragma unroll
-    for (int s = 0; s < kMaxSlices; ++s) {
-      if (s >= G) break;
-      const int32_t off = row_top - __shfl(htop, s, 64);
+    if constexpr (!STAGED) {
+      // batch 0: align the top 256 bins of every slice in LDS
 #pragma unroll
       for (int k = 0; k < kBlk; ++k) {
-        const int j = 64 * k + l + off;
-        if (w[s][k] != 0ull && j < 64 * kBlk) {
-          atomicAdd(&L.u.m.cnt[j], (uint32_t)(w[s][k] >> kCountShift));
-          atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.m.mass[j]),
-                    (unsigned long long)(w[s][k] & kMassMask));
+        L.u.m.cnt[64 * k + l] = 0u;
+        L.u.m.mass[64 * k + l] = 0ull;
+      }
+#pragma unroll
+      for (int s = 0; s < kMaxSlices; ++s) {
+        if (s >= G) break;
+        const int32_t off = row_top - __shfl(htop, s, 64);
+#pragma unroll
+        for (int k = 0; k < kBlk; ++k) {
+          const int j = 64 * k + l + off;
+          if (w[s][k] != 0ull && j < 64 * kBlk) {
+            atomicAdd(&L.u.m.cnt[j], (uint32_t)(w[s][k] >> kCountShift));
+            atomicAdd(reinterpret_cast<unsigned long long*>(&L.u.m.mass[j]),
+                      (unsigned long long)(w[s][k] & kMassMask));
+          }
         }
       }
     }
@@ -402,11 +485,11 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
     for (int b = 0; b < kBins / (64 * kBlk) && cut < 0; ++b) {
       uint32_t cnt[kBlk];
       uint64_t msum[kBlk];
-      if (b == 0) {
+      if (b < staged_batches) {
 #pragma unroll
         for (int k = 0; k < kBlk; ++k) {
-          cnt[k] = L.u.m.cnt[64 * k + l];
-          msum[k] = L.u.m.mass[64 * k + l];
+          cnt[k] = L.u.m.cnt[64 * kBlk * b + 64 * k + l];
+          msum[k] = L.u.m.mass[64 * kBlk * b + 64 * k + l];
         }
       } else {
         // deeper batch: read the slices' bins already aligned, four slices'
@@ -496,7 +579,7 @@ __device__ __forceinline__ void merge_wave(const Workspace& ws, const SamplePlan
 
 __device__ __forceinline__ void merge_row(const Workspace& ws, const SamplePlan& P, int row, const RowCtx& c,
                           const lsamp_row_params& prm, TaskLds& L) {
-  if (threadIdx.x < 64) merge_wave(ws, P, row, c, prm, L);
+  if (threadIdx.x < 64) merge_wave<false>(ws, P, row, c, prm, L);
   __syncthreads();
 }
 
@@ -2533,7 +2616,8 @@ __device__ __forceinline__ int slice_job(const Workspace& ws, const SamplePlan& 
         __syncthreads();
       }
       if (!L.xlast && L.wait != 1) return kJobLeave;
-      if (tid < 64) merge_wave(ws, P, row, c, prm, L);
+      merge_stage(ws, P, row, c, L);
+      if (tid < 64) merge_wave<true>(ws, P, row, c, prm, L);
       if (tid == 0) L.won = (L.xlast || ((claimed >> own) & 1u) == 0u) ? 1 : 0;
       __syncthreads();
       if (!L.won) return kJobLeave;  // (the last arriver does this select)
