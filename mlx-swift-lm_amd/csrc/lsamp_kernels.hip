@@ -667,21 +667,41 @@ __device__ __forceinline__ void finalize_tail(const Workspace& ws, const SampleP
     const double e_excl = carry_e + ie - e;
     bool keep_p = true, keep_m = true;
     if (mlx) {
+      // tie group [g0, g1) of equal values (sorted by id ascending): its
+      // edges inside the block from the lanes' neighbours (two ballots);
+      // a group that crosses the block's edge is searched in LDS
+      // (the lane moves run on every lane: a lane move inside a branch
+      // would read the lanes the branch leaves out)
+      const uint32_t up = (uint32_t)__shfl_up((int)kr, 1, 64);
+      const uint32_t dn = (uint32_t)__shfl_down((int)kr, 1, 64);
+      const uint32_t kprev = l > 0 ? up : (r0 > 0 ? (uint32_t)(F.keys[r0 - 1] >> 32) : ~kr);
+      const uint32_t knext = l < 63 ? dn : (r0 + 64 < nc ? (uint32_t)(F.keys[r0 + 64] >> 32) : ~kr);
+      const uint64_t starts = __ballot(in && (r == 0 || kprev != kr));
+      const uint64_t ends = __ballot(in && (r == nc - 1 || knext != kr));
       if (in) {
-        // tie group [g0, g1) of equal values (sorted by id ascending)
-        int lo = 0, hi = r;
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if ((uint32_t)(F.keys[mid] >> 32) == kr) hi = mid; else lo = mid + 1;
+        const uint64_t below = starts & (~0ull >> (63 - l));  // starts at lanes <= l
+        const uint64_t above = ends & (~0ull << l);           // ends at lanes >= l
+        int g0, g1;
+        if (below) {
+          g0 = r0 + 63 - __builtin_clzll(below);
+        } else {
+          int lo = 0, hi = r;
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if ((uint32_t)(F.keys[mid] >> 32) == kr) hi = mid; else lo = mid + 1;
+          }
+          g0 = lo;
         }
-        const int g0 = lo;
-        lo = r;
-        hi = nc - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if ((uint32_t)(F.keys[mid] >> 32) == kr) lo = mid; else hi = mid - 1;
+        if (above) {
+          g1 = r0 + __builtin_ctzll(above) + 1;
+        } else {
+          int lo = r, hi = nc - 1;
+          while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if ((uint32_t)(F.keys[mid] >> 32) == kr) lo = mid; else hi = mid - 1;
+          }
+          g1 = lo + 1;
         }
-        const int g1 = lo + 1;
         // mass ranked strictly before r when equal values put higher ids first
         // (ascending stable argsort, Evaluate.swift:463-469)
         const double sp = info.mass_above + e_excl - (double)(r - g0) * e + (double)(g1 - 1 - r) * e;

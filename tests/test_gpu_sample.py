@@ -91,6 +91,22 @@ def test_ties_and_nonfinite(ctx):
                 compare(cfg, run_gpu(ctx, cfg), run_oracle(cfg), label=f"ties {sem} {T} {top_k}")
 
 
+def test_mlxlm_top_p_over_long_tie_groups(ctx):
+    """mlx-lm top-p on logits quantized to steps of 0.25 (tie groups of
+    hundreds of tokens, so the finalize's candidate blocks of 64 hold groups
+    that start and end inside a block and groups that cross its edges):
+    tokens and keep sets equal the oracle's (Evaluate.swift:462-471, the
+    stable ascending argsort's order among equal values)."""
+    rng = np.random.default_rng(2024)
+    rows, V = 16, 5003
+    x = (np.round(rng.normal(0.0, 1.5, (rows, V)) * 4.0) / 4.0).astype(np.float32)
+    params = [W.resolve_mlxlm(temperature=[0.7, 1.0][r % 2], top_p=[0.5, 0.8, 0.9, 0.97][r % 4])
+              for r in range(rows)]
+    for us in (rng.random(rows, dtype=np.float32), GRID[:rows]):
+        cfg = small_cfg(_ffi.SEM_MLXLM, x, params, us)
+        compare(cfg, run_gpu(ctx, cfg), run_oracle(cfg), label="mlx-lm long tie groups")
+
+
 def test_penalties_both_semantics(ctx):
     rng = np.random.default_rng(11)
     V = 1000
