@@ -525,12 +525,16 @@ lsamp_status lsamp_commit(lsamp_context* ctx, const lsamp_commit_args* args, voi
  * draw (lsamp_sample), then the penalty commit of the drawn tokens into the
  * device table (lsamp_commit, :162), and the log-probabilities of the RAW
  * logits for the drawn tokens and the top k (lsamp_logprobs, :167-176), all
- * enqueued on `stream`.  When the draw runs the one-pass top-k kernel (AUTO
- * mode, 16-bit logits, `sample.params_host` showing argmax or CBv2 top-k <=
- * LSAMP_TOPK_MAX_K rows) that kernel writes the log-probabilities in the same
- * pass over the logits (launch info `fused` = 3); otherwise they are a second
- * pass (lsamp_logprobs).  Ids are the same either way and values agree to
- * float rounding of the log-sum-exp.  Graph-capturable like its parts. */
+ * enqueued on `stream`.  The kernel that draws writes the log-probabilities
+ * in the same pass over the logits: the one-pass top-k kernel (AUTO mode,
+ * 16-bit logits, `sample.params_host` showing argmax or CBv2 top-k <=
+ * LSAMP_TOPK_MAX_K rows; launch info `fused` = 3) or the fused sampling
+ * kernel (every other step that fits its grid, fp32 included, fp32 top-k
+ * batches too; `fused` = 4).  Only a step that runs the split kernels (an
+ * fp32 batch larger than one round of the fused grid, or LSAMP_MODE_SPLIT)
+ * takes a second pass (lsamp_logprobs).  Ids are the same either way and
+ * values agree to float rounding of the log-sum-exp.  Graph-capturable like
+ * its parts. */
 typedef struct lsamp_step_args {
   lsamp_sample_args sample;          /* the draw; its penalty arguments usually
                                         point at `table` (row_ptr[r] = r * capacity,
