@@ -107,6 +107,51 @@ def test_mlxlm_top_p_over_long_tie_groups(ctx):
         compare(cfg, run_gpu(ctx, cfg), run_oracle(cfg), label="mlx-lm long tie groups")
 
 
+@pytest.mark.parametrize("dtype", [_ffi.DTYPE_F32, _ffi.DTYPE_BF16])
+def test_full_rows_with_many_minus_inf_logits(ctx, dtype):
+    """Full-vocabulary rows (the fused histogram path) whose raw logits hold
+    -inf runs and scatter, some NaN, and penalty entries on -inf tokens: the
+    histogram's token counts leave out every -inf token, so keep sets,
+    kept weights and tokens equal the oracle's."""
+    rng = np.random.default_rng(4242 + dtype)
+    V, R = 151936, 8
+    x = rng.normal(0, 2.5, (R, V)).astype(np.float32)
+    x[0, rng.random(V) < 0.3] = -np.inf
+    x[1, rng.random(V) < 0.99] = -np.inf
+    x[2, :] = -np.inf
+    x[2, [5, 77777, V - 1]] = [1.0, 2.0, 1.5]
+    x[3, rng.random(V) < 0.2] = -np.inf
+    x[3, rng.random(V) < 0.01] = np.nan
+    x[4, 30000:90000] = -np.inf  # whole slices
+    x[5, ::2] = -np.inf
+    x[6, rng.random(V) < 0.5] = -np.inf
+    x[6, :64] += 12.0  # a few strong tokens over a thinned row
+    xin = x if dtype == _ffi.DTYPE_F32 else W.f32_to_bf16_bits(x)
+    us = rng.random(R, dtype=np.float32)
+    for sem in (_ffi.SEM_MLXLM, _ffi.SEM_CBV2):
+        ents = []
+        for r in range(R):
+            hist = np.concatenate([rng.integers(0, V, 24), np.nonzero(np.isneginf(x[r]))[0][:16]])
+            if sem == _ffi.SEM_MLXLM:
+                ring_r, ring_p, ring_f = TokenRing(32), TokenRing(32), TokenRing(32)
+                for t in (ring_r, ring_p, ring_f):
+                    t.load_prompt(hist)
+                ents.append(mlxlm_entries(ring_r, ring_p, ring_f))
+            else:
+                st = Cbv2RowState(prompt=hist[:20], output=hist[20:], repetition_window=32,
+                                  repetition_on=True, counts_on=True, bias={}, vocab=V)
+                ents.append(st.entries())
+        for pkw in (dict(temperature=0.9, top_p=0.9, min_p=0.02), dict(temperature=1.2, top_p=0.97)):
+            if sem == _ffi.SEM_MLXLM:
+                p = W.resolve_mlxlm(repetition_penalty=1.2, presence_penalty=0.3,
+                                    frequency_penalty=0.1, **pkw)
+            else:
+                p = W.resolve_cbv2(vocab=V, repetition_penalty=1.2, repetition_context_size=32,
+                                   presence_penalty=0.3, frequency_penalty=0.1, **pkw)
+            cfg = small_cfg(sem, xin, [p] * R, us, dtype=dtype, entries=ents)
+            compare(cfg, run_gpu(ctx, cfg), run_oracle(cfg), label=f"-inf rows {sem} {pkw}")
+
+
 def test_penalties_both_semantics(ctx):
     rng = np.random.default_rng(11)
     V = 1000
