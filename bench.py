@@ -422,7 +422,7 @@ def bench_step_fused(args):
     from lsamp.api import Context
 
     n = int(args.step_config[1])
-    cfg = W.CONFIGS[n]()
+    cfg = W.WORKLOADS[n]()
     B, V = cfg["rows"], cfg["vocab"]
     R = args.copies if n != 3 else min(args.copies, 4)
     steps, warm = args.steps, args.warmup
@@ -626,7 +626,7 @@ def bench_config(args, n):
     from lsamp import _ffi, workloads as W
     from lsamp.api import Context
 
-    cfg = W.CONFIGS[n]()
+    cfg = W.WORKLOADS[n]()
     B, V = cfg["rows"], cfg["vocab"]
     R = args.copies if n != 3 else min(args.copies, 4)  # c3 copies are 134 MB each
     dev = torch.device("cuda", 0)

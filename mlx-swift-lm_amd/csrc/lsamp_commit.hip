@@ -57,7 +57,7 @@ __device__ __forceinline__ Found take_from(int src, int32_t idx, const lsamp_pen
 __global__ __launch_bounds__(64) void k_commit(lsamp_commit_args a) {
   const lsamp_penalty_table& T = a.table;
   const int r = blockIdx.x, lane = threadIdx.x;
-  // round 1: the row's bookkeeping and its whole window row, all independent
+  // first memory round trip: the row's bookkeeping and its whole window row, all independent
   const int32_t t = a.tokens[r];
   const uint32_t mode = T.mode[r];
   const int32_t len0 = T.row_len[r];
@@ -79,7 +79,7 @@ __global__ __launch_bounds__(64) void k_commit(lsamp_commit_args a) {
   // the token this write evicts (slot pos of the ring)
   const int32_t ev = !rep ? -1 : pos < 64 ? read_lane(wlane, pos) : win[pos];
 
-  // round 2: the row's entries and window counts, in registers
+  // second memory round trip: the row's entries and window counts, in registers
   lsamp_penalty_entry e[kCommitRegs];
   int32_t wc[kCommitRegs];
 #pragma unroll

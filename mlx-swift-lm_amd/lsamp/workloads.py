@@ -260,7 +260,7 @@ def config5(sequences: int = 32, window: int = 4, vocab: int = V_QWEN) -> dict:
                 workload=f"MTP verify S={sequences} W={window} V={vocab} bf16 T0.8 top-p0.95")
 
 
-CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
+WORKLOADS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
 
 
 def algorithmic_bytes(cfg: dict) -> int:

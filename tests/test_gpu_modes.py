@@ -52,7 +52,7 @@ def _assert_same(a, b, label):
 
 @pytest.mark.parametrize("n", [1, 2, 3, 4])
 def test_fused_equals_split_full_configs(ctx, n):
-    cfg = W.CONFIGS[n]()
+    cfg = W.WORKLOADS[n]()
     f, s = _both_modes(ctx, cfg)
     _assert_same(f, s, f"config{n}")
 

@@ -31,7 +31,7 @@ def _keys(rows, seed, step):
 
 @pytest.mark.parametrize("n,kw", [(2, {}), (3, {"rows": 32}), (4, {"rows": 16})])
 def test_keyed_draw_matches_the_oracle(ctx, n, kw):
-    cfg = W.CONFIGS[n](**kw)
+    cfg = W.WORKLOADS[n](**kw)
     for step in (0, 1, 57):
         keys = _keys(cfg["rows"], seed=20240501 + n, step=step)
         u = np.array([O.rng_uniform(int(k), 0) for k in keys], np.float32)

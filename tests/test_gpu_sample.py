@@ -262,7 +262,7 @@ def test_configs_reduced(ctx, n):
     if n == 4:
         cfg = W.config4(rows=8)
     else:
-        cfg = W.CONFIGS[n](**kw[n])
+        cfg = W.WORKLOADS[n](**kw[n])
     g = run_gpu(ctx, cfg)
     o = run_oracle(cfg)
     compare(cfg, g, o, label=f"config{n} reduced")
@@ -270,7 +270,7 @@ def test_configs_reduced(ctx, n):
 
 @pytest.mark.parametrize("n", [1, 2, 3, 4])
 def test_configs_full(ctx, n):
-    cfg = W.CONFIGS[n]()
+    cfg = W.WORKLOADS[n]()
     g = run_gpu(ctx, cfg)
     o = run_oracle(cfg, threads=16)
     boundary = compare(cfg, g, o, label=f"config{n}")
